@@ -1,0 +1,958 @@
+// Host side of the C ABI declared in include/ferro_gpu.h: weight upload and
+// repacking, the paged KV cache, the forward pass and the on-device greedy
+// speculative step. Each entry point names the reference interface it
+// replaces in the header.
+#include "ferro_gpu.h"
+#include "internal.h"
+
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+#include <string>
+#include <thread>
+#include <vector>
+
+using namespace fg;
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(int code, const std::string& msg) {
+    g_err = msg;
+    return code;
+}
+
+#define HIPCHK(x)                                                                                   \
+    do {                                                                                            \
+        hipError_t e_ = (x);                                                                        \
+        if (e_ != hipSuccess) return fail(FG_E_DEVICE, std::string(#x) + ": " + hipGetErrorString(e_)); \
+    } while (0)
+
+constexpr int ATT_QMAX = 64;   // queries per attention work item (k_attn)
+constexpr int SPLIT_POS = 128; // context positions per attention work item
+
+template <class F>
+void parallel_for(int n, F f) {
+    int nt = (int)std::thread::hardware_concurrency();
+    nt = std::max(1, std::min(nt, 16));
+    nt = std::min(nt, std::max(1, n));
+    if (nt == 1) {
+        for (int i = 0; i < n; i++) f(i);
+        return;
+    }
+    std::vector<std::thread> th;
+    for (int t = 0; t < nt; t++)
+        th.emplace_back([=, &f] {
+            for (int i = t; i < n; i += nt) f(i);
+        });
+    for (auto& x : th) x.join();
+}
+
+int round_up(int a, int b) { return (a + b - 1) / b * b; }
+
+// Carves aligned sub-buffers out of one allocation; with base == nullptr it
+// only measures.
+struct Carver {
+    char* base;
+    size_t off = 0;
+    explicit Carver(void* b) : base((char*)b) {}
+    template <class T>
+    T* take(size_t n) {
+        off = (off + 255) & ~(size_t)255;
+        T* p = base ? (T*)(base + off) : nullptr;
+        off += n * sizeof(T);
+        return p;
+    }
+};
+
+}  // namespace
+
+// ---------------------------------------------------------------------------
+// Handles
+// ---------------------------------------------------------------------------
+struct fg_ctx {
+    int device = 0;
+    hipStream_t stream = nullptr;
+    void* ws = nullptr;
+    size_t ws_cap = 0;
+    void* dmeta = nullptr;
+    size_t dmeta_cap = 0;
+    void* hmeta = nullptr;
+    size_t hmeta_cap = 0;
+    hipEvent_t ev[3] = {nullptr, nullptr, nullptr};
+    float last_us[3] = {0, 0, 0};
+};
+
+struct DLayer {
+    float* attn_norm = nullptr;
+    DMat wqkv;
+    float* bqkv = nullptr;
+    DMat wo;
+    float* mlp_norm = nullptr;
+    DMat w_gate_up;
+    DMat w_down;
+};
+
+struct fg_model {
+    fg_config cfg{};
+    std::vector<DLayer> layers;
+    uint16_t* embed = nullptr;
+    DMat lm_head;
+    float* norm = nullptr;
+    float* cos_t = nullptr;
+    float* sin_t = nullptr;
+    int max_pos = 0;
+    bool owns = true;
+    std::vector<void*> allocs;
+    int64_t ref_bytes = 0;
+};
+
+struct fg_kv {
+    int layers = 0, kv_heads = 0, head_dim = 0, block_size = 0, blocks = 0;
+    float* k = nullptr;  // [layer][blocks*bs*nkv*hd]
+    float* v = nullptr;
+    size_t layer_floats() const { return (size_t)blocks * block_size * kv_heads * head_dim; }
+};
+
+struct fg_mat {
+    DMat m;
+    int device = 0;
+};
+
+static int ensure(void** p, size_t* cap, size_t need, hipStream_t st, bool host) {
+    if (need <= *cap && *p) return 0;
+    if (st) HIPCHK(hipStreamSynchronize(st));
+    size_t n = std::max(need + need / 4, (size_t)1 << 20);
+    if (*p) {
+        if (host)
+            HIPCHK(hipHostFree(*p));
+        else
+            HIPCHK(hipFree(*p));
+        *p = nullptr;
+        *cap = 0;
+    }
+    if (host) {
+        if (hipHostMalloc(p, n, hipHostMallocDefault) != hipSuccess) return fail(FG_E_NOMEM, "pinned host allocation failed");
+    } else {
+        if (hipMalloc(p, n) != hipSuccess) return fail(FG_E_NOMEM, "device allocation failed");
+    }
+    *cap = n;
+    return 0;
+}
+
+// ---------------------------------------------------------------------------
+// Repacking from the reference's formats to the device layout (internal.h).
+// ---------------------------------------------------------------------------
+static inline int qcode(const uint8_t* q, int kind, int K, int r, int k) {
+    const int p = r / 32, c = r % 32;
+    if (kind == INT8) return (int8_t)q[((size_t)p * K + k) * 32 + c];
+    const uint8_t b = q[((size_t)p * K + k) * 16 + (c % 16)];
+    return (c < 16 ? (b & 15) : (b >> 4)) - 8;
+}
+
+static int repack(const fg_matrix& src, DMat& d, std::vector<uint8_t>& w, std::vector<float>& s) {
+    if (src.rows <= 0 || src.cols <= 0 || src.rows % 32 || (src.format != FG_BF16 && src.cols % 32))
+        return fail(FG_E_SHAPE, "matrix rows must be a multiple of 32 (and cols of 32 when quantized)");
+    if (src.format == FG_BF16 && !src.bf16) return fail(FG_E_ARG, "bf16 matrix without data");
+    if (src.format != FG_BF16 && (!src.q || !src.s)) return fail(FG_E_ARG, "quantized matrix without codes/scales");
+    if (src.format < 0 || src.format > 2) return fail(FG_E_ARG, "unknown matrix format");
+    const int N = src.rows, K = src.cols;
+    d.kind = src.format;
+    d.rows = N;
+    d.cols = K;
+    d.n_tiles = N / 16;
+    d.kb = round_up((K + 31) / 32, 4);
+    const int KB = d.kb, KC = KB / 4;
+    if (d.kind == BF16) {
+        d.ref_bytes = (int64_t)N * K * 2;
+        w.assign((size_t)d.n_tiles * KB * 64 * 16, 0);
+        uint16_t* out = (uint16_t*)w.data();
+        parallel_for(d.n_tiles, [&](int t) {
+            for (int kb = 0; kb < KB; kb++)
+                for (int l = 0; l < 64; l++) {
+                    const int n = t * 16 + l % 16, k0 = kb * 32 + 8 * (l / 16);
+                    uint16_t* o = out + (((size_t)t * KB + kb) * 64 + l) * 8;
+                    for (int sl = 0; sl < 8; sl++) o[sl] = k0 + sl < K ? src.bf16[(size_t)n * K + k0 + sl] : 0;
+                }
+        });
+        s.clear();
+        return 0;
+    }
+    const int G = K / 32;
+    const bool q4 = d.kind == INT4;
+    d.ref_bytes = (int64_t)N * K / (q4 ? 2 : 1) + (int64_t)N * G * 4;
+    s.assign((size_t)d.n_tiles * KC * 16 * 4, 0.0f);
+    parallel_for(d.n_tiles, [&](int t) {
+        for (int kb = 0; kb < G; kb++)
+            for (int r = 0; r < 16; r++) {
+                const int n = t * 16 + r, p = n / 32, c = n % 32;
+                float v = src.s[((size_t)p * G + kb) * 32 + c];
+                if (q4) v *= 0.0625f;
+                s[(((size_t)t * KC + kb / 4) * 16 + r) * 4 + kb % 4] = v;
+            }
+    });
+    if (q4) {
+        w.assign((size_t)d.n_tiles * KC * 64 * 16, 0);
+        uint32_t* out = (uint32_t*)w.data();
+        parallel_for(d.n_tiles, [&](int t) {
+            for (int kb = 0; kb < G; kb++)
+                for (int l = 0; l < 64; l++) {
+                    const int n = t * 16 + l % 16, k0 = kb * 32 + 8 * (l / 16);
+                    uint32_t word = 0;
+                    for (int sl = 0; sl < 8; sl++) {
+                        const int code = qcode(src.q, INT4, K, n, k0 + sl);
+                        const int ni = sl < 4 ? 2 * sl : 2 * (sl - 4) + 1;
+                        word |= (uint32_t)(code & 15) << (4 * ni);
+                    }
+                    out[(((size_t)t * KC + kb / 4) * 64 + l) * 4 + kb % 4] = word;
+                }
+        });
+    } else {
+        w.assign((size_t)d.n_tiles * (KB / 2) * 64 * 16, 0);
+        int8_t* out = (int8_t*)w.data();
+        parallel_for(d.n_tiles, [&](int t) {
+            for (int kb = 0; kb < G; kb++)
+                for (int l = 0; l < 64; l++) {
+                    const int n = t * 16 + l % 16, k0 = kb * 32 + 8 * (l / 16);
+                    int8_t* o = out + (((size_t)t * (KB / 2) + kb / 2) * 64 + l) * 16 + (kb % 2) * 8;
+                    for (int sl = 0; sl < 8; sl++) o[sl] = (int8_t)qcode(src.q, INT8, K, n, k0 + sl);
+                }
+        });
+    }
+    return 0;
+}
+
+static int upload_mat(const fg_matrix& src, DMat& d, std::vector<void*>* allocs) {
+    std::vector<uint8_t> w;
+    std::vector<float> s;
+    int rc = repack(src, d, w, s);
+    if (rc) return rc;
+    d.w_bytes = w.size();
+    d.s_bytes = s.size() * 4;
+    if (hipMalloc(&d.w, d.w_bytes) != hipSuccess) return fail(FG_E_NOMEM, "weight allocation failed");
+    if (allocs) allocs->push_back(d.w);
+    HIPCHK(hipMemcpy(d.w, w.data(), d.w_bytes, hipMemcpyHostToDevice));
+    if (d.s_bytes) {
+        if (hipMalloc((void**)&d.s, d.s_bytes) != hipSuccess) return fail(FG_E_NOMEM, "scale allocation failed");
+        if (allocs) allocs->push_back(d.s);
+        HIPCHK(hipMemcpy(d.s, s.data(), d.s_bytes, hipMemcpyHostToDevice));
+    }
+    return 0;
+}
+
+template <class T>
+static int upload_vec(const T* src, size_t n, T** dst, std::vector<void*>& allocs) {
+    if (hipMalloc((void**)dst, n * sizeof(T)) != hipSuccess) return fail(FG_E_NOMEM, "allocation failed");
+    allocs.push_back(*dst);
+    HIPCHK(hipMemcpy(*dst, src, n * sizeof(T), hipMemcpyHostToDevice));
+    return 0;
+}
+
+// inv_freq and the cos/sin tables, in f32 with the C library's powf, cosf
+// and sinf (src/model.rs:434-448, 461-492).
+static void rope_tables(const fg_config& c, int max_pos, std::vector<float>& cs, std::vector<float>& sn) {
+    const int dim = c.head_dim, half = dim / 2;
+    std::vector<float> f(half);
+    for (int i = 0; i < half; i++) f[i] = 1.0f / powf(c.rope_theta, (float)(2 * i) / (float)dim);
+    if (c.rope_llama3) {
+        const float old = (float)c.rope_orig_max_pos;
+        const float low_wavelen = old / c.rope_low_freq, high_wavelen = old / c.rope_high_freq;
+        for (int i = 0; i < half; i++) {
+            const float fr = f[i];
+            const float wavelen = 2.0f * 3.14159265358979323846f / fr;
+            if (wavelen < high_wavelen) {
+                f[i] = fr;
+            } else if (wavelen > low_wavelen) {
+                f[i] = fr / c.rope_factor;
+            } else {
+                const float smooth = (old / wavelen - c.rope_low_freq) / (c.rope_high_freq - c.rope_low_freq);
+                const float a = (1.0f - smooth) * fr;
+                const float b = smooth * fr;
+                f[i] = a / c.rope_factor + b;
+            }
+        }
+    }
+    cs.resize((size_t)max_pos * half);
+    sn.resize((size_t)max_pos * half);
+    parallel_for(max_pos, [&](int p) {
+        for (int i = 0; i < half; i++) {
+            volatile float a = (float)p * f[i];
+            cs[(size_t)p * half + i] = cosf(a);
+            sn[(size_t)p * half + i] = sinf(a);
+        }
+    });
+}
+
+// ---------------------------------------------------------------------------
+// Forward plan: row bookkeeping (src/model.rs:278-294), attention work items
+// and the logits rows (src/model.rs:338-350), packed into one int32 upload.
+// ---------------------------------------------------------------------------
+struct ChunkIn {
+    const uint32_t* tokens;  // host tokens, or nullptr when they come from device
+    int n, pos;
+    const uint32_t* blocks;
+    int n_blocks, logits;
+};
+
+struct Plan {
+    int t = 0, S = 0, G = 0, W = 0, T = 0;
+    std::vector<int32_t> pos, slot, row_group, g_row0, g_nrows, g_table, g_wi0, g_nsplit, wi_group, wi_split, sel;
+    std::vector<uint32_t> tables, tokens;
+    bool host_tokens = true;
+    // offsets (in int32 words) of each array inside the packed metadata
+    size_t o_pos, o_slot, o_rg, o_grow0, o_gnrows, o_gtable, o_gwi0, o_gnsplit, o_wig, o_wis, o_tables, o_sel, o_tok,
+        words;
+};
+
+static int build_plan(const fg_config& c, const fg_kv& kv, int max_pos, const ChunkIn* ch, int nch, Plan& P) {
+    const int bs = kv.block_size;
+    const int group = c.heads / c.kv_heads;
+    const int rg = std::max(1, std::min(16, ATT_QMAX / group));
+    P = Plan();
+    for (int ci = 0; ci < nch; ci++) {
+        const ChunkIn& k = ch[ci];
+        if (k.n < 0 || k.pos < 0) return fail(FG_E_ARG, "negative chunk length or position");
+        if (k.n == 0) continue;
+        if ((int64_t)k.n_blocks * bs < (int64_t)k.pos + k.n)
+            return fail(FG_E_SHAPE, "chunk overruns its cache blocks");
+        if (k.pos + k.n > max_pos) return fail(FG_E_SHAPE, "position beyond max_position");
+        if (!k.blocks) return fail(FG_E_ARG, "chunk without a block table");
+        const int used = (k.pos + k.n + bs - 1) / bs;
+        const int toff = (int)P.tables.size();
+        for (int b = 0; b < used; b++) {
+            if (k.blocks[b] >= (uint32_t)kv.blocks) return fail(FG_E_ARG, "block id beyond the cache");
+            P.tables.push_back(k.blocks[b]);
+        }
+        const int row_base = P.t;
+        for (int i = 0; i < k.n; i++) {
+            const int p = k.pos + i;
+            P.pos.push_back(p);
+            P.slot.push_back((int32_t)(k.blocks[p / bs] * (uint32_t)bs + p % bs));
+            if (k.tokens) {
+                if (k.tokens[i] >= (uint32_t)c.vocab) return fail(FG_E_ARG, "token outside the vocabulary");
+                P.tokens.push_back(k.tokens[i]);
+            } else {
+                P.tokens.push_back(0);
+            }
+        }
+        for (int r0 = 0; r0 < k.n; r0 += rg) {
+            const int nr = std::min(rg, k.n - r0);
+            const int gi = (int)P.g_row0.size();
+            P.g_row0.push_back(row_base + r0);
+            P.g_nrows.push_back(nr);
+            P.g_table.push_back(toff);
+            P.g_wi0.push_back((int)P.wi_group.size());
+            const int L = k.pos + r0 + nr;
+            const int ns = (L + SPLIT_POS - 1) / SPLIT_POS;
+            P.g_nsplit.push_back(ns);
+            for (int s = 0; s < ns; s++) {
+                P.wi_group.push_back(gi);
+                P.wi_split.push_back(s);
+            }
+            for (int i = 0; i < nr; i++) P.row_group.push_back(gi);
+        }
+        if (k.logits == FG_LOGITS_LAST) P.sel.push_back(row_base + k.n - 1);
+        if (k.logits == FG_LOGITS_ALL)
+            for (int i = 0; i < k.n; i++) P.sel.push_back(row_base + i);
+        P.t += k.n;
+    }
+    P.S = (int)P.sel.size();
+    P.G = (int)P.g_row0.size();
+    P.W = (int)P.wi_group.size();
+    P.T = (int)P.tables.size();
+    size_t o = 0;
+    auto place = [&](size_t n) {
+        size_t r = o;
+        o += (n + 63) / 64 * 64;
+        return r;
+    };
+    P.o_pos = place(P.t);
+    P.o_slot = place(P.t);
+    P.o_rg = place(P.t);
+    P.o_grow0 = place(P.G);
+    P.o_gnrows = place(P.G);
+    P.o_gtable = place(P.G);
+    P.o_gwi0 = place(P.G);
+    P.o_gnsplit = place(P.G);
+    P.o_wig = place(P.W);
+    P.o_wis = place(P.W);
+    P.o_tables = place(P.T);
+    P.o_sel = place(P.S);
+    P.o_tok = place(P.t);
+    P.words = o;
+    return 0;
+}
+
+static void pack_plan(const Plan& P, int32_t* h) {
+    auto cp = [&](size_t off, const std::vector<int32_t>& v) {
+        if (!v.empty()) memcpy(h + off, v.data(), v.size() * 4);
+    };
+    cp(P.o_pos, P.pos);
+    cp(P.o_slot, P.slot);
+    cp(P.o_rg, P.row_group);
+    cp(P.o_grow0, P.g_row0);
+    cp(P.o_gnrows, P.g_nrows);
+    cp(P.o_gtable, P.g_table);
+    cp(P.o_gwi0, P.g_wi0);
+    cp(P.o_gnsplit, P.g_nsplit);
+    cp(P.o_wig, P.wi_group);
+    cp(P.o_wis, P.wi_split);
+    if (!P.tables.empty()) memcpy(h + P.o_tables, P.tables.data(), P.tables.size() * 4);
+    cp(P.o_sel, P.sel);
+    if (!P.tokens.empty()) memcpy(h + P.o_tok, P.tokens.data(), P.tokens.size() * 4);
+}
+
+// Workspace of one forward pass over a plan.
+struct Work {
+    float *x, *rinv, *part, *q, *att, *apart, *hsel, *rsel, *lpart, *logits;
+    void* pa;
+    float* pxs;
+    float2* best;
+    uint32_t* am;
+    int kb_max, passes, splits_max, nblk, lm_splits;
+    size_t part_floats;
+};
+
+static int kind_of(const DMat& m) { return m.kind; }
+
+static size_t layout_work(const fg_model* m, const Plan& P, Work& w, void* base) {
+    const fg_config& c = m->cfg;
+    const int t = P.t, H = c.hidden, qd = c.heads * c.head_dim, I = c.intermediate;
+    Carver cv(base);
+    w.kb_max = 0;
+    w.splits_max = 1;
+    size_t pf = 0;
+    for (const DLayer& l : m->layers)
+        for (const DMat* d : {&l.wqkv, &l.wo, &l.w_gate_up, &l.w_down}) {
+            w.kb_max = std::max(w.kb_max, d->kb);
+            const GemvPlan gp = plan_gemv(*d, t);
+            w.splits_max = std::max(w.splits_max, gp.splits);
+            pf = std::max(pf, (size_t)gp.splits * t * d->rows);
+        }
+    w.kb_max = std::max(w.kb_max, m->lm_head.kb);
+    w.passes = std::max((t + 3) / 4, (P.S + 3) / 4);
+    w.part_floats = pf;
+    const GemvPlan lp = plan_gemv(m->lm_head, std::max(P.S, 1));
+    w.lm_splits = lp.splits;
+    w.nblk = std::max(1, std::min(64, (c.vocab + 4095) / 4096));
+    w.x = cv.take<float>((size_t)t * H);
+    w.rinv = cv.take<float>(t);
+    w.pa = cv.take<uint8_t>((size_t)w.kb_max * w.passes * 64 * 16);
+    w.pxs = cv.take<float>((size_t)w.kb_max * w.passes * 4);
+    w.part = cv.take<float>(pf);
+    w.q = cv.take<float>((size_t)t * qd);
+    w.att = cv.take<float>((size_t)t * qd);
+    w.apart = cv.take<float>((size_t)std::max(P.W, 1) * c.kv_heads * ATT_QMAX * (c.head_dim + 2));
+    w.hsel = cv.take<float>((size_t)std::max(P.S, 1) * H);
+    w.rsel = cv.take<float>(std::max(P.S, 1));
+    w.lpart = cv.take<float>((size_t)lp.splits * std::max(P.S, 1) * c.vocab);
+    w.logits = cv.take<float>((size_t)std::max(P.S, 1) * c.vocab);
+    w.best = cv.take<float2>((size_t)std::max(P.S, 1) * w.nblk);
+    w.am = cv.take<uint32_t>(std::max(P.S, 1));
+    (void)I;
+    return cv.off + 256;
+}
+
+static Pieces pieces_for(const Work& w, int kb, int passes) {
+    Pieces p;
+    p.a = w.pa;
+    p.xs = w.pxs;
+    p.kb = kb;
+    p.passes = passes;
+    return p;
+}
+
+// Runs one forward pass. `meta` is the device copy of the plan's packed
+// metadata; tokens come from tok_dev with stride tok_stride. Outputs:
+// logits rows to logits_dev (may be null), argmax to am_out (or the
+// workspace), optional aux copy of the argmax (for chaining draft rounds),
+// and the hidden-state taps to host.
+static int run_forward(fg_ctx* ctx, const fg_model* m, fg_kv* kv, const Plan& P, const int32_t* meta,
+                       const uint32_t* tok_dev, int tok_stride, Work& w, float* logits_dev, uint32_t* am_out,
+                       uint32_t* aux, int aux_stride, int aux_off, float* hidden_host) {
+    const fg_config& c = m->cfg;
+    hipStream_t st = ctx->stream;
+    const int t = P.t, H = c.hidden, hd = c.head_dim, nh = c.heads, nkv = c.kv_heads, I = c.intermediate;
+    const int qd = nh * hd;
+    const int passes = (t + 3) / 4;
+    if (t == 0) return 0;
+    const int32_t* d_pos = meta + P.o_pos;
+    const int32_t* d_slot = meta + P.o_slot;
+
+    launch_embed(st, tok_dev, tok_stride, m->embed, t, H, w.x);
+    if (hidden_host)
+        HIPCHK(hipMemcpyAsync(hidden_host, w.x, (size_t)t * H * 4, hipMemcpyDeviceToHost, st));
+    launch_residual_rms(st, w.x, nullptr, 1, t, H, c.rms_eps, w.rinv);
+
+    AttnArgs aa{};
+    aa.q = w.q;
+    aa.row_pos = d_pos;
+    aa.wi_group = meta + P.o_wig;
+    aa.wi_split = meta + P.o_wis;
+    aa.g_row0 = meta + P.o_grow0;
+    aa.g_nrows = meta + P.o_gnrows;
+    aa.g_table = meta + P.o_gtable;
+    aa.g_wi0 = meta + P.o_gwi0;
+    aa.g_nsplit = meta + P.o_gnsplit;
+    aa.tables = (const uint32_t*)(meta + P.o_tables);
+    aa.part = w.apart;
+    aa.out = w.att;
+    aa.row_group = meta + P.o_rg;
+    aa.n_wi = P.W;
+    aa.nh = nh;
+    aa.nkv = nkv;
+    aa.hd = hd;
+    aa.bs = kv->block_size;
+    aa.split_pos = SPLIT_POS;
+    aa.qmax = ATT_QMAX;
+    aa.scale = 1.0f / sqrtf((float)hd);
+
+    for (size_t li = 0; li < m->layers.size(); li++) {
+        const DLayer& l = m->layers[li];
+        float* kc = kv->k + li * kv->layer_floats();
+        float* vc = kv->v + li * kv->layer_floats();
+        // attention block
+        Pieces pa = pieces_for(w, l.wqkv.kb, passes);
+        launch_pieces(st, kind_of(l.wqkv), w.x, H, t, H, l.attn_norm, w.rinv, pa);
+        GemvPlan gp = plan_gemv(l.wqkv, t);
+        launch_gemv(st, l.wqkv, pa, t, gp, w.part);
+        launch_rope_kv(st, w.part, gp.splits, t, l.bqkv, d_pos, d_slot, m->cos_t, m->sin_t, nh, nkv, hd,
+                       kv->block_size, w.q, kc, vc);
+        aa.kc = kc;
+        aa.vc = vc;
+        launch_attention(st, aa, t);
+        Pieces po = pieces_for(w, l.wo.kb, passes);
+        launch_pieces(st, kind_of(l.wo), w.att, qd, t, qd, nullptr, nullptr, po);
+        gp = plan_gemv(l.wo, t);
+        launch_gemv(st, l.wo, po, t, gp, w.part);
+        launch_residual_rms(st, w.x, w.part, gp.splits, t, H, c.rms_eps, w.rinv);
+        // MLP block
+        Pieces pg = pieces_for(w, l.w_gate_up.kb, passes);
+        launch_pieces(st, kind_of(l.w_gate_up), w.x, H, t, H, l.mlp_norm, w.rinv, pg);
+        gp = plan_gemv(l.w_gate_up, t);
+        launch_gemv(st, l.w_gate_up, pg, t, gp, w.part);
+        Pieces pd = pieces_for(w, l.w_down.kb, passes);
+        launch_silu_pieces(st, w.part, gp.splits, t, I, pd, nullptr, kind_of(l.w_down));
+        gp = plan_gemv(l.w_down, t);
+        launch_gemv(st, l.w_down, pd, t, gp, w.part);
+        launch_residual_rms(st, w.x, w.part, gp.splits, t, H, c.rms_eps, w.rinv);
+        if (hidden_host)
+            HIPCHK(hipMemcpyAsync(hidden_host + (li + 1) * (size_t)t * H, w.x, (size_t)t * H * 4,
+                                  hipMemcpyDeviceToHost, st));
+    }
+    HIPCHK(hipGetLastError());
+    if (P.S == 0) return 0;
+    // final norm on the selected rows, lm_head, argmax
+    launch_gather_rows(st, w.x, meta + P.o_sel, P.S, H, w.hsel);
+    launch_residual_rms(st, w.hsel, nullptr, 1, P.S, H, c.rms_eps, w.rsel);
+    const int sp = (P.S + 3) / 4;
+    Pieces pl = pieces_for(w, m->lm_head.kb, sp);
+    launch_pieces(st, kind_of(m->lm_head), w.hsel, H, P.S, H, m->norm, w.rsel, pl);
+    const GemvPlan lp = plan_gemv(m->lm_head, P.S);
+    launch_gemv(st, m->lm_head, pl, P.S, lp, w.lpart);
+    launch_argmax(st, w.lpart, lp.splits, P.S, c.vocab, logits_dev, w.best, w.nblk, am_out ? am_out : w.am, aux,
+                  aux_stride, aux_off);
+    HIPCHK(hipGetLastError());
+    return 0;
+}
+
+// ---------------------------------------------------------------------------
+// C ABI
+// ---------------------------------------------------------------------------
+extern "C" {
+
+const char* fg_last_error(void) { return g_err.c_str(); }
+
+int fg_ctx_create(int device, fg_ctx** out) {
+    if (!out) return fail(FG_E_ARG, "null out");
+    int n = 0;
+    HIPCHK(hipGetDeviceCount(&n));
+    if (device < 0 || device >= n) return fail(FG_E_ARG, "no such device");
+    HIPCHK(hipSetDevice(device));
+    fg_ctx* c = new fg_ctx();
+    c->device = device;
+    if (hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking) != hipSuccess) {
+        delete c;
+        return fail(FG_E_DEVICE, "stream creation failed");
+    }
+    for (auto& e : c->ev) HIPCHK(hipEventCreate(&e));
+    *out = c;
+    return 0;
+}
+
+void fg_ctx_destroy(fg_ctx* c) {
+    if (!c) return;
+    (void)hipSetDevice(c->device);
+    (void)hipStreamSynchronize(c->stream);
+    if (c->ws) (void)hipFree(c->ws);
+    if (c->dmeta) (void)hipFree(c->dmeta);
+    if (c->hmeta) (void)hipHostFree(c->hmeta);
+    for (auto& e : c->ev)
+        if (e) (void)hipEventDestroy(e);
+    (void)hipStreamDestroy(c->stream);
+    delete c;
+}
+
+int fg_ctx_sync(fg_ctx* c) {
+    if (!c) return fail(FG_E_ARG, "null ctx");
+    HIPCHK(hipStreamSynchronize(c->stream));
+    return 0;
+}
+
+int fg_model_upload(fg_ctx* ctx, const fg_config* cfg, const fg_layer* layers, const uint16_t* embed,
+                    const float* norm, const uint16_t* lm_head, fg_model** out) {
+    if (!ctx || !cfg || (!layers && cfg->layers > 0) || !embed || !norm || !out) return fail(FG_E_ARG, "null argument");
+    const fg_config& c = *cfg;
+    if (c.heads <= 0 || c.kv_heads <= 0 || c.heads % c.kv_heads || c.head_dim % 16 || c.hidden % 16 ||
+        c.head_dim > 128 || c.vocab <= 0 || c.layers < 0 || c.max_position <= 0)
+        return fail(FG_E_SHAPE, "unsupported model shape");
+    if (c.heads / c.kv_heads > ATT_QMAX) return fail(FG_E_SHAPE, "GQA group too large");
+    HIPCHK(hipSetDevice(ctx->device));
+    fg_model* m = new fg_model();
+    m->cfg = c;
+    const int H = c.hidden, qkv = (c.heads + 2 * c.kv_heads) * c.head_dim;
+    auto bad = [&](int rc) {
+        fg_model_destroy(m);
+        return rc;
+    };
+    m->layers.resize(c.layers);
+    int64_t ref = 0;
+    for (int i = 0; i < c.layers; i++) {
+        const fg_layer& s = layers[i];
+        DLayer& d = m->layers[i];
+        if (!s.attn_norm || !s.mlp_norm || (c.qkv_bias && !s.bqkv)) return bad(fail(FG_E_ARG, "layer missing a vector"));
+        if (s.wqkv.rows != qkv || s.wqkv.cols != H || s.wo.rows != H || s.wo.cols != c.heads * c.head_dim ||
+            s.w_gate_up.rows != 2 * c.intermediate || s.w_gate_up.cols != H || s.w_down.rows != H ||
+            s.w_down.cols != c.intermediate)
+            return bad(fail(FG_E_SHAPE, "weight shapes do not match the config"));  // src/model.rs:243-261
+        int rc;
+        if ((rc = upload_vec(s.attn_norm, H, &d.attn_norm, m->allocs))) return bad(rc);
+        if ((rc = upload_vec(s.mlp_norm, H, &d.mlp_norm, m->allocs))) return bad(rc);
+        if (c.qkv_bias && (rc = upload_vec(s.bqkv, qkv, &d.bqkv, m->allocs))) return bad(rc);
+        if ((rc = upload_mat(s.wqkv, d.wqkv, &m->allocs))) return bad(rc);
+        if ((rc = upload_mat(s.wo, d.wo, &m->allocs))) return bad(rc);
+        if ((rc = upload_mat(s.w_gate_up, d.w_gate_up, &m->allocs))) return bad(rc);
+        if ((rc = upload_mat(s.w_down, d.w_down, &m->allocs))) return bad(rc);
+        ref += d.wqkv.ref_bytes + d.wo.ref_bytes + d.w_gate_up.ref_bytes + d.w_down.ref_bytes;
+    }
+    int rc;
+    if ((rc = upload_vec(embed, (size_t)c.vocab * H, &m->embed, m->allocs))) return bad(rc);
+    fg_matrix lm{FG_BF16, c.vocab, H, 0, (lm_head && !c.tie_embeddings) ? lm_head : embed, nullptr, nullptr};
+    if (c.vocab % 32) return bad(fail(FG_E_SHAPE, "vocab must be a multiple of 32"));
+    if ((rc = upload_mat(lm, m->lm_head, &m->allocs))) return bad(rc);
+    ref += (int64_t)c.vocab * H * 2 * ((lm_head && !c.tie_embeddings) ? 2 : 1);
+    if ((rc = upload_vec(norm, H, &m->norm, m->allocs))) return bad(rc);
+    m->max_pos = c.max_position;
+    std::vector<float> cs, sn;
+    rope_tables(c, m->max_pos, cs, sn);
+    if ((rc = upload_vec(cs.data(), cs.size(), &m->cos_t, m->allocs))) return bad(rc);
+    if ((rc = upload_vec(sn.data(), sn.size(), &m->sin_t, m->allocs))) return bad(rc);
+    m->ref_bytes = ref;
+    *out = m;
+    return 0;
+}
+
+int fg_model_truncated(fg_ctx* ctx, const fg_model* base, int32_t layers, fg_model** out) {
+    if (!ctx || !base || !out || layers < 0) return fail(FG_E_ARG, "bad argument");
+    fg_model* m = new fg_model();
+    m->cfg = base->cfg;
+    m->layers.assign(base->layers.begin(), base->layers.begin() + std::min<size_t>(layers, base->layers.size()));
+    m->cfg.layers = (int)m->layers.size();
+    m->embed = base->embed;
+    m->lm_head = base->lm_head;
+    m->norm = base->norm;
+    m->cos_t = base->cos_t;
+    m->sin_t = base->sin_t;
+    m->max_pos = base->max_pos;
+    m->owns = false;
+    int64_t ref = (int64_t)m->cfg.vocab * m->cfg.hidden * 2;
+    for (const DLayer& d : m->layers) ref += d.wqkv.ref_bytes + d.wo.ref_bytes + d.w_gate_up.ref_bytes + d.w_down.ref_bytes;
+    m->ref_bytes = ref;
+    *out = m;
+    return 0;
+}
+
+void fg_model_destroy(fg_model* m) {
+    if (!m) return;
+    if (m->owns)
+        for (void* p : m->allocs) (void)hipFree(p);
+    delete m;
+}
+
+int64_t fg_model_weight_bytes(const fg_model* m) { return m ? m->ref_bytes : 0; }
+
+int fg_kv_create(fg_ctx* ctx, int32_t layers, int32_t kv_heads, int32_t head_dim, int32_t block_size, int32_t blocks,
+                 fg_kv** out) {
+    if (!ctx || !out || layers <= 0 || kv_heads <= 0 || head_dim <= 0 || block_size != 16 || blocks <= 0)
+        return fail(FG_E_ARG, "bad cache shape (block_size must be 16)");
+    HIPCHK(hipSetDevice(ctx->device));
+    fg_kv* kv = new fg_kv();
+    kv->layers = layers;
+    kv->kv_heads = kv_heads;
+    kv->head_dim = head_dim;
+    kv->block_size = block_size;
+    kv->blocks = blocks;
+    const size_t bytes = kv->layer_floats() * layers * 4;
+    if (hipMalloc((void**)&kv->k, bytes) != hipSuccess || hipMalloc((void**)&kv->v, bytes) != hipSuccess) {
+        fg_kv_destroy(kv);
+        return fail(FG_E_NOMEM, "cache allocation failed");
+    }
+    HIPCHK(hipMemset(kv->k, 0, bytes));
+    HIPCHK(hipMemset(kv->v, 0, bytes));
+    *out = kv;
+    return 0;
+}
+
+void fg_kv_destroy(fg_kv* kv) {
+    if (!kv) return;
+    if (kv->k) (void)hipFree(kv->k);
+    if (kv->v) (void)hipFree(kv->v);
+    delete kv;
+}
+
+int fg_kv_read(fg_ctx* ctx, const fg_kv* kv, int32_t layer, float* k_out, float* v_out) {
+    if (!ctx || !kv || layer < 0 || layer >= kv->layers || !k_out || !v_out) return fail(FG_E_ARG, "bad argument");
+    const size_t n = kv->layer_floats();
+    HIPCHK(hipMemcpyAsync(k_out, kv->k + layer * n, n * 4, hipMemcpyDeviceToHost, ctx->stream));
+    HIPCHK(hipMemcpyAsync(v_out, kv->v + layer * n, n * 4, hipMemcpyDeviceToHost, ctx->stream));
+    HIPCHK(hipStreamSynchronize(ctx->stream));
+    return 0;
+}
+
+int fg_kv_write(fg_ctx* ctx, fg_kv* kv, int32_t layer, const float* k, const float* v) {
+    if (!ctx || !kv || layer < 0 || layer >= kv->layers || !k || !v) return fail(FG_E_ARG, "bad argument");
+    const size_t n = kv->layer_floats();
+    HIPCHK(hipMemcpyAsync(kv->k + layer * n, k, n * 4, hipMemcpyHostToDevice, ctx->stream));
+    HIPCHK(hipMemcpyAsync(kv->v + layer * n, v, n * 4, hipMemcpyHostToDevice, ctx->stream));
+    HIPCHK(hipStreamSynchronize(ctx->stream));
+    return 0;
+}
+
+static int check_model_kv(const fg_model* m, const fg_kv* kv) {
+    if (kv->layers < (int)m->layers.size() || kv->kv_heads != m->cfg.kv_heads || kv->head_dim != m->cfg.head_dim)
+        return fail(FG_E_SHAPE, "cache does not match the model");
+    return 0;
+}
+
+int fg_forward(fg_ctx* ctx, const fg_model* m, fg_kv* kv, const fg_chunk* chunks, int32_t n_chunks, float* logits_out,
+               uint32_t* argmax_out, int32_t* rows_out, float* hidden_out) {
+    if (!ctx || !m || !kv || (!chunks && n_chunks > 0) || n_chunks < 0) return fail(FG_E_ARG, "null argument");
+    int rc = check_model_kv(m, kv);
+    if (rc) return rc;
+    HIPCHK(hipSetDevice(ctx->device));
+    std::vector<ChunkIn> in(n_chunks);
+    for (int i = 0; i < n_chunks; i++) {
+        if (chunks[i].n > 0 && !chunks[i].tokens) return fail(FG_E_ARG, "chunk without tokens");
+        in[i] = ChunkIn{chunks[i].tokens, chunks[i].n, chunks[i].pos, chunks[i].blocks, chunks[i].n_blocks,
+                        chunks[i].logits};
+    }
+    Plan P;
+    if ((rc = build_plan(m->cfg, *kv, m->max_pos, in.data(), n_chunks, P))) return rc;
+    if (rows_out) *rows_out = P.S;
+    if (P.t == 0) return 0;
+    if ((rc = ensure(&ctx->hmeta, &ctx->hmeta_cap, P.words * 4, ctx->stream, true))) return rc;
+    if ((rc = ensure(&ctx->dmeta, &ctx->dmeta_cap, P.words * 4, ctx->stream, false))) return rc;
+    pack_plan(P, (int32_t*)ctx->hmeta);
+    HIPCHK(hipMemcpyAsync(ctx->dmeta, ctx->hmeta, P.words * 4, hipMemcpyHostToDevice, ctx->stream));
+    Work w{};
+    const size_t need = layout_work(m, P, w, nullptr);
+    if ((rc = ensure(&ctx->ws, &ctx->ws_cap, need, ctx->stream, false))) return rc;
+    layout_work(m, P, w, ctx->ws);
+    const int32_t* meta = (const int32_t*)ctx->dmeta;
+    rc = run_forward(ctx, m, kv, P, meta, (const uint32_t*)(meta + P.o_tok), 1, w, logits_out ? w.logits : nullptr,
+                     nullptr, nullptr, 0, 0, hidden_out);
+    if (rc) return rc;
+    if (P.S > 0 && logits_out)
+        HIPCHK(hipMemcpyAsync(logits_out, w.logits, (size_t)P.S * m->cfg.vocab * 4, hipMemcpyDeviceToHost, ctx->stream));
+    if (P.S > 0 && argmax_out)
+        HIPCHK(hipMemcpyAsync(argmax_out, w.am, (size_t)P.S * 4, hipMemcpyDeviceToHost, ctx->stream));
+    HIPCHK(hipStreamSynchronize(ctx->stream));
+    return 0;
+}
+
+int fg_spec_step(fg_ctx* ctx, const fg_model* target, fg_kv* tkv, const fg_model* draft, fg_kv* dkv,
+                 const fg_spec_seq* seqs, int32_t n_seqs, int32_t k, uint32_t* out_tokens, int32_t* out_count,
+                 int32_t* out_accepted) {
+    if (!ctx || !target || !tkv || !draft || !dkv || !seqs || n_seqs <= 0 || k <= 0 || !out_tokens || !out_count ||
+        !out_accepted)
+        return fail(FG_E_ARG, "bad argument");
+    if (draft->cfg.vocab != target->cfg.vocab) return fail(FG_E_SHAPE, "draft and target must share a vocabulary");
+    int rc;
+    if ((rc = check_model_kv(target, tkv)) || (rc = check_model_kv(draft, dkv))) return rc;
+    HIPCHK(hipSetDevice(ctx->device));
+    const int K1 = k + 1;
+    // Plans: draft rounds 0..k-1, then the verify pass.
+    std::vector<Plan> plans(k + 1);
+    std::vector<ChunkIn> in(n_seqs);
+    for (int s = 0; s < n_seqs; s++) {
+        const fg_spec_seq& q = seqs[s];
+        if (!q.tail || q.n_tail < 1) return fail(FG_E_ARG, "empty tail");
+        if (q.draft_pos + q.n_tail != q.pos + 1) return fail(FG_E_ARG, "tail must end at the last token");
+        in[s] = ChunkIn{q.tail, q.n_tail, q.draft_pos, q.draft_blocks, q.n_draft_blocks, FG_LOGITS_LAST};
+    }
+    if ((rc = build_plan(draft->cfg, *dkv, draft->max_pos, in.data(), n_seqs, plans[0]))) return rc;
+    static const uint32_t zero_tok[64] = {0};
+    for (int r = 1; r < k; r++) {
+        for (int s = 0; s < n_seqs; s++)
+            in[s] = ChunkIn{nullptr, 1, seqs[s].pos + r, seqs[s].draft_blocks, seqs[s].n_draft_blocks, FG_LOGITS_LAST};
+        if ((rc = build_plan(draft->cfg, *dkv, draft->max_pos, in.data(), n_seqs, plans[r]))) return rc;
+    }
+    for (int s = 0; s < n_seqs; s++)
+        in[s] = ChunkIn{nullptr, K1, seqs[s].pos, seqs[s].blocks, seqs[s].n_blocks, FG_LOGITS_ALL};
+    if ((rc = build_plan(target->cfg, *tkv, target->max_pos, in.data(), n_seqs, plans[k]))) return rc;
+    (void)zero_tok;
+    // One packed upload: every plan, then the verify token rows and outputs.
+    std::vector<size_t> base(k + 1);
+    size_t words = 0;
+    for (int r = 0; r <= k; r++) {
+        base[r] = words;
+        words += plans[r].words;
+    }
+    const size_t o_vtok = words;
+    words += (size_t)n_seqs * K1 + 64;
+    const size_t o_out = words;
+    words += (size_t)n_seqs * K1 + 64;
+    const size_t o_cnt = words;
+    words += (size_t)n_seqs + 64;
+    const size_t o_acc = words;
+    words += (size_t)n_seqs + 64;
+    const size_t o_am = words;
+    words += (size_t)n_seqs * K1 + 64;
+    if ((rc = ensure(&ctx->hmeta, &ctx->hmeta_cap, words * 4, ctx->stream, true))) return rc;
+    if ((rc = ensure(&ctx->dmeta, &ctx->dmeta_cap, words * 4, ctx->stream, false))) return rc;
+    int32_t* h = (int32_t*)ctx->hmeta;
+    for (int r = 0; r <= k; r++) pack_plan(plans[r], h + base[r]);
+    uint32_t* hv = (uint32_t*)(h + o_vtok);
+    for (int s = 0; s < n_seqs; s++) {
+        hv[s * K1] = seqs[s].tail[seqs[s].n_tail - 1];
+        for (int j = 1; j < K1; j++) hv[s * K1 + j] = 0;
+    }
+    HIPCHK(hipMemcpyAsync(ctx->dmeta, ctx->hmeta, o_out * 4, hipMemcpyHostToDevice, ctx->stream));
+    size_t need = 0;
+    Work w{};
+    const fg_model* models[2] = {draft, target};
+    for (int r = 0; r <= k; r++) need = std::max(need, layout_work(models[r == k], plans[r], w, nullptr));
+    if ((rc = ensure(&ctx->ws, &ctx->ws_cap, need, ctx->stream, false))) return rc;
+    int32_t* dm = (int32_t*)ctx->dmeta;
+    uint32_t* vtok = (uint32_t*)(dm + o_vtok);
+    HIPCHK(hipEventRecord(ctx->ev[0], ctx->stream));
+    for (int r = 0; r < k; r++) {
+        layout_work(draft, plans[r], w, ctx->ws);
+        const int32_t* meta = dm + base[r];
+        const uint32_t* tok = r == 0 ? (const uint32_t*)(meta + plans[r].o_tok) : vtok + r;
+        const int stride = r == 0 ? 1 : K1;
+        // the draft's greedy proposal d_{r+1} goes to verify row s, column r+1
+        if ((rc = run_forward(ctx, draft, dkv, plans[r], meta, tok, stride, w, nullptr,
+                              (uint32_t*)(dm + o_am), vtok, K1, r + 1, nullptr)))
+            return rc;
+    }
+    HIPCHK(hipEventRecord(ctx->ev[1], ctx->stream));
+    layout_work(target, plans[k], w, ctx->ws);
+    if ((rc = run_forward(ctx, target, tkv, plans[k], dm + base[k], vtok, 1, w, nullptr, (uint32_t*)(dm + o_am),
+                          nullptr, 0, 0, nullptr)))
+        return rc;
+    launch_accept(ctx->stream, (const uint32_t*)(dm + o_am), vtok, n_seqs, k, (uint32_t*)(dm + o_out), dm + o_cnt,
+                  dm + o_acc);
+    HIPCHK(hipGetLastError());
+    HIPCHK(hipEventRecord(ctx->ev[2], ctx->stream));
+    HIPCHK(hipMemcpyAsync(h + o_out, dm + o_out, (words - o_out) * 4, hipMemcpyDeviceToHost, ctx->stream));
+    HIPCHK(hipStreamSynchronize(ctx->stream));
+    memcpy(out_tokens, h + o_out, (size_t)n_seqs * K1 * 4);
+    memcpy(out_count, h + o_cnt, (size_t)n_seqs * 4);
+    memcpy(out_accepted, h + o_acc, (size_t)n_seqs * 4);
+    float a = 0, b = 0;
+    HIPCHK(hipEventElapsedTime(&a, ctx->ev[0], ctx->ev[1]));
+    HIPCHK(hipEventElapsedTime(&b, ctx->ev[1], ctx->ev[2]));
+    ctx->last_us[0] = a * 1000.0f;
+    ctx->last_us[1] = b * 1000.0f;
+    ctx->last_us[2] = (a + b) * 1000.0f;
+    return 0;
+}
+
+int fg_last_step_times(const fg_ctx* ctx, float* us3) {
+    if (!ctx || !us3) return fail(FG_E_ARG, "null argument");
+    memcpy(us3, ctx->last_us, sizeof(ctx->last_us));
+    return 0;
+}
+
+int fg_mat_upload(fg_ctx* ctx, const fg_matrix* w, fg_mat** out) {
+    if (!ctx || !w || !out) return fail(FG_E_ARG, "null argument");
+    HIPCHK(hipSetDevice(ctx->device));
+    fg_mat* m = new fg_mat();
+    m->device = ctx->device;
+    int rc = upload_mat(*w, m->m, nullptr);
+    if (rc) {
+        fg_mat_destroy(m);
+        return rc;
+    }
+    *out = m;
+    return 0;
+}
+
+void fg_mat_destroy(fg_mat* m) {
+    if (!m) return;
+    if (m->m.w) (void)hipFree(m->m.w);
+    if (m->m.s) (void)hipFree(m->m.s);
+    delete m;
+}
+
+// Workspace for a lone product: pieces, partials, (x, y when staged).
+static size_t layout_mat(const DMat& d, int m, const GemvPlan& gp, Pieces& p, float** part, float** xbuf,
+                         float** ybuf, void* base) {
+    Carver cv(base);
+    p.kb = d.kb;
+    p.passes = (m + 3) / 4;
+    p.a = cv.take<uint8_t>((size_t)d.kb * p.passes * 64 * 16);
+    p.xs = cv.take<float>((size_t)d.kb * p.passes * 4);
+    *part = cv.take<float>((size_t)gp.splits * m * d.rows);
+    *xbuf = cv.take<float>((size_t)m * d.cols);
+    *ybuf = cv.take<float>((size_t)m * d.rows);
+    return cv.off + 256;
+}
+
+int fg_matmul(fg_ctx* ctx, const fg_mat* w, const float* x, int32_t m, const float* bias, float* y) {
+    if (!ctx || !w || !x || !y || m <= 0) return fail(FG_E_ARG, "bad argument");
+    HIPCHK(hipSetDevice(ctx->device));
+    const DMat& d = w->m;
+    const GemvPlan gp = plan_gemv(d, m);
+    Pieces p;
+    float *part, *xb, *yb;
+    const size_t need = layout_mat(d, m, gp, p, &part, &xb, &yb, nullptr) + (size_t)d.rows * 4 + 256;
+    int rc;
+    if ((rc = ensure(&ctx->ws, &ctx->ws_cap, need, ctx->stream, false))) return rc;
+    layout_mat(d, m, gp, p, &part, &xb, &yb, ctx->ws);
+    float* bb = nullptr;
+    if (bias) {
+        bb = yb + (size_t)m * d.rows;
+        bb = (float*)(((uintptr_t)bb + 255) & ~(uintptr_t)255);
+        HIPCHK(hipMemcpyAsync(bb, bias, (size_t)d.rows * 4, hipMemcpyHostToDevice, ctx->stream));
+    }
+    HIPCHK(hipMemcpyAsync(xb, x, (size_t)m * d.cols * 4, hipMemcpyHostToDevice, ctx->stream));
+    launch_pieces(ctx->stream, d.kind, xb, d.cols, m, d.cols, nullptr, nullptr, p);
+    launch_gemv(ctx->stream, d, p, m, gp, part);
+    launch_reduce(ctx->stream, part, gp.splits, m, d.rows, bb, yb);
+    HIPCHK(hipGetLastError());
+    HIPCHK(hipMemcpyAsync(y, yb, (size_t)m * d.rows * 4, hipMemcpyDeviceToHost, ctx->stream));
+    HIPCHK(hipStreamSynchronize(ctx->stream));
+    return 0;
+}
+
+int fg_matmul_device(fg_ctx* ctx, const fg_mat* w, const float* x_dev, int32_t m, float* y_dev) {
+    if (!ctx || !w || !x_dev || !y_dev || m <= 0) return fail(FG_E_ARG, "bad argument");
+    const DMat& d = w->m;
+    const GemvPlan gp = plan_gemv(d, m);
+    Pieces p;
+    float *part, *xb, *yb;
+    const size_t need = layout_mat(d, m, gp, p, &part, &xb, &yb, nullptr);
+    int rc;
+    if ((rc = ensure(&ctx->ws, &ctx->ws_cap, need, ctx->stream, false))) return rc;
+    layout_mat(d, m, gp, p, &part, &xb, &yb, ctx->ws);
+    launch_pieces(ctx->stream, d.kind, x_dev, d.cols, m, d.cols, nullptr, nullptr, p);
+    launch_gemv(ctx->stream, d, p, m, gp, part);
+    launch_reduce(ctx->stream, part, gp.splits, m, d.rows, nullptr, y_dev);
+    HIPCHK(hipGetLastError());
+    return 0;
+}
+
+}  // extern "C"

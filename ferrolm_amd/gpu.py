@@ -1,0 +1,312 @@
+"""ctypes binding of libferro_gpu.so (the C ABI in include/ferro_gpu.h).
+
+This is the product path: every call runs the HIP kernels for gfx950. There
+is no CPU fallback — if the library is missing or no GPU is present, the
+calls raise.
+"""
+from __future__ import annotations
+
+import ctypes as C
+from dataclasses import dataclass
+from pathlib import Path
+
+import numpy as np
+
+from .weights import BF16, Config, HostModel, Matrix
+
+PKG = Path(__file__).resolve().parent
+LIB_PATH = PKG / "libferro_gpu.so"
+
+f32p = C.POINTER(C.c_float)
+u16p = C.POINTER(C.c_uint16)
+u8p = C.POINTER(C.c_uint8)
+u32p = C.POINTER(C.c_uint32)
+i32p = C.POINTER(C.c_int32)
+
+LOGITS_NONE, LOGITS_LAST, LOGITS_ALL = 0, 1, 2
+
+
+class FgConfig(C.Structure):
+    _fields_ = [(n, C.c_int32) for n in ("vocab", "hidden", "intermediate", "layers", "heads", "kv_heads",
+                                          "head_dim")] + [
+        ("rms_eps", C.c_float), ("rope_theta", C.c_float), ("rope_llama3", C.c_int32),
+        ("rope_factor", C.c_float), ("rope_low_freq", C.c_float), ("rope_high_freq", C.c_float),
+        ("rope_orig_max_pos", C.c_int32), ("max_position", C.c_int32), ("tie_embeddings", C.c_int32),
+        ("qkv_bias", C.c_int32)]
+
+
+class FgMatrix(C.Structure):
+    _fields_ = [("format", C.c_int32), ("rows", C.c_int32), ("cols", C.c_int32), ("_pad", C.c_int32),
+                ("bf16", u16p), ("q", u8p), ("s", f32p)]
+
+
+class FgLayer(C.Structure):
+    _fields_ = [("attn_norm", f32p), ("wqkv", FgMatrix), ("bqkv", f32p), ("wo", FgMatrix),
+                ("mlp_norm", f32p), ("w_gate_up", FgMatrix), ("w_down", FgMatrix)]
+
+
+class FgChunk(C.Structure):
+    _fields_ = [("tokens", u32p), ("n", C.c_int32), ("pos", C.c_int32), ("blocks", u32p),
+                ("n_blocks", C.c_int32), ("logits", C.c_int32)]
+
+
+class FgSpecSeq(C.Structure):
+    _fields_ = [("tail", u32p), ("n_tail", C.c_int32), ("draft_pos", C.c_int32), ("pos", C.c_int32),
+                ("blocks", u32p), ("n_blocks", C.c_int32), ("draft_blocks", u32p), ("n_draft_blocks", C.c_int32)]
+
+
+EXPORTS = {
+    "fg_ctx_create": (C.c_int, [C.c_int, C.POINTER(C.c_void_p)]),
+    "fg_ctx_destroy": (None, [C.c_void_p]),
+    "fg_last_error": (C.c_char_p, []),
+    "fg_ctx_sync": (C.c_int, [C.c_void_p]),
+    "fg_model_upload": (C.c_int, [C.c_void_p, C.POINTER(FgConfig), C.POINTER(FgLayer), u16p, f32p, u16p,
+                                  C.POINTER(C.c_void_p)]),
+    "fg_model_truncated": (C.c_int, [C.c_void_p, C.c_void_p, C.c_int32, C.POINTER(C.c_void_p)]),
+    "fg_model_destroy": (None, [C.c_void_p]),
+    "fg_model_weight_bytes": (C.c_int64, [C.c_void_p]),
+    "fg_kv_create": (C.c_int, [C.c_void_p, C.c_int32, C.c_int32, C.c_int32, C.c_int32, C.c_int32,
+                               C.POINTER(C.c_void_p)]),
+    "fg_kv_destroy": (None, [C.c_void_p]),
+    "fg_kv_read": (C.c_int, [C.c_void_p, C.c_void_p, C.c_int32, f32p, f32p]),
+    "fg_kv_write": (C.c_int, [C.c_void_p, C.c_void_p, C.c_int32, f32p, f32p]),
+    "fg_forward": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.POINTER(FgChunk), C.c_int32, f32p, u32p, i32p,
+                             f32p]),
+    "fg_spec_step": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.POINTER(FgSpecSeq),
+                               C.c_int32, C.c_int32, u32p, i32p, i32p]),
+    "fg_last_step_times": (C.c_int, [C.c_void_p, f32p]),
+    "fg_mat_upload": (C.c_int, [C.c_void_p, C.POINTER(FgMatrix), C.POINTER(C.c_void_p)]),
+    "fg_mat_destroy": (None, [C.c_void_p]),
+    "fg_matmul": (C.c_int, [C.c_void_p, C.c_void_p, f32p, C.c_int32, f32p, f32p]),
+    "fg_matmul_device": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_int32, C.c_void_p]),
+}
+
+_lib = None
+
+
+def lib():
+    """Loads libferro_gpu.so (built by ferrolm_amd.build); raises if absent."""
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            raise RuntimeError(f"{LIB_PATH} is not built: run `python -m ferrolm_amd.build`")
+        l = C.CDLL(str(LIB_PATH))
+        for name, (res, args) in EXPORTS.items():
+            fn = getattr(l, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = l
+    return _lib
+
+
+class FgError(RuntimeError):
+    pass
+
+
+def check(rc: int) -> None:
+    if rc != 0:
+        raise FgError(f"ferro_gpu error {rc}: {lib().fg_last_error().decode()}")
+
+
+def ptr(a, t):
+    if a is None:
+        return C.cast(None, t)
+    assert a.flags["C_CONTIGUOUS"], "arrays passed to the library must be contiguous"
+    return a.ctypes.data_as(t)
+
+
+def config_struct(c: Config) -> FgConfig:
+    return FgConfig(c.vocab, c.hidden, c.intermediate, c.layers, c.heads, c.kv_heads, c.head_dim, c.rms_eps,
+                    c.rope_theta, int(c.rope_llama3), c.rope_factor, c.rope_low_freq, c.rope_high_freq,
+                    c.rope_orig_max_pos, c.max_position, int(c.tie_embeddings), int(c.qkv_bias))
+
+
+def matrix_struct(m: Matrix) -> FgMatrix:
+    return FgMatrix(m.kind, m.rows, m.cols, 0, ptr(m.bf16, u16p), ptr(m.q, u8p), ptr(m.s, f32p))
+
+
+class Context:
+    """A device context: one HIP stream and its workspace (fg_ctx)."""
+
+    def __init__(self, device: int = 0):
+        h = C.c_void_p()
+        check(lib().fg_ctx_create(device, C.byref(h)))
+        self.h = h
+
+    def sync(self) -> None:
+        check(lib().fg_ctx_sync(self.h))
+
+    def close(self) -> None:
+        if getattr(self, "h", None):
+            lib().fg_ctx_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        self.close()
+
+
+class Model:
+    """Device copy of a HostModel (fg_model_upload)."""
+
+    def __init__(self, ctx: Context, hm: HostModel | None, _handle=None, _base=None, cfg: Config | None = None):
+        self.ctx = ctx
+        self._base = _base
+        if _handle is not None:
+            self.h = _handle
+            self.cfg = cfg
+            return
+        self.cfg = hm.cfg
+        ls = (FgLayer * max(1, len(hm.layers)))()
+        for i, l in enumerate(hm.layers):
+            ls[i] = FgLayer(ptr(l.attn_norm, f32p), matrix_struct(l.wqkv), ptr(l.bqkv, f32p), matrix_struct(l.wo),
+                            ptr(l.mlp_norm, f32p), matrix_struct(l.w_gate_up), matrix_struct(l.w_down))
+        cs = config_struct(hm.cfg)
+        h = C.c_void_p()
+        check(lib().fg_model_upload(ctx.h, C.byref(cs), ls, ptr(hm.embed, u16p), ptr(hm.norm, f32p),
+                                    ptr(hm.lm_head, u16p), C.byref(h)))
+        self.h = h
+
+    def truncated(self, n: int) -> "Model":
+        from dataclasses import replace
+        h = C.c_void_p()
+        check(lib().fg_model_truncated(self.ctx.h, self.h, n, C.byref(h)))
+        return Model(self.ctx, None, _handle=h, _base=self, cfg=replace(self.cfg, layers=min(n, self.cfg.layers)))
+
+    def weight_bytes(self) -> int:
+        return int(lib().fg_model_weight_bytes(self.h))
+
+    def close(self) -> None:
+        if getattr(self, "h", None):
+            lib().fg_model_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        self.close()
+
+
+class KvCache:
+    """Paged f32 KV cache on the device (fg_kv_create), reference layout."""
+
+    def __init__(self, ctx: Context, cfg: Config, blocks: int, block_size: int = 16):
+        self.ctx = ctx
+        self.cfg = cfg
+        self.blocks = blocks
+        self.block_size = block_size
+        h = C.c_void_p()
+        check(lib().fg_kv_create(ctx.h, cfg.layers, cfg.kv_heads, cfg.head_dim, block_size, blocks, C.byref(h)))
+        self.h = h
+
+    def _n(self) -> int:
+        return self.blocks * self.block_size * self.cfg.kv_heads * self.cfg.head_dim
+
+    def layer(self, i: int):
+        k = np.zeros(self._n(), np.float32)
+        v = np.zeros(self._n(), np.float32)
+        check(lib().fg_kv_read(self.ctx.h, self.h, i, ptr(k, f32p), ptr(v, f32p)))
+        return k, v
+
+    def set_layer(self, i: int, k: np.ndarray, v: np.ndarray) -> None:
+        k = np.ascontiguousarray(k, np.float32)
+        v = np.ascontiguousarray(v, np.float32)
+        check(lib().fg_kv_write(self.ctx.h, self.h, i, ptr(k, f32p), ptr(v, f32p)))
+
+    def close(self) -> None:
+        if getattr(self, "h", None):
+            lib().fg_kv_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        self.close()
+
+
+@dataclass
+class ForwardOut:
+    logits: np.ndarray | None
+    argmax: np.ndarray
+    hidden: np.ndarray | None
+
+
+def forward(ctx: Context, model: Model, kv: KvCache, chunks, logits: bool = True, hidden: bool = False) -> ForwardOut:
+    """Model::forward on the device. chunks: (tokens, pos, blocks, mode)."""
+    arr = (FgChunk * max(1, len(chunks)))()
+    keep = []
+    rows = 0
+    t = 0
+    for i, (tok, pos, blocks, mode) in enumerate(chunks):
+        tok = np.ascontiguousarray(tok, dtype=np.uint32)
+        blocks = np.ascontiguousarray(blocks, dtype=np.uint32)
+        keep += [tok, blocks]
+        arr[i] = FgChunk(ptr(tok, u32p), len(tok), pos, ptr(blocks, u32p), len(blocks), mode)
+        rows += len(tok) if mode == LOGITS_ALL else (1 if mode == LOGITS_LAST and len(tok) else 0)
+        t += len(tok)
+    lg = np.zeros((rows, model.cfg.vocab), np.float32) if logits else None
+    am = np.zeros(rows, np.uint32)
+    hid = np.zeros((model.cfg.layers + 1, t, model.cfg.hidden), np.float32) if hidden else None
+    nrows = C.c_int32(0)
+    check(lib().fg_forward(ctx.h, model.h, kv.h, arr, len(chunks), ptr(lg, f32p), ptr(am, u32p), C.byref(nrows),
+                           ptr(hid, f32p)))
+    assert nrows.value == rows
+    return ForwardOut(lg, am, hid)
+
+
+@dataclass
+class SpecSeq:
+    tail: np.ndarray
+    draft_pos: int
+    pos: int
+    blocks: np.ndarray
+    draft_blocks: np.ndarray
+
+
+def spec_step(ctx: Context, target: Model, tkv: KvCache, draft: Model, dkv: KvCache, seqs: list, k: int):
+    """One greedy speculative step on device. Returns (tokens per sequence,
+    accepted counts)."""
+    n = len(seqs)
+    arr = (FgSpecSeq * n)()
+    keep = []
+    for i, s in enumerate(seqs):
+        tail = np.ascontiguousarray(s.tail, np.uint32)
+        bl = np.ascontiguousarray(s.blocks, np.uint32)
+        db = np.ascontiguousarray(s.draft_blocks, np.uint32)
+        keep += [tail, bl, db]
+        arr[i] = FgSpecSeq(ptr(tail, u32p), len(tail), s.draft_pos, s.pos, ptr(bl, u32p), len(bl), ptr(db, u32p),
+                           len(db))
+    out = np.zeros((n, k + 1), np.uint32)
+    cnt = np.zeros(n, np.int32)
+    acc = np.zeros(n, np.int32)
+    check(lib().fg_spec_step(ctx.h, target.h, tkv.h, draft.h, dkv.h, arr, n, k, ptr(out, u32p), ptr(cnt, i32p),
+                             ptr(acc, i32p)))
+    return [out[i, :cnt[i]].copy() for i in range(n)], acc
+
+
+def last_step_times(ctx: Context) -> np.ndarray:
+    t = np.zeros(3, np.float32)
+    check(lib().fg_last_step_times(ctx.h, ptr(t, f32p)))
+    return t
+
+
+class Mat:
+    """A single device matrix (kernels::matmul's operand)."""
+
+    def __init__(self, ctx: Context, m: Matrix):
+        self.ctx = ctx
+        self.rows, self.cols, self.kind = m.rows, m.cols, m.kind
+        ms = matrix_struct(m)
+        h = C.c_void_p()
+        check(lib().fg_mat_upload(ctx.h, C.byref(ms), C.byref(h)))
+        self.h = h
+
+    def matmul(self, x: np.ndarray, bias: np.ndarray | None = None) -> np.ndarray:
+        x = np.ascontiguousarray(x, np.float32)
+        y = np.zeros((x.shape[0], self.rows), np.float32)
+        b = None if bias is None else np.ascontiguousarray(bias, np.float32)
+        check(lib().fg_matmul(self.ctx.h, self.h, ptr(x, f32p), x.shape[0], ptr(b, f32p), ptr(y, f32p)))
+        return y
+
+    def close(self) -> None:
+        if getattr(self, "h", None):
+            lib().fg_mat_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        self.close()

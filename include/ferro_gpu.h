@@ -1,0 +1,198 @@
+/*
+ * ferro_gpu.h — C ABI of the MI355X (gfx950) speculative-decoding verify
+ * path for ferrolm.
+ *
+ * The reference has no FFI: its seam is the internal Rust call
+ * `Model::forward(&self, pool, cache: &mut KvCache, chunks: &[Chunk]) ->
+ * Vec<f32>` (src/model.rs:269) and the engine's accept loop
+ * (src/engine.rs:563-616). Each entry point below replaces one reference
+ * interface, named at its declaration, so a Rust caller binds it with a
+ * thin `extern "C"` block.
+ *
+ * Conventions
+ *  - Every function returns 0 on success and a negative FG_E_* code on
+ *    failure; fg_last_error() gives the message (thread-local). Nothing
+ *    aborts or unwinds across the ABI: the reference's shape `assert!`s
+ *    (src/model.rs:284-287, src/kernels.rs:251-252, src/quant.rs:83-86)
+ *    become FG_E_SHAPE returns.
+ *  - Host pointers are borrowed for the duration of the call only.
+ *  - One host thread per context. Work is queued on the context's HIP
+ *    stream; calls that return results to host memory synchronise it.
+ *  - Token ids are uint32, positions and counts int32, weights in the
+ *    reference's formats (see fg_matrix).
+ */
+#ifndef FERRO_GPU_H
+#define FERRO_GPU_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define FG_OK 0
+#define FG_E_ARG -1      /* null pointer or out-of-range argument */
+#define FG_E_SHAPE -2    /* shapes do not fit (reference: assert! panic) */
+#define FG_E_DEVICE -3   /* HIP runtime error */
+#define FG_E_NOMEM -4    /* device allocation failed */
+
+enum { FG_BF16 = 0, FG_INT8 = 1, FG_INT4 = 2 };
+enum { FG_LOGITS_NONE = 0, FG_LOGITS_LAST = 1, FG_LOGITS_ALL = 2 }; /* src/model.rs:74-79 */
+
+typedef struct fg_ctx fg_ctx;
+typedef struct fg_model fg_model;
+typedef struct fg_kv fg_kv;
+typedef struct fg_mat fg_mat;
+
+/* Model hyperparameters: the fields of Config (src/config.rs:21-39) the
+ * forward pass reads. */
+typedef struct {
+    int32_t vocab, hidden, intermediate, layers, heads, kv_heads, head_dim;
+    float rms_eps, rope_theta;
+    int32_t rope_llama3; /* RopeScaling::Llama3 when nonzero */
+    float rope_factor, rope_low_freq, rope_high_freq;
+    int32_t rope_orig_max_pos;
+    int32_t max_position;
+    int32_t tie_embeddings;
+    int32_t qkv_bias;
+} fg_config;
+
+/* One weight matrix as the reference holds it (rows x cols, y = x W^T):
+ *  - FG_BF16: `bf16` row-major bf16 bit patterns (the data given to
+ *    Matrix::new, src/kernels.rs:53);
+ *  - FG_INT8 / FG_INT4: a QMatrix (src/quant.rs:64-76): `q` codes per
+ *    32-row panel and input position (int8: one signed byte per row; int4:
+ *    byte i = row i low nibble | row i+16 high nibble, each offset by 8),
+ *    `s` f32 scales [panel][group of 32][32 rows].
+ * The library repacks on upload into its own device layout. */
+typedef struct {
+    int32_t format, rows, cols, _pad;
+    const uint16_t* bf16;
+    const uint8_t* q;
+    const float* s;
+} fg_matrix;
+
+/* One transformer layer (Layer, src/model.rs:28-38): q/k/v and gate/up
+ * stacked, norms already carrying any AWQ fold (src/awq.rs:109-122). */
+typedef struct {
+    const float* attn_norm;
+    fg_matrix wqkv;
+    const float* bqkv; /* NULL unless qkv_bias */
+    fg_matrix wo;
+    const float* mlp_norm;
+    fg_matrix w_gate_up;
+    fg_matrix w_down;
+} fg_layer;
+
+/* Chunk (src/model.rs:84-89): `n` tokens at positions pos..pos+n-1 of a
+ * sequence whose cache blocks are `blocks`. */
+typedef struct {
+    const uint32_t* tokens;
+    int32_t n, pos;
+    const uint32_t* blocks;
+    int32_t n_blocks, logits;
+} fg_chunk;
+
+/* One sequence of a speculative step (state of Seq, src/engine.rs:150-168
+ * that Engine::execute/propose read, src/engine.rs:499-717). */
+typedef struct {
+    const uint32_t* tail;   /* tokens[draft_computed..]: the draft's round-0 input */
+    int32_t n_tail;         /* >= 1 */
+    int32_t draft_pos;      /* draft_computed */
+    int32_t pos;            /* computed == tokens.len() - 1 */
+    const uint32_t* blocks; /* target block table (>= pos + k + 1 slots) */
+    int32_t n_blocks;
+    const uint32_t* draft_blocks; /* draft block table (>= pos + k slots) */
+    int32_t n_draft_blocks;
+} fg_spec_seq;
+
+/* ---- context ---------------------------------------------------------- */
+/* Engine::new's device side: binds `device`, creates the stream and
+ * workspace. No reference counterpart beyond Pool::new (src/pool.rs:45). */
+int fg_ctx_create(int device, fg_ctx** out);
+void fg_ctx_destroy(fg_ctx* ctx);
+const char* fg_last_error(void);
+/* Blocks until all work queued on the context has finished. */
+int fg_ctx_sync(fg_ctx* ctx);
+
+/* ---- weights ---------------------------------------------------------- */
+/* Model::load/random + Model::quantize output handed to the device
+ * (src/model.rs:92-219). embed is vocab x hidden bf16 row-major; lm_head
+ * NULL when tied (src/model.rs:263-265). */
+int fg_model_upload(fg_ctx* ctx, const fg_config* cfg, const fg_layer* layers,
+                    const uint16_t* embed, const float* norm,
+                    const uint16_t* lm_head, fg_model** out);
+/* Model::truncated (src/model.rs:237-241): the first `layers` layers of
+ * `base`, sharing its device weights. `base` must outlive the result. */
+int fg_model_truncated(fg_ctx* ctx, const fg_model* base, int32_t layers,
+                       fg_model** out);
+void fg_model_destroy(fg_model* m);
+/* Device bytes of the model's weights in the reference's accounting
+ * (Model::weight_bytes, src/model.rs:221-229). */
+int64_t fg_model_weight_bytes(const fg_model* m);
+
+/* ---- paged KV cache --------------------------------------------------- */
+/* KvCache::new (src/kv.rs:33-44): f32 keys and values for every layer in
+ * the reference layout [layer][block][kv_head][block_size][head_dim]. */
+int fg_kv_create(fg_ctx* ctx, int32_t layers, int32_t kv_heads,
+                 int32_t head_dim, int32_t block_size, int32_t blocks,
+                 fg_kv** out);
+void fg_kv_destroy(fg_kv* kv);
+/* KvCache::layer (src/kv.rs:58-61): copies one layer's K and V to host
+ * (each blocks*block_size*kv_heads*head_dim floats). For tests. */
+int fg_kv_read(fg_ctx* ctx, const fg_kv* kv, int32_t layer, float* k_out,
+               float* v_out);
+/* Overwrites one layer's K and V from host. For tests and baselines. */
+int fg_kv_write(fg_ctx* ctx, fg_kv* kv, int32_t layer, const float* k,
+                const float* v);
+
+/* ---- forward ---------------------------------------------------------- */
+/* Model::forward (src/model.rs:269-362): runs the chunks through the
+ * model, writes their keys/values into `kv` and produces the requested
+ * logits rows in chunk order. logits_out (rows x vocab, may be NULL)
+ * receives the logits; argmax_out (rows, may be NULL) their greedy token,
+ * sampler::argmax (src/sampler.rs:42-51): first index of the maximum.
+ * *rows_out (may be NULL) receives the row count. hidden_out, if not NULL,
+ * receives the residual stream after the embedding and after each layer,
+ * (layers+1) x tokens x hidden — the per-layer tap for parity tests. */
+int fg_forward(fg_ctx* ctx, const fg_model* m, fg_kv* kv,
+               const fg_chunk* chunks, int32_t n_chunks, float* logits_out,
+               uint32_t* argmax_out, int32_t* rows_out, float* hidden_out);
+
+/* ---- speculative step ------------------------------------------------- */
+/* One greedy speculative step for n_seqs sequences, entirely on device:
+ * Engine::propose's k draft rounds (src/engine.rs:658-717), the target's
+ * verify pass over [last, d1..dk] (src/engine.rs:512-542, Logits::All),
+ * greedy accept-prefix + bonus token (src/engine.rs:563-610). Only the
+ * emitted ids cross to the host: out_tokens[s*(k+1) + j], j <
+ * out_count[s]; out_accepted[s] = accepted proposals. The caller's
+ * rollback is the reference's (src/engine.rs:613-615):
+ * computed = pos + 1 + accepted, draft_computed = min(pos + k, pos + 1 +
+ * accepted). Draft proposals never leave the device. */
+int fg_spec_step(fg_ctx* ctx, const fg_model* target, fg_kv* target_kv,
+                 const fg_model* draft, fg_kv* draft_kv,
+                 const fg_spec_seq* seqs, int32_t n_seqs, int32_t k,
+                 uint32_t* out_tokens, int32_t* out_count,
+                 int32_t* out_accepted);
+
+/* Device time in microseconds of the last fg_spec_step's phases, measured
+ * with HIP events on the context stream: [0] draft rounds, [1] verify
+ * (target forward + argmax + accept), [2] whole step. */
+int fg_last_step_times(const fg_ctx* ctx, float* us3);
+
+/* ---- single matrix (kernels::matmul, src/kernels.rs:249-275) ----------- */
+int fg_mat_upload(fg_ctx* ctx, const fg_matrix* w, fg_mat** out);
+void fg_mat_destroy(fg_mat* m);
+/* y (m x rows) = x (m x cols) W^T (+ bias), host buffers. */
+int fg_matmul(fg_ctx* ctx, const fg_mat* w, const float* x, int32_t m,
+              const float* bias, float* y);
+/* The same product on device-resident buffers (x_dev, y_dev device
+ * pointers), queued on the context stream without synchronising; used to
+ * time the GEMV kernels. */
+int fg_matmul_device(fg_ctx* ctx, const fg_mat* w, const float* x_dev,
+                     int32_t m, float* y_dev);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

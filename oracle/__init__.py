@@ -1,0 +1,277 @@
+"""ctypes binding of the CPU oracle (liboracle.so, built from ferro_oracle.c).
+
+TEST INFRASTRUCTURE ONLY. The oracle is a C restatement of the reference's
+CPU path (Rust, /root/reference/src), used as the parity checker for the
+HIP path and as bench.py's timed CPU baseline. Only tests/, the smoke()
+entry point and bench.py's cpu_baseline leg import this module; nothing in
+the ferrolm_amd package does.
+
+Parity pins (tests/test_oracle.py): the three transformers fixtures of the
+reference's tests/reference.rs (logits within 1e-3 of the largest logit and
+40 exact greedy tokens), the reference's kernel and quantizer unit-test
+properties (src/kernels.rs:758-818, src/quant.rs:456-523), closed forms
+(f64 matmul, dense softmax attention) and engine invariants
+(speculative greedy == target alone, self-draft accepts everything,
+tests/engine.rs:134-160).
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import subprocess
+from pathlib import Path
+
+import numpy as np
+
+from ferrolm_amd.weights import BF16, HostModel, Matrix
+
+HERE = Path(__file__).resolve().parent
+LIB = HERE / "liboracle.so"
+
+f32p = C.POINTER(C.c_float)
+u16p = C.POINTER(C.c_uint16)
+u8p = C.POINTER(C.c_uint8)
+u32p = C.POINTER(C.c_uint32)
+i32p = C.POINTER(C.c_int32)
+i64p = C.POINTER(C.c_int64)
+
+
+class OrConfig(C.Structure):
+    _fields_ = [(n, C.c_int32) for n in ("vocab", "hidden", "intermediate", "layers", "heads", "kv_heads",
+                                          "head_dim")] + [
+        ("rms_eps", C.c_float), ("rope_theta", C.c_float), ("rope_llama3", C.c_int32),
+        ("rope_factor", C.c_float), ("rope_low_freq", C.c_float), ("rope_high_freq", C.c_float),
+        ("rope_orig_max_pos", C.c_int32), ("max_position", C.c_int32), ("tie_embeddings", C.c_int32),
+        ("qkv_bias", C.c_int32)]
+
+
+class OrMatrix(C.Structure):
+    _fields_ = [("kind", C.c_int32), ("rows", C.c_int32), ("cols", C.c_int32), ("_pad", C.c_int32),
+                ("bf16", u16p), ("q", u8p), ("s", f32p)]
+
+
+class OrLayer(C.Structure):
+    _fields_ = [("attn_norm", f32p), ("wqkv", OrMatrix), ("bqkv", f32p), ("wo", OrMatrix),
+                ("mlp_norm", f32p), ("w_gate_up", OrMatrix), ("w_down", OrMatrix)]
+
+
+class OrChunk(C.Structure):
+    _fields_ = [("tokens", u32p), ("n", C.c_int32), ("pos", C.c_int32), ("blocks", u32p),
+                ("n_blocks", C.c_int32), ("logits", C.c_int32)]
+
+
+def build() -> None:
+    """Compiles liboracle.so with the committed Makefile."""
+    subprocess.run(["make", "-s", "-C", str(HERE), "-B"], check=True)
+
+
+_lib = None
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not LIB.exists():
+            build()
+        l = C.CDLL(str(LIB))
+        sig = {
+            "or_rng_new": (C.c_uint64, [C.c_uint64]),
+            "or_rng_next": (C.c_uint64, [C.POINTER(C.c_uint64)]),
+            "or_rng_uniform": (C.c_double, [C.POINTER(C.c_uint64)]),
+            "or_rng_normal": (C.c_double, [C.POINTER(C.c_uint64)]),
+            "or_f32_to_bf16": (C.c_uint16, [C.c_float]),
+            "or_exp": (C.c_float, [C.c_float]),
+            "or_dot": (C.c_float, [f32p, f32p, C.c_int32]),
+            "or_rms_norm": (None, [f32p, f32p, C.c_int32, C.c_int32, C.c_float, f32p]),
+            "or_silu_mul": (None, [f32p, C.c_int32, C.c_int32, f32p]),
+            "or_argmax": (C.c_uint32, [f32p, C.c_int32]),
+            "or_set_threads": (None, [C.c_int32]),
+            "or_quantize": (C.c_int32, [C.c_int32, C.c_int32, C.c_int32, f32p, f32p, u8p, f32p]),
+            "or_dequantize": (None, [C.c_int32, C.c_int32, C.c_int32, u8p, f32p, f32p]),
+            "or_matmul": (C.c_int32, [C.POINTER(OrMatrix), f32p, C.c_int32, f32p, f32p]),
+            "or_model_create": (C.c_void_p, [C.POINTER(OrConfig), C.POINTER(OrLayer), u16p, f32p, u16p]),
+            "or_model_truncated": (C.c_void_p, [C.c_void_p, C.c_int32]),
+            "or_model_destroy": (None, [C.c_void_p]),
+            "or_kv_create": (C.c_void_p, [C.c_int32] * 5),
+            "or_kv_destroy": (None, [C.c_void_p]),
+            "or_kv_read": (C.c_int32, [C.c_void_p, C.c_int32, f32p, f32p]),
+            "or_kv_write_layer": (C.c_int32, [C.c_void_p, C.c_int32, f32p, f32p]),
+            "or_forward": (C.c_int32, [C.c_void_p, C.c_void_p, C.POINTER(OrChunk), C.c_int32, f32p, f32p]),
+            "or_generate": (C.c_int32, [C.c_void_p, C.c_void_p, u32p, C.c_int32, C.c_int32, C.c_int32,
+                                        C.c_int32, C.c_int32, u32p, i32p, i64p]),
+            "or_verify": (C.c_int32, [C.c_void_p, C.c_void_p, u32p, C.c_int32, C.c_int32, C.c_uint32, u32p,
+                                      C.c_int32, u32p, i32p, f32p]),
+        }
+        for name, (res, args) in sig.items():
+            fn = getattr(l, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = l
+    return _lib
+
+
+def ptr(a: np.ndarray | None, t):
+    if a is None:
+        return C.cast(None, t)
+    assert a.flags["C_CONTIGUOUS"]
+    return a.ctypes.data_as(t)
+
+
+def config_struct(cfg) -> OrConfig:
+    return OrConfig(cfg.vocab, cfg.hidden, cfg.intermediate, cfg.layers, cfg.heads, cfg.kv_heads, cfg.head_dim,
+                    cfg.rms_eps, cfg.rope_theta, int(cfg.rope_llama3), cfg.rope_factor, cfg.rope_low_freq,
+                    cfg.rope_high_freq, cfg.rope_orig_max_pos, cfg.max_position, int(cfg.tie_embeddings),
+                    int(cfg.qkv_bias))
+
+
+def matrix_struct(m: Matrix) -> OrMatrix:
+    return OrMatrix(m.kind, m.rows, m.cols, 0, ptr(m.bf16, u16p), ptr(m.q, u8p), ptr(m.s, f32p))
+
+
+def threads(n: int) -> None:
+    lib().or_set_threads(n)
+
+
+class Model:
+    """An oracle copy of a HostModel (Model::forward on the CPU)."""
+
+    def __init__(self, hm: HostModel, _handle=None, _base=None):
+        self.cfg = hm.cfg
+        self._base = _base
+        if _handle is not None:
+            self.h = _handle
+            return
+        ls = (OrLayer * len(hm.layers))()
+        for i, l in enumerate(hm.layers):
+            ls[i] = OrLayer(ptr(l.attn_norm, f32p), matrix_struct(l.wqkv), ptr(l.bqkv, f32p), matrix_struct(l.wo),
+                            ptr(l.mlp_norm, f32p), matrix_struct(l.w_gate_up), matrix_struct(l.w_down))
+        cs = config_struct(hm.cfg)
+        self.h = lib().or_model_create(C.byref(cs), ls, ptr(hm.embed, u16p), ptr(hm.norm, f32p),
+                                       ptr(hm.lm_head, u16p))
+        if not self.h:
+            raise ValueError("oracle rejected the model (shape mismatch)")
+
+    def truncated(self, n: int) -> "Model":
+        from dataclasses import replace
+        h = lib().or_model_truncated(self.h, n)
+        m = Model.__new__(Model)
+        m.cfg = replace(self.cfg, layers=min(n, self.cfg.layers))
+        m.h = h
+        m._base = self
+        return m
+
+    def __del__(self):
+        if getattr(self, "h", None) and lib:
+            lib().or_model_destroy(self.h)
+            self.h = None
+
+    def kv(self, blocks: int, block_size: int = 16) -> "KvCache":
+        return KvCache(self.cfg, blocks, block_size)
+
+    def forward(self, kv: "KvCache", chunks, hidden: bool = False):
+        """chunks: list of (tokens, pos, blocks, logits_mode) with logits_mode
+        0 none, 1 last, 2 all. Returns logits [rows, vocab] (and the hidden
+        states [(layers+1), t, hidden] if asked)."""
+        arr = (OrChunk * len(chunks))()
+        keep = []
+        rows = 0
+        t = 0
+        for i, (tok, pos, blocks, mode) in enumerate(chunks):
+            tok = np.ascontiguousarray(tok, dtype=np.uint32)
+            blocks = np.ascontiguousarray(blocks, dtype=np.uint32)
+            keep += [tok, blocks]
+            arr[i] = OrChunk(ptr(tok, u32p), len(tok), pos, ptr(blocks, u32p), len(blocks), mode)
+            rows += len(tok) if mode == 2 else (1 if mode == 1 and len(tok) else 0)
+            t += len(tok)
+        logits = np.zeros((rows, self.cfg.vocab), dtype=np.float32)
+        hid = np.zeros((self.cfg.layers + 1, t, self.cfg.hidden), dtype=np.float32) if hidden else None
+        n = lib().or_forward(self.h, kv.h, arr, len(chunks), ptr(logits, f32p), ptr(hid, f32p))
+        if n < 0:
+            raise ValueError("chunk overruns its cache blocks")
+        return (logits, hid) if hidden else logits
+
+
+class KvCache:
+    def __init__(self, cfg, blocks: int, block_size: int = 16):
+        self.cfg = cfg
+        self.blocks = blocks
+        self.block_size = block_size
+        self.h = lib().or_kv_create(cfg.layers, cfg.kv_heads, cfg.head_dim, block_size, blocks)
+
+    def layer(self, i: int):
+        n = self.blocks * self.block_size * self.cfg.kv_heads * self.cfg.head_dim
+        k = np.zeros(n, np.float32)
+        v = np.zeros(n, np.float32)
+        lib().or_kv_read(self.h, i, ptr(k, f32p), ptr(v, f32p))
+        return k, v
+
+    def set_layer(self, i: int, k: np.ndarray, v: np.ndarray) -> None:
+        k = np.ascontiguousarray(k, np.float32)
+        v = np.ascontiguousarray(v, np.float32)
+        lib().or_kv_write_layer(self.h, i, ptr(k, f32p), ptr(v, f32p))
+
+    def __del__(self):
+        if getattr(self, "h", None):
+            lib().or_kv_destroy(self.h)
+            self.h = None
+
+
+def generate(target: Model, draft: Model | None, prompt, max_tokens: int, k: int, kv_blocks: int = 1024,
+             max_batch_tokens: int = 512):
+    """Greedy generation through the reference engine's speculative loop.
+    Returns (tokens, per-step accepted counts, (proposed, accepted, steps))."""
+    prompt = np.ascontiguousarray(prompt, dtype=np.uint32)
+    out = np.zeros(max_tokens, np.uint32)
+    acc = np.zeros(max_tokens, np.int32)
+    st = np.zeros(3, np.int64)
+    n = lib().or_generate(target.h, draft.h if draft else None, ptr(prompt, u32p), len(prompt), max_tokens, k,
+                          kv_blocks, max_batch_tokens, ptr(out, u32p), ptr(acc, i32p), ptr(st, i64p))
+    if n < 0:
+        raise RuntimeError("oracle generate failed")
+    return out[:n], acc[:int(st[2])], tuple(int(x) for x in st)
+
+
+def verify(target: Model, kv: KvCache, blocks, pos: int, last: int, drafts):
+    """One greedy verify step (returns emitted ids, accepted count, logits)."""
+    blocks = np.ascontiguousarray(blocks, dtype=np.uint32)
+    drafts = np.ascontiguousarray(drafts, dtype=np.uint32)
+    k = len(drafts)
+    out = np.zeros(k + 1, np.uint32)
+    acc = C.c_int32(0)
+    logits = np.zeros((k + 1, target.cfg.vocab), np.float32)
+    n = lib().or_verify(target.h, kv.h, ptr(blocks, u32p), len(blocks), pos, last, ptr(drafts, u32p), k,
+                        ptr(out, u32p), C.byref(acc), ptr(logits, f32p))
+    if n < 0:
+        raise RuntimeError("oracle verify failed")
+    return out[:n], acc.value, logits
+
+
+def quantize(kind: int, w: np.ndarray, importance: np.ndarray | None = None) -> Matrix:
+    rows, cols = w.shape
+    w = np.ascontiguousarray(w, dtype=np.float32)
+    bpk = 32 if kind == 1 else 16
+    q = np.zeros(rows // 32 * cols * bpk, np.uint8)
+    s = np.zeros(rows // 32 * (cols // 32) * 32, np.float32)
+    imp = None if importance is None else np.ascontiguousarray(importance, np.float32)
+    if lib().or_quantize(kind, rows, cols, ptr(w, f32p), ptr(imp, f32p), ptr(q, u8p), ptr(s, f32p)):
+        raise ValueError("bad shape for quantization")
+    return Matrix(kind, rows, cols, q=q, s=s)
+
+
+def matmul(w: Matrix, x: np.ndarray, bias: np.ndarray | None = None) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    m = x.shape[0]
+    y = np.zeros((m, w.rows), np.float32)
+    ms = matrix_struct(w)
+    if lib().or_matmul(C.byref(ms), ptr(x, f32p), m, ptr(bias, f32p), ptr(y, f32p)):
+        raise ValueError("bad matrix")
+    return y
+
+
+def exp(x: float) -> float:
+    return lib().or_exp(x)
+
+
+def argmax(v: np.ndarray) -> int:
+    v = np.ascontiguousarray(v, np.float32)
+    return int(lib().or_argmax(ptr(v, f32p), len(v)))

@@ -1,0 +1,968 @@
+/*
+ * CPU oracle for the ferrolm speculative-decoding verify path.
+ *
+ * TEST INFRASTRUCTURE ONLY: the parity checker for the HIP path and the
+ * timed CPU baseline. Not linked into, loaded by or called from the
+ * product library. See ferro_oracle.h for the contract.
+ *
+ * A restatement of the reference's CPU algorithm (Rust). Each definition
+ * names the reference function it follows as file:line in
+ * /root/reference. Compile with -ffp-contract=off: every fused
+ * multiply-add below is an explicit fmaf(), exactly where the reference
+ * uses mul_add or an FMA intrinsic, and nothing else is contracted.
+ *
+ * Storage differs from the reference where it does not change a single
+ * rounding: bf16 matrices are packed in 32-row panels in natural column
+ * order (the reference permutes columns inside a panel only so its SIMD
+ * unpack lands in order, src/kernels.rs:27-36); quantized matrices keep
+ * the reference's QMatrix layout byte for byte (src/quant.rs:70-76).
+ */
+#include "ferro_oracle.h"
+
+#include <math.h>
+#include <omp.h>
+#include <stdlib.h>
+#include <string.h>
+
+#define PANEL 32
+#define GROUP 32
+
+#if defined(__x86_64__)
+#define HOT __attribute__((target_clones("avx512f", "arch=haswell", "default")))
+#else
+#define HOT
+#endif
+
+/* ------------------------------------------------------------------ */
+/* rng: src/rng.rs:8-44 (xorshift64*, Box-Muller)                      */
+/* ------------------------------------------------------------------ */
+uint64_t or_rng_new(uint64_t seed) { return (seed * 0x9E3779B97F4A7C15ULL) | 1ULL; }
+
+uint64_t or_rng_next(uint64_t* s) {
+    *s ^= *s >> 12;
+    *s ^= *s << 25;
+    *s ^= *s >> 27;
+    return *s * 0x2545F4914F6CDD1DULL;
+}
+
+double or_rng_uniform(uint64_t* s) {
+    return (double)(or_rng_next(s) >> 11) / (double)(1ULL << 53);
+}
+
+double or_rng_normal(uint64_t* s) {
+    double u = 1.0 - or_rng_uniform(s);
+    double v = or_rng_uniform(s);
+    return sqrt(-2.0 * log(u)) * cos(6.283185307179586 * v);
+}
+
+/* ------------------------------------------------------------------ */
+/* bf16: src/safetensors.rs:166-178                                    */
+/* ------------------------------------------------------------------ */
+static inline float bf16f(uint16_t x) {
+    uint32_t b = (uint32_t)x << 16;
+    float f;
+    memcpy(&f, &b, 4);
+    return f;
+}
+
+float or_bf16_to_f32(uint16_t x) { return bf16f(x); }
+
+uint16_t or_f32_to_bf16(float x) {
+    uint32_t b;
+    memcpy(&b, &x, 4);
+    if (isnan(x)) return (uint16_t)((b >> 16) | 0x40);
+    uint32_t round = 0x7FFF + ((b >> 16) & 1);
+    return (uint16_t)((b + round) >> 16);
+}
+
+void or_set_threads(int32_t n) {
+    if (n > 0) omp_set_num_threads(n);
+}
+
+/* ------------------------------------------------------------------ */
+/* dot / hsum8: src/kernels.rs:191-213 (8 lanes, fixed lane sum)       */
+/* ------------------------------------------------------------------ */
+static inline float hsum8(const float* l) {
+    return ((l[0] + l[4]) + (l[2] + l[6])) + ((l[1] + l[5]) + (l[3] + l[7]));
+}
+
+float or_dot(const float* a, const float* b, int32_t n) {
+    float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    for (int32_t i = 0; i + 8 <= n; i += 8)
+        for (int l = 0; l < 8; l++) acc[l] = fmaf(a[i + l], b[i + l], acc[l]);
+    return hsum8(acc);
+}
+
+/* rms_norm: src/kernels.rs:597-607 */
+void or_rms_norm(const float* x, const float* w, int32_t dim, int32_t rows, float eps, float* out) {
+    for (int32_t r = 0; r < rows; r++) {
+        const float* xr = x + (size_t)r * dim;
+        float* o = out + (size_t)r * dim;
+        float ms = or_dot(xr, xr, dim) / (float)dim;
+        float rr = 1.0f / sqrtf(ms + eps);
+        for (int32_t i = 0; i < dim; i++) o[i] = w[i] * (xr[i] * rr);
+    }
+}
+
+/* exp: src/kernels.rs:609-637 (range reduction + Cephes polynomial) */
+static const float LOG2E = 1.44269504088896340736f;
+static const float LN2_HI = 0.6933594f;
+static const float LN2_LO = -2.1219444e-4f;
+static const float EXP_C[6] = {1.9875691e-4f, 1.3982e-3f, 8.333452e-3f,
+                               4.1665796e-2f, 0.16666665f, 0.5f};
+
+float or_exp(float x) {
+    /* f32::clamp: NaN passes through */
+    if (x < -87.0f) x = -87.0f;
+    if (x > 88.0f) x = 88.0f;
+    float n = rintf(x * LOG2E); /* round_ties_even in the default mode */
+    float r = fmaf(n, -LN2_LO, fmaf(n, -LN2_HI, x));
+    float p = EXP_C[0];
+    for (int i = 1; i < 6; i++) p = fmaf(p, r, EXP_C[i]);
+    float y = fmaf(p, r * r, r) + 1.0f;
+    int32_t e = ((int32_t)n + 127) << 23;
+    float scale;
+    memcpy(&scale, &e, 4);
+    return y * scale;
+}
+
+/* silu_mul: src/kernels.rs:650-663 */
+void or_silu_mul(const float* gate_up, int32_t inter, int32_t rows, float* out) {
+    for (int32_t r = 0; r < rows; r++) {
+        const float* g = gate_up + (size_t)r * 2 * inter;
+        const float* u = g + inter;
+        float* o = out + (size_t)r * inter;
+        for (int32_t i = 0; i < inter; i++) {
+            float e = or_exp(-g[i]);
+            o[i] = g[i] / (1.0f + e) * u[i];
+        }
+    }
+}
+
+/* argmax: src/sampler.rs:41-51 (first index of the maximum; NaN never wins) */
+uint32_t or_argmax(const float* v, int32_t n) {
+    int32_t best = 0;
+    for (int32_t i = 0; i < n; i++)
+        if (v[i] > v[best]) best = i;
+    return (uint32_t)best;
+}
+
+/* ------------------------------------------------------------------ */
+/* Matrices                                                            */
+/* ------------------------------------------------------------------ */
+typedef struct {
+    int32_t kind, rows, cols;
+    uint16_t* packed; /* bf16: [panel][k][32] */
+    uint8_t* q;       /* QMatrix codes, reference layout */
+    float* s;         /* QMatrix scales [panel][group][32] */
+    int owns;
+} omat;
+
+static int32_t bytes_per_k(int32_t kind) { return kind == OR_INT8 ? PANEL : PANEL / 2; }
+
+static int omat_init(omat* m, const or_matrix_desc* d) {
+    memset(m, 0, sizeof(*m));
+    m->kind = d->kind;
+    m->rows = d->rows;
+    m->cols = d->cols;
+    m->owns = 1;
+    if (d->rows % PANEL) return -1;
+    size_t rc = (size_t)d->rows * d->cols;
+    if (d->kind == OR_BF16) {
+        m->packed = (uint16_t*)malloc(rc * 2);
+        if (!m->packed) return -1;
+        int32_t K = d->cols;
+#pragma omp parallel for schedule(static)
+        for (int32_t r = 0; r < d->rows; r++) {
+            int32_t p = r / PANEL, c = r % PANEL;
+            const uint16_t* row = d->bf16 + (size_t)r * K;
+            uint16_t* dst = m->packed + (size_t)p * K * PANEL + c;
+            for (int32_t k = 0; k < K; k++) dst[(size_t)k * PANEL] = row[k];
+        }
+    } else {
+        if (d->cols % GROUP) return -1;
+        size_t qb = (size_t)d->rows / PANEL * d->cols * bytes_per_k(d->kind);
+        size_t sn = (size_t)d->rows / PANEL * (d->cols / GROUP) * PANEL;
+        m->q = (uint8_t*)malloc(qb);
+        m->s = (float*)malloc(sn * 4);
+        if (!m->q || !m->s) return -1;
+        memcpy(m->q, d->q, qb);
+        memcpy(m->s, d->s, sn * 4);
+    }
+    return 0;
+}
+
+static void omat_free(omat* m) {
+    if (!m->owns) return;
+    free(m->packed);
+    free(m->q);
+    free(m->s);
+    memset(m, 0, sizeof(*m));
+}
+
+/* Matrix::row_f32 / QMatrix::row_f32 (src/kernels.rs:121-130, src/quant.rs:145-168) */
+static int32_t qcode(const uint8_t* q, int32_t kind, int32_t cols, int32_t r, int32_t k) {
+    int32_t p = r / PANEL, c = r % PANEL;
+    size_t base = ((size_t)p * cols + k) * bytes_per_k(kind);
+    if (kind == OR_INT8) return (int32_t)(int8_t)q[base + c];
+    uint8_t b = q[base + c % 16];
+    return (int32_t)(c < 16 ? (b & 0x0F) : (b >> 4)) - 8;
+}
+
+static void omat_row_f32(const omat* m, int32_t r, float* out) {
+    if (m->kind == OR_BF16) {
+        int32_t p = r / PANEL, c = r % PANEL;
+        const uint16_t* panel = m->packed + (size_t)p * m->cols * PANEL;
+        for (int32_t k = 0; k < m->cols; k++) out[k] = bf16f(panel[(size_t)k * PANEL + c]);
+    } else {
+        int32_t G = m->cols / GROUP, p = r / PANEL, c = r % PANEL;
+        for (int32_t k = 0; k < m->cols; k++)
+            out[k] = (float)qcode(m->q, m->kind, m->cols, r, k) * m->s[((size_t)p * G + k / GROUP) * PANEL + c];
+    }
+}
+
+void or_dequantize(int32_t kind, int32_t rows, int32_t cols, const uint8_t* q, const float* s, float* out) {
+    int32_t G = cols / GROUP;
+#pragma omp parallel for schedule(static)
+    for (int32_t r = 0; r < rows; r++) {
+        int32_t p = r / PANEL, c = r % PANEL;
+        for (int32_t k = 0; k < cols; k++)
+            out[(size_t)r * cols + k] = (float)qcode(q, kind, cols, r, k) * s[((size_t)p * G + k / GROUP) * PANEL + c];
+    }
+}
+
+/* QMatrix::quantize: src/quant.rs:78-143 */
+static const float CLIPS8[6] = {1.0f, 0.98f, 0.96f, 0.94f, 0.92f, 0.9f};
+static const float CLIPS4[11] = {1.0f, 0.95f, 0.9f, 0.85f, 0.8f, 0.75f, 0.7f, 0.65f, 0.6f, 0.55f, 0.5f};
+
+int32_t or_quantize(int32_t kind, int32_t rows, int32_t cols, const float* w, const float* importance,
+                    uint8_t* q, float* s) {
+    if (kind == OR_BF16 || rows % PANEL || cols % GROUP) return -1;
+    int32_t groups = cols / GROUP, bpk = bytes_per_k(kind);
+    int32_t lo = kind == OR_INT8 ? -127 : -8, hi = kind == OR_INT8 ? 127 : 7;
+    const float* clips = kind == OR_INT8 ? CLIPS8 : CLIPS4;
+    int32_t nclips = kind == OR_INT8 ? 6 : 11;
+    memset(q, 0, (size_t)rows / PANEL * cols * bpk);
+    /* Panels are independent: each owns its bytes and scales. */
+#pragma omp parallel for schedule(dynamic)
+    for (int32_t p = 0; p < rows / PANEL; p++) {
+        int32_t codes[GROUP], best_codes[GROUP];
+        for (int32_t c = 0; c < PANEL; c++) {
+            int32_t r = p * PANEL + c;
+            for (int32_t g = 0; g < groups; g++) {
+                const float* vals = w + (size_t)r * cols + (size_t)g * GROUP;
+                const float* imp = importance ? importance + (size_t)g * GROUP : NULL;
+                float amax = 0.0f;
+                for (int i = 0; i < GROUP; i++) {
+                    float a = fabsf(vals[i]);
+                    amax = a > amax ? a : amax; /* f32::max, NaN ignored */
+                }
+                double best_err = INFINITY;
+                float best_scale = 0.0f;
+                if (amax > 0.0f) {
+                    for (int32_t ci = 0; ci < nclips; ci++) {
+                        float scale = clips[ci] * amax / (float)hi;
+                        double err = 0.0;
+                        for (int kk = 0; kk < GROUP; kk++) {
+                            float v = vals[kk];
+                            float t = roundf(v / scale); /* f32::round: half away from zero */
+                            int32_t code = (int32_t)t;   /* in range: |v/scale| <= 1/0.5*7 */
+                            if (code < lo) code = lo;
+                            if (code > hi) code = hi;
+                            codes[kk] = code;
+                            double d = (double)(v - (float)code * scale);
+                            err += d * d * (imp ? (double)imp[kk] : 1.0);
+                        }
+                        if (err < best_err) {
+                            best_err = err;
+                            best_scale = scale;
+                            memcpy(best_codes, codes, sizeof(codes));
+                        }
+                    }
+                } else {
+                    memset(best_codes, 0, sizeof(best_codes));
+                }
+                s[((size_t)p * groups + g) * PANEL + c] = best_scale;
+                for (int kk = 0; kk < GROUP; kk++) {
+                    int32_t k = g * GROUP + kk, code = best_codes[kk];
+                    size_t base = ((size_t)p * cols + k) * bpk;
+                    if (kind == OR_INT8) {
+                        q[base + c] = (uint8_t)(int8_t)code;
+                    } else {
+                        uint8_t nib = (uint8_t)(code + 8);
+                        if (c < 16)
+                            q[base + c] = (uint8_t)((q[base + c] & 0xF0) | nib);
+                        else
+                            q[base + c - 16] = (uint8_t)((q[base + c - 16] & 0x0F) | (nib << 4));
+                    }
+                }
+            }
+        }
+    }
+    return 0;
+}
+
+/* ------------------------------------------------------------------ */
+/* matmul: src/kernels.rs:244-376 (bf16) and src/quant.rs:175-304      */
+/* Every output is one chain from zero, in order over k (bf16), or per */
+/* group a chain over its 32 positions then fmaf(gs, scale, acc).      */
+/* ------------------------------------------------------------------ */
+HOT static void mm_bf16_panel(const float* x, int32_t m, int32_t K, const uint16_t* panel, float* y,
+                              int32_t n, int32_t p) {
+    int32_t i = 0;
+    for (; i + 4 <= m; i += 4) {
+        float a0[PANEL] = {0}, a1[PANEL] = {0}, a2[PANEL] = {0}, a3[PANEL] = {0};
+        const float *x0 = x + (size_t)i * K, *x1 = x0 + K, *x2 = x1 + K, *x3 = x2 + K;
+        for (int32_t k = 0; k < K; k++) {
+            const uint16_t* w = panel + (size_t)k * PANEL;
+            float wf[PANEL];
+            for (int c = 0; c < PANEL; c++) wf[c] = bf16f(w[c]);
+            float v0 = x0[k], v1 = x1[k], v2 = x2[k], v3 = x3[k];
+            for (int c = 0; c < PANEL; c++) {
+                a0[c] = fmaf(v0, wf[c], a0[c]);
+                a1[c] = fmaf(v1, wf[c], a1[c]);
+                a2[c] = fmaf(v2, wf[c], a2[c]);
+                a3[c] = fmaf(v3, wf[c], a3[c]);
+            }
+        }
+        memcpy(y + (size_t)(i + 0) * n + (size_t)p * PANEL, a0, sizeof(a0));
+        memcpy(y + (size_t)(i + 1) * n + (size_t)p * PANEL, a1, sizeof(a1));
+        memcpy(y + (size_t)(i + 2) * n + (size_t)p * PANEL, a2, sizeof(a2));
+        memcpy(y + (size_t)(i + 3) * n + (size_t)p * PANEL, a3, sizeof(a3));
+    }
+    for (; i < m; i++) {
+        float a0[PANEL] = {0};
+        const float* x0 = x + (size_t)i * K;
+        for (int32_t k = 0; k < K; k++) {
+            const uint16_t* w = panel + (size_t)k * PANEL;
+            float v0 = x0[k];
+            for (int c = 0; c < PANEL; c++) a0[c] = fmaf(v0, bf16f(w[c]), a0[c]);
+        }
+        memcpy(y + (size_t)i * n + (size_t)p * PANEL, a0, sizeof(a0));
+    }
+}
+
+static inline void load_codes(const uint8_t* q, int32_t kind, float* cf) {
+    if (kind == OR_INT8) {
+        for (int c = 0; c < PANEL; c++) cf[c] = (float)(int8_t)q[c];
+    } else {
+        for (int c = 0; c < 16; c++) {
+            cf[c] = (float)((int32_t)(q[c] & 0x0F) - 8);
+            cf[c + 16] = (float)((int32_t)(q[c] >> 4) - 8);
+        }
+    }
+}
+
+HOT static void mm_q_panel(const float* x, int32_t m, int32_t K, const uint8_t* qp, const float* sp,
+                           int32_t kind, float* y, int32_t n, int32_t p) {
+    int32_t bpk = bytes_per_k(kind), G = K / GROUP;
+    int32_t i = 0;
+    for (; i + 4 <= m; i += 4) {
+        float a0[PANEL] = {0}, a1[PANEL] = {0}, a2[PANEL] = {0}, a3[PANEL] = {0};
+        const float *x0 = x + (size_t)i * K, *x1 = x0 + K, *x2 = x1 + K, *x3 = x2 + K;
+        for (int32_t g = 0; g < G; g++) {
+            float g0[PANEL] = {0}, g1[PANEL] = {0}, g2[PANEL] = {0}, g3[PANEL] = {0};
+            for (int32_t kk = g * GROUP; kk < (g + 1) * GROUP; kk++) {
+                float cf[PANEL];
+                load_codes(qp + (size_t)kk * bpk, kind, cf);
+                float v0 = x0[kk], v1 = x1[kk], v2 = x2[kk], v3 = x3[kk];
+                for (int c = 0; c < PANEL; c++) {
+                    g0[c] = fmaf(v0, cf[c], g0[c]);
+                    g1[c] = fmaf(v1, cf[c], g1[c]);
+                    g2[c] = fmaf(v2, cf[c], g2[c]);
+                    g3[c] = fmaf(v3, cf[c], g3[c]);
+                }
+            }
+            const float* sc = sp + (size_t)g * PANEL;
+            for (int c = 0; c < PANEL; c++) {
+                a0[c] = fmaf(g0[c], sc[c], a0[c]);
+                a1[c] = fmaf(g1[c], sc[c], a1[c]);
+                a2[c] = fmaf(g2[c], sc[c], a2[c]);
+                a3[c] = fmaf(g3[c], sc[c], a3[c]);
+            }
+        }
+        memcpy(y + (size_t)(i + 0) * n + (size_t)p * PANEL, a0, sizeof(a0));
+        memcpy(y + (size_t)(i + 1) * n + (size_t)p * PANEL, a1, sizeof(a1));
+        memcpy(y + (size_t)(i + 2) * n + (size_t)p * PANEL, a2, sizeof(a2));
+        memcpy(y + (size_t)(i + 3) * n + (size_t)p * PANEL, a3, sizeof(a3));
+    }
+    for (; i < m; i++) {
+        float a0[PANEL] = {0};
+        const float* x0 = x + (size_t)i * K;
+        for (int32_t g = 0; g < G; g++) {
+            float g0[PANEL] = {0};
+            for (int32_t kk = g * GROUP; kk < (g + 1) * GROUP; kk++) {
+                float cf[PANEL];
+                load_codes(qp + (size_t)kk * bpk, kind, cf);
+                float v0 = x0[kk];
+                for (int c = 0; c < PANEL; c++) g0[c] = fmaf(v0, cf[c], g0[c]);
+            }
+            const float* sc = sp + (size_t)g * PANEL;
+            for (int c = 0; c < PANEL; c++) a0[c] = fmaf(g0[c], sc[c], a0[c]);
+        }
+        memcpy(y + (size_t)i * n + (size_t)p * PANEL, a0, sizeof(a0));
+    }
+    (void)G;
+}
+
+/* kernels::matmul: src/kernels.rs:249-275 (bias added after the chains) */
+static void omat_matmul(const omat* w, const float* x, int32_t m, const float* bias, float* y) {
+    int32_t n = w->rows, K = w->cols, panels = n / PANEL;
+    if (m == 0) return;
+#pragma omp parallel for schedule(dynamic, 1)
+    for (int32_t p = 0; p < panels; p++) {
+        if (w->kind == OR_BF16)
+            mm_bf16_panel(x, m, K, w->packed + (size_t)p * K * PANEL, y, n, p);
+        else
+            mm_q_panel(x, m, K, w->q + (size_t)p * K * bytes_per_k(w->kind),
+                       w->s + (size_t)p * (K / GROUP) * PANEL, w->kind, y, n, p);
+    }
+    if (bias)
+        for (int32_t i = 0; i < m; i++)
+            for (int32_t j = 0; j < n; j++) y[(size_t)i * n + j] += bias[j];
+}
+
+int32_t or_matmul(const or_matrix_desc* d, const float* x, int32_t m, const float* bias, float* y) {
+    omat w;
+    if (omat_init(&w, d)) {
+        omat_free(&w);
+        return -1;
+    }
+    omat_matmul(&w, x, m, bias, y);
+    omat_free(&w);
+    return 0;
+}
+
+/* ------------------------------------------------------------------ */
+/* Model                                                                */
+/* ------------------------------------------------------------------ */
+typedef struct {
+    float* attn_norm;
+    omat wqkv;
+    float* bqkv;
+    omat wo;
+    float* mlp_norm;
+    omat w_gate_up;
+    omat w_down;
+} olayer;
+
+struct or_model {
+    or_config cfg;
+    olayer* layers;
+    int32_t n_layers;
+    omat embed;
+    omat lm_head; /* kind -1 when tied */
+    float* norm;
+    float* inv_freq;
+    int owns;
+};
+
+static float* dup_f32(const float* p, size_t n) {
+    if (!p) return NULL;
+    float* d = (float*)malloc(n * 4);
+    memcpy(d, p, n * 4);
+    return d;
+}
+
+/* inv_freq: src/model.rs:461-492 (f32, powf, Llama 3 scaling) */
+static float* make_inv_freq(const or_config* c) {
+    int32_t dim = c->head_dim;
+    float* f = (float*)malloc((size_t)(dim / 2) * 4);
+    for (int32_t i = 0; i < dim / 2; i++) f[i] = 1.0f / powf(c->rope_theta, (float)(2 * i) / (float)dim);
+    if (c->rope_llama3) {
+        float old = (float)c->rope_orig_max_pos;
+        float low_wavelen = old / c->rope_low_freq;
+        float high_wavelen = old / c->rope_high_freq;
+        for (int32_t i = 0; i < dim / 2; i++) {
+            float fr = f[i];
+            float wavelen = 2.0f * 3.14159265358979323846f / fr;
+            if (wavelen < high_wavelen) {
+                f[i] = fr;
+            } else if (wavelen > low_wavelen) {
+                f[i] = fr / c->rope_factor;
+            } else {
+                float smooth = (old / wavelen - c->rope_low_freq) / (c->rope_high_freq - c->rope_low_freq);
+                f[i] = (1.0f - smooth) * fr / c->rope_factor + smooth * fr;
+            }
+        }
+    }
+    return f;
+}
+
+or_model* or_model_create(const or_config* cfg, const or_layer_desc* layers, const uint16_t* embed,
+                          const float* norm, const uint16_t* lm_head) {
+    or_model* m = (or_model*)calloc(1, sizeof(or_model));
+    m->cfg = *cfg;
+    m->owns = 1;
+    int32_t H = cfg->hidden, qkv = (cfg->heads + 2 * cfg->kv_heads) * cfg->head_dim;
+    m->n_layers = cfg->layers;
+    m->layers = (olayer*)calloc((size_t)cfg->layers, sizeof(olayer));
+    int bad = 0;
+    for (int32_t i = 0; i < cfg->layers; i++) {
+        const or_layer_desc* d = &layers[i];
+        olayer* l = &m->layers[i];
+        l->attn_norm = dup_f32(d->attn_norm, H);
+        l->mlp_norm = dup_f32(d->mlp_norm, H);
+        l->bqkv = cfg->qkv_bias ? dup_f32(d->bqkv, qkv) : NULL;
+        bad |= omat_init(&l->wqkv, &d->wqkv);
+        bad |= omat_init(&l->wo, &d->wo);
+        bad |= omat_init(&l->w_gate_up, &d->w_gate_up);
+        bad |= omat_init(&l->w_down, &d->w_down);
+        /* check_shapes: src/model.rs:243-261 */
+        bad |= l->wqkv.rows != qkv || l->wqkv.cols != H || l->wo.rows != H ||
+               l->wo.cols != cfg->heads * cfg->head_dim || l->w_gate_up.rows != 2 * cfg->intermediate ||
+               l->w_gate_up.cols != H || l->w_down.rows != H || l->w_down.cols != cfg->intermediate;
+    }
+    or_matrix_desc ed = {OR_BF16, cfg->vocab, H, 0, embed, NULL, NULL};
+    bad |= omat_init(&m->embed, &ed);
+    if (lm_head && !cfg->tie_embeddings) {
+        or_matrix_desc ld = {OR_BF16, cfg->vocab, H, 0, lm_head, NULL, NULL};
+        bad |= omat_init(&m->lm_head, &ld);
+    } else {
+        m->lm_head.kind = -1;
+    }
+    m->norm = dup_f32(norm, H);
+    m->inv_freq = make_inv_freq(cfg);
+    if (bad) {
+        or_model_destroy(m);
+        return NULL;
+    }
+    return m;
+}
+
+or_model* or_model_truncated(const or_model* base, int32_t layers) {
+    or_model* m = (or_model*)calloc(1, sizeof(or_model));
+    *m = *base;
+    m->owns = 0;
+    if (layers < m->n_layers) m->n_layers = layers;
+    m->cfg.layers = m->n_layers;
+    return m;
+}
+
+void or_model_destroy(or_model* m) {
+    if (!m) return;
+    if (m->owns) {
+        for (int32_t i = 0; i < m->cfg.layers; i++) {
+            olayer* l = &m->layers[i];
+            free(l->attn_norm);
+            free(l->mlp_norm);
+            free(l->bqkv);
+            omat_free(&l->wqkv);
+            omat_free(&l->wo);
+            omat_free(&l->w_gate_up);
+            omat_free(&l->w_down);
+        }
+        free(m->layers);
+        omat_free(&m->embed);
+        if (m->lm_head.kind >= 0) omat_free(&m->lm_head);
+        free(m->norm);
+        free(m->inv_freq);
+    }
+    free(m);
+}
+
+/* ------------------------------------------------------------------ */
+/* KvCache: src/kv.rs:23-71 ([layer][block][kv_head][offset][dim], f32) */
+/* ------------------------------------------------------------------ */
+struct or_kv {
+    int32_t layers, kv_heads, head_dim, block_size, blocks;
+    float** k;
+    float** v;
+};
+
+or_kv* or_kv_create(int32_t layers, int32_t kv_heads, int32_t head_dim, int32_t block_size, int32_t blocks) {
+    or_kv* kv = (or_kv*)calloc(1, sizeof(or_kv));
+    kv->layers = layers;
+    kv->kv_heads = kv_heads;
+    kv->head_dim = head_dim;
+    kv->block_size = block_size;
+    kv->blocks = blocks;
+    size_t n = (size_t)blocks * block_size * kv_heads * head_dim;
+    kv->k = (float**)calloc((size_t)layers, sizeof(float*));
+    kv->v = (float**)calloc((size_t)layers, sizeof(float*));
+    for (int32_t l = 0; l < layers; l++) {
+        kv->k[l] = (float*)calloc(n, 4);
+        kv->v[l] = (float*)calloc(n, 4);
+    }
+    return kv;
+}
+
+void or_kv_destroy(or_kv* kv) {
+    if (!kv) return;
+    for (int32_t l = 0; l < kv->layers; l++) {
+        free(kv->k[l]);
+        free(kv->v[l]);
+    }
+    free(kv->k);
+    free(kv->v);
+    free(kv);
+}
+
+static size_t kv_layer_floats(const or_kv* kv) {
+    return (size_t)kv->blocks * kv->block_size * kv->kv_heads * kv->head_dim;
+}
+
+int32_t or_kv_read(const or_kv* kv, int32_t layer, float* k_out, float* v_out) {
+    if (layer < 0 || layer >= kv->layers) return -1;
+    memcpy(k_out, kv->k[layer], kv_layer_floats(kv) * 4);
+    memcpy(v_out, kv->v[layer], kv_layer_floats(kv) * 4);
+    return 0;
+}
+
+int32_t or_kv_write_layer(or_kv* kv, int32_t layer, const float* k, const float* v) {
+    if (layer < 0 || layer >= kv->layers) return -1;
+    memcpy(kv->k[layer], k, kv_layer_floats(kv) * 4);
+    memcpy(kv->v[layer], v, kv_layer_floats(kv) * 4);
+    return 0;
+}
+
+/* KvCache::write: src/kv.rs:46-56 */
+static void kv_write(or_kv* kv, int32_t layer, size_t slot, const float* k, const float* v) {
+    int32_t bs = kv->block_size, hd = kv->head_dim, nkv = kv->kv_heads;
+    size_t b = slot / bs, o = slot % bs;
+    for (int32_t h = 0; h < nkv; h++) {
+        size_t at = ((b * nkv + h) * bs + o) * hd;
+        memcpy(kv->k[layer] + at, k + (size_t)h * hd, (size_t)hd * 4);
+        memcpy(kv->v[layer] + at, v + (size_t)h * hd, (size_t)hd * 4);
+    }
+}
+
+/* attend: src/kernels.rs:703-756 (scores by dot, softmax in position
+ * order, weighted values as an in-order fma chain) for the `heads` query
+ * heads sharing one kv head. */
+static void attend(const float* q, int32_t heads, int32_t hd, int32_t n, float scale, const float* K,
+                   const float* V, const uint32_t* blocks, int32_t bs, size_t block_stride, size_t head_off,
+                   float* scores, float* out) {
+    int32_t p = 0;
+    for (int32_t bi = 0; p < n; bi++) {
+        size_t base = (size_t)blocks[bi] * block_stride + head_off;
+        for (int32_t o = 0; o < bs && p < n; o++, p++) {
+            const float* kp = K + base + (size_t)o * hd;
+            for (int32_t j = 0; j < heads; j++) scores[(size_t)j * n + p] = or_dot(q + (size_t)j * hd, kp, hd) * scale;
+        }
+    }
+    for (int32_t j = 0; j < heads; j++) {
+        float* s = scores + (size_t)j * n;
+        float mx = -INFINITY;
+        for (int32_t i = 0; i < n; i++) mx = s[i] > mx ? s[i] : mx;
+        for (int32_t i = 0; i < n; i++) s[i] -= mx;
+        for (int32_t i = 0; i < n; i++) s[i] = or_exp(s[i]);
+        float sum = -0.0f;
+        for (int32_t i = 0; i < n; i++) sum += s[i];
+        for (int32_t i = 0; i < n; i++) s[i] /= sum;
+    }
+    memset(out, 0, (size_t)heads * hd * 4);
+    p = 0;
+    for (int32_t bi = 0; p < n; bi++) {
+        size_t base = (size_t)blocks[bi] * block_stride + head_off;
+        for (int32_t o = 0; o < bs && p < n; o++, p++) {
+            const float* vp = V + base + (size_t)o * hd;
+            for (int32_t j = 0; j < heads; j++) {
+                float w = scores[(size_t)j * n + p];
+                float* oj = out + (size_t)j * hd;
+                for (int32_t d = 0; d < hd; d++) oj[d] = fmaf(w, vp[d], oj[d]);
+            }
+        }
+    }
+}
+
+/* rope: src/model.rs:451-459 */
+static void rope(float* x, const float* cs, const float* sn, int32_t hd) {
+    int32_t half = hd / 2;
+    for (int32_t i = 0; i < half; i++) {
+        float a = x[i], b = x[i + half];
+        x[i] = a * cs[i] + -b * sn[i];
+        x[i + half] = b * cs[i] + a * sn[i];
+    }
+}
+
+/* Model::forward: src/model.rs:267-362 */
+int32_t or_forward(const or_model* m, or_kv* kv, const or_chunk* chunks, int32_t n_chunks, float* logits_out,
+                   float* hidden_out) {
+    const or_config* c = &m->cfg;
+    int32_t H = c->hidden, hd = c->head_dim, nh = c->heads, nkv = c->kv_heads, I = c->intermediate;
+    int32_t q_dim = nh * hd, qkv_dim = (nh + 2 * nkv) * hd, half = hd / 2;
+    int32_t bs = kv->block_size;
+    int32_t t = 0;
+    for (int32_t ci = 0; ci < n_chunks; ci++) t += chunks[ci].n;
+    if (t == 0) return 0;
+    int32_t* pos = (int32_t*)malloc((size_t)t * 4);
+    size_t* slot = (size_t*)malloc((size_t)t * sizeof(size_t));
+    int32_t* owner = (int32_t*)malloc((size_t)t * 4);
+    int32_t r = 0;
+    for (int32_t ci = 0; ci < n_chunks; ci++) {
+        const or_chunk* ch = &chunks[ci];
+        if ((int64_t)ch->n_blocks * bs < (int64_t)ch->pos + ch->n) {
+            free(pos);
+            free(slot);
+            free(owner);
+            return -1; /* "chunk overruns its cache blocks" */
+        }
+        for (int32_t i = 0; i < ch->n; i++, r++) {
+            int32_t p = ch->pos + i;
+            pos[r] = p;
+            slot[r] = (size_t)ch->blocks[p / bs] * bs + p % bs;
+            owner[r] = ci;
+        }
+    }
+    float* x = (float*)malloc((size_t)t * H * 4);
+    r = 0;
+    for (int32_t ci = 0; ci < n_chunks; ci++)
+        for (int32_t i = 0; i < chunks[ci].n; i++, r++) {
+            uint32_t tok = chunks[ci].tokens[i];
+            if ((int32_t)tok >= c->vocab) tok = 0; /* callers validate ids */
+            omat_row_f32(&m->embed, (int32_t)tok, x + (size_t)r * H);
+        }
+    if (hidden_out) memcpy(hidden_out, x, (size_t)t * H * 4);
+    /* rope_tables: src/model.rs:434-448 */
+    float* cs = (float*)malloc((size_t)t * half * 4);
+    float* sn = (float*)malloc((size_t)t * half * 4);
+    for (r = 0; r < t; r++)
+        for (int32_t i = 0; i < half; i++) {
+            float a = (float)pos[r] * m->inv_freq[i];
+            cs[(size_t)r * half + i] = cosf(a);
+            sn[(size_t)r * half + i] = sinf(a);
+        }
+    float* xn = (float*)malloc((size_t)t * H * 4);
+    float* qkv = (float*)malloc((size_t)t * qkv_dim * 4);
+    float* att = (float*)malloc((size_t)t * q_dim * 4);
+    float* proj = (float*)malloc((size_t)t * H * 4);
+    float* gate_up = (float*)malloc((size_t)t * 2 * I * 4);
+    float* act = (float*)malloc((size_t)t * I * 4);
+    int32_t group = nh / nkv;
+    float scale = 1.0f / sqrtf((float)hd);
+    size_t block_stride = (size_t)nkv * hd * bs;
+    int32_t maxn = 0;
+    for (r = 0; r < t; r++) maxn = pos[r] + 1 > maxn ? pos[r] + 1 : maxn;
+
+    for (int32_t li = 0; li < m->n_layers; li++) {
+        const olayer* l = &m->layers[li];
+        or_rms_norm(x, l->attn_norm, H, t, c->rms_eps, xn);
+        omat_matmul(&l->wqkv, xn, t, l->bqkv, qkv);
+        for (r = 0; r < t; r++) {
+            float* row = qkv + (size_t)r * qkv_dim;
+            for (int32_t h = 0; h < nh + nkv; h++) rope(row + (size_t)h * hd, cs + (size_t)r * half, sn + (size_t)r * half, hd);
+            kv_write(kv, li, slot[r], row + q_dim, row + q_dim + nkv * hd);
+        }
+        /* Model::attention: src/model.rs:394-432, one task per (row, kv head) */
+#pragma omp parallel
+        {
+            float* scores = (float*)malloc((size_t)group * maxn * 4);
+#pragma omp for schedule(dynamic, 1)
+            for (int32_t task = 0; task < t * nkv; task++) {
+                int32_t rr = task / nkv, g = task % nkv;
+                const or_chunk* ch = &chunks[owner[rr]];
+                attend(qkv + (size_t)rr * qkv_dim + (size_t)g * group * hd, group, hd, pos[rr] + 1, scale, kv->k[li],
+                       kv->v[li], ch->blocks, bs, block_stride, (size_t)g * bs * hd,
+                       scores, att + (size_t)rr * q_dim + (size_t)g * group * hd);
+            }
+            free(scores);
+        }
+        omat_matmul(&l->wo, att, t, NULL, proj);
+        for (size_t i = 0; i < (size_t)t * H; i++) x[i] += proj[i];
+        or_rms_norm(x, l->mlp_norm, H, t, c->rms_eps, xn);
+        omat_matmul(&l->w_gate_up, xn, t, NULL, gate_up);
+        or_silu_mul(gate_up, I, t, act);
+        omat_matmul(&l->w_down, act, t, NULL, proj);
+        for (size_t i = 0; i < (size_t)t * H; i++) x[i] += proj[i];
+        if (hidden_out) memcpy(hidden_out + (size_t)(li + 1) * t * H, x, (size_t)t * H * 4);
+    }
+
+    /* Only the requested rows go through the head: src/model.rs:338-361 */
+    int32_t* rows = (int32_t*)malloc((size_t)t * 4);
+    int32_t nr = 0;
+    r = 0;
+    for (int32_t ci = 0; ci < n_chunks; ci++) {
+        int32_t n = chunks[ci].n;
+        if (chunks[ci].logits == OR_LOGITS_LAST && n > 0) rows[nr++] = r + n - 1;
+        if (chunks[ci].logits == OR_LOGITS_ALL)
+            for (int32_t i = 0; i < n; i++) rows[nr++] = r + i;
+        r += n;
+    }
+    if (nr > 0 && logits_out) {
+        float* hsel = (float*)malloc((size_t)nr * H * 4);
+        for (int32_t i = 0; i < nr; i++)
+            or_rms_norm(x + (size_t)rows[i] * H, m->norm, H, 1, c->rms_eps, hsel + (size_t)i * H);
+        omat_matmul(m->lm_head.kind >= 0 ? &m->lm_head : &m->embed, hsel, nr, NULL, logits_out);
+        free(hsel);
+    }
+    free(rows);
+    free(pos);
+    free(slot);
+    free(owner);
+    free(x);
+    free(cs);
+    free(sn);
+    free(xn);
+    free(qkv);
+    free(att);
+    free(proj);
+    free(gate_up);
+    free(act);
+    return nr;
+}
+
+/* ------------------------------------------------------------------ */
+/* Greedy speculative decoding for one sequence                         */
+/* ------------------------------------------------------------------ */
+
+/* The target pass and greedy accept of Engine::execute
+ * (src/engine.rs:511-616, Logits::All branch, greedy). */
+int32_t or_verify(const or_model* target, or_kv* kv, const uint32_t* blocks, int32_t n_blocks, int32_t pos,
+                  uint32_t last, const uint32_t* drafts, int32_t k, uint32_t* out, int32_t* accepted,
+                  float* logits_out) {
+    int32_t V = target->cfg.vocab;
+    uint32_t* in = (uint32_t*)malloc((size_t)(k + 1) * 4);
+    in[0] = last;
+    for (int32_t j = 0; j < k; j++) in[j + 1] = drafts[j];
+    or_chunk ch = {in, k + 1, pos, blocks, n_blocks, OR_LOGITS_ALL};
+    float* logits = logits_out ? logits_out : (float*)malloc((size_t)(k + 1) * V * 4);
+    int32_t nr = or_forward(target, kv, &ch, 1, logits, NULL);
+    free(in);
+    if (nr != k + 1) {
+        if (!logits_out) free(logits);
+        return -1;
+    }
+    int32_t acc = 0, n = 0;
+    for (int32_t j = 0; j < k; j++) {
+        uint32_t tk = or_argmax(logits + (size_t)j * V, V);
+        if (tk == drafts[j]) {
+            out[n++] = drafts[j];
+            acc++;
+        } else {
+            out[n++] = tk;
+            break;
+        }
+    }
+    if (acc == k) out[n++] = or_argmax(logits + (size_t)k * V, V);
+    if (accepted) *accepted = acc;
+    if (!logits_out) free(logits);
+    return n;
+}
+
+typedef struct {
+    uint32_t* ids;
+    int32_t n, cap;
+} blist;
+
+static int blist_grow_to(blist* b, int32_t tokens, int32_t bs, int32_t* next_free, int32_t limit) {
+    while ((int64_t)b->n * bs < tokens) {
+        if (*next_free >= limit) return -1;
+        if (b->n == b->cap) {
+            b->cap = b->cap ? b->cap * 2 : 64;
+            b->ids = (uint32_t*)realloc(b->ids, (size_t)b->cap * 4);
+        }
+        b->ids[b->n++] = (uint32_t)(*next_free)++;
+    }
+    return 0;
+}
+
+int32_t or_generate(const or_model* target, const or_model* draft, const uint32_t* prompt, int32_t n_prompt,
+                    int32_t max_tokens, int32_t k, int32_t kv_blocks, int32_t max_batch_tokens, uint32_t* out,
+                    int32_t* accepted_out, int64_t* stats) {
+    const int32_t bs = 16, max_seqs = 64;
+    const or_config* c = &target->cfg;
+    if (!draft) k = 0;
+    int32_t max_len = c->max_position < kv_blocks * bs ? c->max_position : kv_blocks * bs;
+    if (n_prompt == 0 || n_prompt >= max_len) return -1; /* src/engine.rs:273-281 */
+    int32_t V = c->vocab;
+    int32_t cap = n_prompt + max_tokens + k + 2;
+    uint32_t* tokens = (uint32_t*)malloc((size_t)cap * 4);
+    memcpy(tokens, prompt, (size_t)n_prompt * 4);
+    int32_t len = n_prompt, computed = 0, draft_computed = 0, generated = 0, nsteps = 0;
+    int64_t proposed = 0, acc_total = 0, spec_steps = 0;
+    blist tb = {0}, db = {0};
+    int32_t t_free = 0, d_free = 0;
+    or_kv* tkv = or_kv_create(c->layers, c->kv_heads, c->head_dim, bs, kv_blocks);
+    or_kv* dkv = draft ? or_kv_create(draft->cfg.layers, draft->cfg.kv_heads, draft->cfg.head_dim, bs,
+                                      kv_blocks + max_seqs)
+                       : NULL;
+    float* logits = (float*)malloc((size_t)(k + 1) * V * 4);
+    uint32_t* drafts = (uint32_t*)malloc((size_t)(k + 1) * 4);
+    uint32_t emit[64];
+    int32_t rc = 0, done = 0;
+    while (!done) {
+        /* schedule: src/engine.rs:395-426 */
+        int32_t budget = max_batch_tokens;
+        int32_t left = len - computed;
+        int32_t decoding = left == 1;
+        int32_t spec = decoding && k > 0 && len + k < max_len && budget > k;
+        int32_t n = spec ? k + 1 : (left < budget ? left : budget);
+        if (blist_grow_to(&tb, computed + n, bs, &t_free, kv_blocks) ||
+            (spec && blist_grow_to(&db, len + k - 1, bs, &d_free, kv_blocks + max_seqs))) {
+            rc = -1; /* the single sequence cannot be preempted in favour of anything */
+            break;
+        }
+        int32_t ne = 0;
+        if (spec) {
+            /* propose: src/engine.rs:656-717 */
+            for (int32_t round = 0; round < k; round++) {
+                or_chunk ch;
+                uint32_t one;
+                if (round == 0) {
+                    ch = (or_chunk){tokens + draft_computed, len - draft_computed, draft_computed, db.ids, db.n,
+                                    OR_LOGITS_LAST};
+                } else {
+                    one = drafts[round - 1];
+                    ch = (or_chunk){&one, 1, len + round - 1, db.ids, db.n, OR_LOGITS_LAST};
+                }
+                if (or_forward(draft, dkv, &ch, 1, logits, NULL) != 1) {
+                    rc = -1;
+                    break;
+                }
+                if (round == 0) draft_computed = len;
+                drafts[round] = or_argmax(logits, V);
+            }
+            if (rc) break;
+            draft_computed = len + k - 1;
+            int32_t accepted = 0;
+            ne = or_verify(target, tkv, tb.ids, tb.n, computed, tokens[computed], drafts, k, emit, &accepted,
+                           logits);
+            if (ne < 0) {
+                rc = -1;
+                break;
+            }
+            proposed += k;
+            acc_total += accepted;
+            if (accepted_out && spec_steps < max_tokens) accepted_out[spec_steps] = accepted;
+            spec_steps++;
+            int32_t base = len;
+            computed = base + accepted;
+            if (draft_computed > base + accepted) draft_computed = base + accepted;
+        } else {
+            int32_t last = computed + n == len;
+            or_chunk ch = {tokens + computed, n, computed, tb.ids, tb.n, last ? OR_LOGITS_LAST : OR_LOGITS_NONE};
+            int32_t nr = or_forward(target, tkv, &ch, 1, logits, NULL);
+            if (nr < 0) {
+                rc = -1;
+                break;
+            }
+            computed += n;
+            if (last) emit[ne++] = or_argmax(logits, V);
+        }
+        /* token delivery: src/engine.rs:618-637 (ignore_eos, no stop ids) */
+        for (int32_t i = 0; i < ne; i++) {
+            tokens[len++] = emit[i];
+            out[generated++] = emit[i];
+            if (generated >= max_tokens || len >= max_len) {
+                done = 1;
+                break;
+            }
+        }
+        nsteps++;
+    }
+    if (stats) {
+        stats[0] = proposed;
+        stats[1] = acc_total;
+        stats[2] = spec_steps;
+    }
+    free(tokens);
+    free(tb.ids);
+    free(db.ids);
+    or_kv_destroy(tkv);
+    or_kv_destroy(dkv);
+    free(logits);
+    free(drafts);
+    (void)nsteps;
+    return rc ? -1 : generated;
+}
