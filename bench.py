@@ -1,0 +1,196 @@
+#!/usr/bin/env python3
+"""Benchmark of the greedy speculative-decoding verify path on one MI355X.
+
+Metric: accepted tok/s and verify-step microseconds for the
+SmolLM2-1.7B-shape int4-AWQ target with a SmolLM2-135M-shape bf16 draft,
+k=3, batch 1 (configuration 2: prompt of 1024 random ids). A "step" is one
+speculative step of the reference engine (src/engine.rs:499-717): k draft
+rounds, the target's verify pass over k+1 rows, greedy accept, rollback.
+
+Flow: build the synthetic models (random weights, seeded), upload them,
+prefill the prompt (untimed), run W warmup steps, then time exactly K steps
+(the API synchronises at every step, so the wall clock brackets finished
+device work). `value` = tokens emitted in the timed steps / their wall time
+(the reference's `generate` rate, src/main.rs:321-327). verify_step_us is
+the device time of the verify pass (HIP events, mean over the timed steps).
+
+roofline: GEMV launches are bracketed with HIP events (fg_profile) during
+a second pass over K steps from the same state; the dominant GEMV kernel
+class gives achieved = algorithmic bytes per launch / mean launch time.
+cpu_baseline: the C oracle (the reference's CPU algorithm restated) resumes
+from a copy of the GPU's KV state before the timed steps and runs as many
+spec steps as fit in --cpu-seconds on the host cores; its emitted tokens are
+compared with the GPU's from the same state.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+METRIC = "accepted tok/s + verify-step µs, 1.7B int4-AWQ target + 135M draft, k=3, bs=1"
+HBM_PEAK_GBS = 8000.0
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=64)
+    ap.add_argument("--warmup", type=int, default=8)
+    ap.add_argument("--config", type=int, default=2)
+    ap.add_argument("--seed", type=int, default=2024)
+    ap.add_argument("--cpu-seconds", type=float, default=20.0)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-profile", action="store_true")
+    a = ap.parse_args()
+    if a.gpus != 1:
+        print(f"bench.py measures one GPU only: this build has no multi-GPU path (--gpus {a.gpus} requested)",
+              file=sys.stderr)
+        return 2
+    from ferrolm_amd import gpu, spec, synth
+    from ferrolm_amd.weights import KIND_NAMES
+
+    t0 = time.time()
+    wl = synth.build(a.config, seed=a.seed)
+    log(f"built {wl.name} models in {time.time() - t0:.1f}s")
+    ctx = gpu.Context(0)
+    target = gpu.Model(ctx, wl.target)
+    draft = gpu.Model(ctx, wl.draft) if wl.draft is not None else target.truncated(wl.draft_layers)
+    log(f"uploaded: target {target.weight_bytes() / 1e9:.3f} GB, draft {draft.weight_bytes() / 1e9:.3f} GB")
+    cfg = wl.target.cfg
+    prompt = synth.prompt_ids(wl.prompt_len, cfg.vocab, a.seed)
+    k = wl.k
+    total_steps = a.warmup + 2 * a.steps
+    kv_blocks = (wl.prompt_len + total_steps * (k + 1) + 64) // 16 + 1
+    r = spec.Runner(ctx, target, draft, prompt, k, kv_blocks=kv_blocks)
+    t1 = time.time()
+    first = r.prefill()
+    log(f"prefill of {wl.prompt_len} tokens: {time.time() - t1:.2f}s, first token {first}")
+    for _ in range(a.warmup):
+        r.step()
+    log(f"warmup {a.warmup} steps done; context {len(r.tokens)}")
+
+    # Snapshot for the CPU baseline and the full-size parity check.
+    snap = None
+    if not a.no_cpu:
+        snap = dict(tokens=list(r.tokens), computed=r.computed, dcomp=r.dcomp, tb=list(r.tb), db=list(r.db),
+                    tkv=[r.tkv.layer(i) for i in range(cfg.layers)],
+                    dkv=[r.dkv.layer(i) for i in range(draft.cfg.layers)])
+    ctx_start = len(r.tokens)
+
+    # Timed region: exactly K steps.
+    st0 = len(r.stats.verify_us)
+    emitted = []
+    ctx.sync()
+    tt = time.perf_counter()
+    for _ in range(a.steps):
+        emitted.append(r.step())
+    ctx.sync()
+    elapsed = time.perf_counter() - tt
+    n_tok = sum(len(e) for e in emitted)
+    value = n_tok / elapsed
+    verify_us = float(np.mean(r.stats.verify_us[st0:]))
+    draft_us = float(np.mean(r.stats.draft_us[st0:]))
+    acc = r.stats.accepted_per_step[st0:]
+    acceptance = float(np.sum(acc)) / (k * len(acc)) if acc else 0.0
+    log(f"timed {a.steps} steps: {elapsed * 1e3:.1f} ms, {n_tok} tokens, {value:.1f} tok/s, "
+        f"verify {verify_us:.1f} us, draft {draft_us:.1f} us, acceptance {acceptance:.3f}")
+
+    roofline = None
+    if not a.no_profile:
+        gpu.profile(ctx, True)
+        gpu.profile_read(ctx, reset=True)
+        tp = time.perf_counter()
+        for _ in range(a.steps):
+            r.step()
+        ctx.sync()
+        prof_elapsed = time.perf_counter() - tp
+        recs = gpu.profile_read(ctx, reset=True)
+        gpu.profile(ctx, False)
+        for rec in recs:
+            log(f"gemv {rec['kind']} passes<={rec['passes']}: {rec['launches']} launches, "
+                f"{rec['us'] / rec['launches']:.2f} us avg, {rec['bytes'] / rec['us'] / 1e3:.0f} GB/s")
+        log(f"profiled pass: {prof_elapsed * 1e3:.1f} ms for {a.steps} steps "
+            f"(unprofiled {elapsed * 1e3:.1f} ms)")
+        tkind = KIND_NAMES[wl.target_kind]
+        dom = [x for x in recs if x["kind"] == tkind] or recs
+        dom = max(dom, key=lambda x: x["us"])
+        ach = dom["bytes"] / dom["us"] / 1e3
+        roofline = {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                    "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": None,
+                    "kernel": f"k_gemv {dom['kind']} (target projections, m={k + 1})",
+                    "bytes_per_launch": round(dom["bytes"] / dom["launches"]),
+                    "us_per_launch": round(dom["us"] / dom["launches"], 3), "launches": dom["launches"]}
+
+    cpu = None
+    parity = None
+    if snap is not None:
+        import oracle
+        ncores = len(os.sched_getaffinity(0))
+        threads = int(os.environ.get("OMP_NUM_THREADS", ncores))
+        oracle.threads(threads)
+        ot = oracle.Model(wl.target)
+        od = oracle.Model(wl.draft) if wl.draft is not None else ot.truncated(wl.draft_layers)
+        okv = ot.kv(kv_blocks)
+        odkv = od.kv(kv_blocks + 64)
+        for i, (kk, vv) in enumerate(snap["tkv"]):
+            okv.set_layer(i, kk, vv)
+        for i, (kk, vv) in enumerate(snap["dkv"]):
+            odkv.set_layer(i, kk, vv)
+        tokens = list(snap["tokens"])
+        comp, dcomp = snap["computed"], snap["dcomp"]
+        tb, db = list(snap["tb"]), list(snap["db"])
+        pool_t, pool_d = max(tb) + 1, max(db) + 1
+        cpu_emitted = []
+        tc = time.perf_counter()
+        while (time.perf_counter() - tc < a.cpu_seconds or len(cpu_emitted) < 2) and len(cpu_emitted) < a.steps:
+            while len(tb) * 16 < comp + k + 1:
+                tb.append(pool_t)
+                pool_t += 1
+            while len(db) * 16 < len(tokens) + k - 1:
+                db.append(pool_d)
+                pool_d += 1
+            out, _, comp, dcomp = oracle.spec_step(ot, okv, od, odkv, tokens, comp, dcomp, tb, db, k)
+            cpu_emitted.append([int(x) for x in out])
+            tokens.extend(int(x) for x in out)
+        cpu_elapsed = time.perf_counter() - tc
+        n_cpu = sum(len(e) for e in cpu_emitted)
+        cpu = {"value": round(n_cpu / cpu_elapsed, 3), "unit": "tok/s", "cores": threads, "kind": "port",
+               "sample": f"{len(cpu_emitted)} spec steps of {wl.name} from the GPU's KV state at context "
+                         f"{ctx_start} ({n_cpu} tokens, {cpu_elapsed:.1f}s), C oracle, {threads} threads",
+               "ms_per_step": round(cpu_elapsed / len(cpu_emitted) * 1e3, 2)}
+        gpu_first = emitted[:len(cpu_emitted)]
+        same = sum(1 for x, y in zip(gpu_first, cpu_emitted) if x == y)
+        parity = {"steps_compared": len(cpu_emitted), "steps_identical": same}
+        log(f"cpu baseline: {cpu['value']} tok/s ({cpu['ms_per_step']} ms/step); parity {same}/{len(cpu_emitted)}")
+
+    line = {
+        "metric": METRIC, "value": round(value, 2), "unit": "tok/s", "n_gpus": 1, "steps": a.steps,
+        "warmup": a.warmup, "ms_per_step": round(elapsed / a.steps * 1e3, 4), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": KIND_NAMES[wl.target_kind], "data": "synthetic",
+        "config": {"workload": f"{wl.name}: {'SmolLM2-1.7B' if a.config == 2 else cfg.hidden}-shape "
+                               f"{KIND_NAMES[wl.target_kind]} target + draft, k={k}, batch {wl.batch}, "
+                               f"prompt {wl.prompt_len} random ids",
+                   "target_layers": cfg.layers, "hidden": cfg.hidden, "k": k, "batch": wl.batch,
+                   "prompt": wl.prompt_len, "context_at_timed_start": ctx_start},
+        "verify_step_us": round(verify_us, 2), "draft_us": round(draft_us, 2), "acceptance": round(acceptance, 4),
+        "roofline": roofline, "cpu_baseline": cpu, "parity": parity,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -19,6 +19,7 @@ CSRC = PKG / "csrc"
 OBJ = PKG / "_build"
 LIB = PKG / "libferro_gpu.so"
 SOURCES = ["kernels.hip", "api.hip"]
+HOST_SOURCES = ["host.cpp"]  # plain C++ (g++), no contraction: exact load-time arithmetic
 ARCH = os.environ.get("FERRO_OFFLOAD_ARCH", "gfx950")
 
 
@@ -49,10 +50,20 @@ def build(verbose: bool = False) -> Path:
             print(r.stderr, file=sys.stderr)
         return out
 
-    with ThreadPoolExecutor(max_workers=len(SOURCES)) as ex:
-        objs = list(ex.map(compile_one, SOURCES))
+    def compile_host(src: str) -> Path:
+        out = OBJ / (Path(src).stem + ".o")
+        cmd = ["g++", "-O2", "-fPIC", "-std=c++17", "-ffp-contract=off", "-pthread", "-Wall",
+               f"-I{ROOT / 'include'}", "-c", str(CSRC / src), "-o", str(out)]
+        r = subprocess.run(cmd, capture_output=True, text=True)
+        if r.returncode != 0:
+            raise RuntimeError(f"g++ failed on {src}:\n{r.stderr}")
+        return out
+
+    with ThreadPoolExecutor(max_workers=len(SOURCES) + len(HOST_SOURCES)) as ex:
+        futs = [ex.submit(compile_one, s) for s in SOURCES] + [ex.submit(compile_host, s) for s in HOST_SOURCES]
+        objs = [f.result() for f in futs]
     tmp = LIB.with_suffix(".so.tmp")
-    cmd = [cc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs)]
+    cmd = [cc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-pthread", "-o", str(tmp), *map(str, objs)]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"link failed:\n{r.stderr}")

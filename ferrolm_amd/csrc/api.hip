@@ -82,7 +82,59 @@ struct fg_ctx {
     size_t hmeta_cap = 0;
     hipEvent_t ev[3] = {nullptr, nullptr, nullptr};
     float last_us[3] = {0, 0, 0};
+    // GEMV launch profiling (fg_profile)
+    bool prof = false;
+    std::vector<hipEvent_t> pev;
+    size_t pev_used = 0;
+    struct Pending {
+        int cls;
+        double bytes;
+        size_t ev;
+    };
+    std::vector<Pending> pending;
+    struct Rec {
+        int64_t n = 0;
+        double us = 0, bytes = 0;
+    };
+    Rec rec[12];
 };
+
+// Algorithmic bytes of one GEMV launch over m rows: codes + group scales
+// (or bf16 weights), f32 activations in, f32 products out.
+static double gemv_bytes(const DMat& d, int m) {
+    const double nk = (double)d.rows * d.cols;
+    double w = d.kind == BF16 ? nk * 2 : d.kind == INT8 ? nk + nk / 32 * 4 : nk / 2 + nk / 32 * 4;
+    return w + (double)m * d.cols * 4 + (double)m * d.rows * 4;
+}
+
+static hipEvent_t prof_event(fg_ctx* c) {
+    if (c->pev_used == c->pev.size()) {
+        hipEvent_t e;
+        if (hipEventCreate(&e) != hipSuccess) return nullptr;
+        c->pev.push_back(e);
+    }
+    return c->pev[c->pev_used++];
+}
+
+// launch_gemv with optional event bracketing.
+static void gemv(fg_ctx* c, const DMat& w, const Pieces& x, int m, const GemvPlan& gp, float* out) {
+    if (!c->prof) {
+        launch_gemv(c->stream, w, x, m, gp, out);
+        return;
+    }
+    const size_t i0 = c->pev_used;
+    hipEvent_t a = prof_event(c), b = prof_event(c);
+    if (!a || !b) {
+        launch_gemv(c->stream, w, x, m, gp, out);
+        return;
+    }
+    (void)hipEventRecord(a, c->stream);
+    launch_gemv(c->stream, w, x, m, gp, out);
+    (void)hipEventRecord(b, c->stream);
+    const int p_total = (m + 3) / 4;
+    const int pg = p_total == 1 ? 0 : p_total == 2 ? 1 : 2;
+    c->pending.push_back({w.kind * 4 + pg, gemv_bytes(w, m), i0});
+}
 
 struct DLayer {
     float* attn_norm = nullptr;
@@ -516,7 +568,7 @@ static int run_forward(fg_ctx* ctx, const fg_model* m, fg_kv* kv, const Plan& P,
         Pieces pa = pieces_for(w, l.wqkv.kb, passes);
         launch_pieces(st, kind_of(l.wqkv), w.x, H, t, H, l.attn_norm, w.rinv, pa);
         GemvPlan gp = plan_gemv(l.wqkv, t);
-        launch_gemv(st, l.wqkv, pa, t, gp, w.part);
+        gemv(ctx, l.wqkv, pa, t, gp, w.part);
         launch_rope_kv(st, w.part, gp.splits, t, l.bqkv, d_pos, d_slot, m->cos_t, m->sin_t, nh, nkv, hd,
                        kv->block_size, w.q, kc, vc);
         aa.kc = kc;
@@ -525,17 +577,17 @@ static int run_forward(fg_ctx* ctx, const fg_model* m, fg_kv* kv, const Plan& P,
         Pieces po = pieces_for(w, l.wo.kb, passes);
         launch_pieces(st, kind_of(l.wo), w.att, qd, t, qd, nullptr, nullptr, po);
         gp = plan_gemv(l.wo, t);
-        launch_gemv(st, l.wo, po, t, gp, w.part);
+        gemv(ctx, l.wo, po, t, gp, w.part);
         launch_residual_rms(st, w.x, w.part, gp.splits, t, H, c.rms_eps, w.rinv);
         // MLP block
         Pieces pg = pieces_for(w, l.w_gate_up.kb, passes);
         launch_pieces(st, kind_of(l.w_gate_up), w.x, H, t, H, l.mlp_norm, w.rinv, pg);
         gp = plan_gemv(l.w_gate_up, t);
-        launch_gemv(st, l.w_gate_up, pg, t, gp, w.part);
+        gemv(ctx, l.w_gate_up, pg, t, gp, w.part);
         Pieces pd = pieces_for(w, l.w_down.kb, passes);
         launch_silu_pieces(st, w.part, gp.splits, t, I, pd, nullptr, kind_of(l.w_down));
         gp = plan_gemv(l.w_down, t);
-        launch_gemv(st, l.w_down, pd, t, gp, w.part);
+        gemv(ctx, l.w_down, pd, t, gp, w.part);
         launch_residual_rms(st, w.x, w.part, gp.splits, t, H, c.rms_eps, w.rinv);
         if (hidden_host)
             HIPCHK(hipMemcpyAsync(hidden_host + (li + 1) * (size_t)t * H, w.x, (size_t)t * H * 4,
@@ -550,7 +602,7 @@ static int run_forward(fg_ctx* ctx, const fg_model* m, fg_kv* kv, const Plan& P,
     Pieces pl = pieces_for(w, m->lm_head.kb, sp);
     launch_pieces(st, kind_of(m->lm_head), w.hsel, H, P.S, H, m->norm, w.rsel, pl);
     const GemvPlan lp = plan_gemv(m->lm_head, P.S);
-    launch_gemv(st, m->lm_head, pl, P.S, lp, w.lpart);
+    gemv(ctx, m->lm_head, pl, P.S, lp, w.lpart);
     launch_argmax(st, w.lpart, lp.splits, P.S, c.vocab, logits_dev, w.best, w.nblk, am_out ? am_out : w.am, aux,
                   aux_stride, aux_off);
     HIPCHK(hipGetLastError());
@@ -590,6 +642,7 @@ void fg_ctx_destroy(fg_ctx* c) {
     if (c->hmeta) (void)hipHostFree(c->hmeta);
     for (auto& e : c->ev)
         if (e) (void)hipEventDestroy(e);
+    for (auto& e : c->pev) (void)hipEventDestroy(e);
     (void)hipStreamDestroy(c->stream);
     delete c;
 }
@@ -876,6 +929,42 @@ int fg_last_step_times(const fg_ctx* ctx, float* us3) {
     return 0;
 }
 
+int fg_profile(fg_ctx* ctx, int32_t on) {
+    if (!ctx) return fail(FG_E_ARG, "null ctx");
+    ctx->prof = on != 0;
+    return 0;
+}
+
+int fg_profile_read(fg_ctx* ctx, int32_t cap, int32_t* cls, int64_t* launches, double* us, double* bytes,
+                    int32_t reset) {
+    if (!ctx || cap < 0 || (cap > 0 && (!cls || !launches || !us || !bytes))) return fail(FG_E_ARG, "bad argument");
+    HIPCHK(hipStreamSynchronize(ctx->stream));
+    for (const auto& p : ctx->pending) {
+        float ms = 0;
+        HIPCHK(hipEventElapsedTime(&ms, ctx->pev[p.ev], ctx->pev[p.ev + 1]));
+        auto& r = ctx->rec[p.cls];
+        r.n++;
+        r.us += ms * 1000.0;
+        r.bytes += p.bytes;
+    }
+    ctx->pending.clear();
+    ctx->pev_used = 0;
+    int n = 0;
+    for (int i = 0; i < 12; i++) {
+        if (!ctx->rec[i].n) continue;
+        if (n < cap) {
+            cls[n] = i;
+            launches[n] = ctx->rec[i].n;
+            us[n] = ctx->rec[i].us;
+            bytes[n] = ctx->rec[i].bytes;
+        }
+        n++;
+    }
+    if (reset)
+        for (auto& r : ctx->rec) r = fg_ctx::Rec();
+    return n;
+}
+
 int fg_mat_upload(fg_ctx* ctx, const fg_matrix* w, fg_mat** out) {
     if (!ctx || !w || !out) return fail(FG_E_ARG, "null argument");
     HIPCHK(hipSetDevice(ctx->device));
@@ -949,7 +1038,7 @@ int fg_matmul_device(fg_ctx* ctx, const fg_mat* w, const float* x_dev, int32_t m
     if ((rc = ensure(&ctx->ws, &ctx->ws_cap, need, ctx->stream, false))) return rc;
     layout_mat(d, m, gp, p, &part, &xb, &yb, ctx->ws);
     launch_pieces(ctx->stream, d.kind, x_dev, d.cols, m, d.cols, nullptr, nullptr, p);
-    launch_gemv(ctx->stream, d, p, m, gp, part);
+    gemv(ctx, d, p, m, gp, part);
     launch_reduce(ctx->stream, part, gp.splits, m, d.rows, nullptr, y_dev);
     HIPCHK(hipGetLastError());
     return 0;

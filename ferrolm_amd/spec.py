@@ -4,8 +4,9 @@ A host-side mirror of the reference engine's single-sequence greedy loop
 (Engine::schedule/execute/propose, src/engine.rs:395-717): chunked prompt
 prefill under the token budget, then speculative steps of k draft proposals
 verified in one target pass, with the reference's rollback of the
-`computed` / `draft_computed` counters. The device does all model work
-(ferrolm_amd.gpu); this loop only does the reference's bookkeeping.
+`computed` / `draft_computed` counters (src/engine.rs:613-615). The device
+does all model work (ferrolm_amd.gpu); this loop only does the reference's
+bookkeeping.
 """
 from __future__ import annotations
 
@@ -23,7 +24,6 @@ class GenStats:
     accepted: int = 0
     spec_steps: int = 0
     accepted_per_step: list = field(default_factory=list)
-    token_times: list = field(default_factory=list)
     verify_us: list = field(default_factory=list)
     draft_us: list = field(default_factory=list)
 
@@ -45,39 +45,50 @@ class BlockPool:
         return True
 
 
-def generate(ctx: gpu.Context, target: gpu.Model, draft: gpu.Model | None, prompt, max_tokens: int, k: int,
-             kv_blocks: int = 1024, max_batch_tokens: int = 512, max_seqs: int = 64, tkv=None, dkv=None,
-             stats: GenStats | None = None):
-    """Returns the generated ids (the first from the prompt's prefill)."""
-    bs = 16
-    cfg = target.cfg
-    if draft is None:
-        k = 0
-    max_len = min(cfg.max_position, kv_blocks * bs)
-    prompt = [int(t) for t in prompt]
-    if not prompt or len(prompt) >= max_len:
-        raise ValueError(f"prompt of {len(prompt)} tokens; this server fits 1 to {max_len - 1}")
-    tkv = tkv or gpu.KvCache(ctx, cfg, kv_blocks)
-    if draft is not None:
-        dkv = dkv or gpu.KvCache(ctx, draft.cfg, kv_blocks + max_seqs)
-    tpool, dpool = BlockPool(kv_blocks), BlockPool(kv_blocks + max_seqs)
-    tb, db = [], []
-    tokens = list(prompt)
-    computed = dcomp = 0
-    out = []
-    st = stats or GenStats()
-    while True:
-        budget = max_batch_tokens
-        left = len(tokens) - computed
-        spec = left == 1 and k > 0 and len(tokens) + k < max_len and budget > k
-        n = k + 1 if spec else min(left, budget)
-        if not tpool.grow(tb, computed + n) or (spec and not dpool.grow(db, len(tokens) + k - 1)):
+class Runner:
+    """One request through the engine's greedy loop (ignore_eos)."""
+
+    def __init__(self, ctx: gpu.Context, target: gpu.Model, draft: gpu.Model | None, prompt, k: int,
+                 kv_blocks: int = 1024, max_batch_tokens: int = 512, max_seqs: int = 64, tkv=None, dkv=None):
+        self.ctx, self.target, self.draft = ctx, target, draft
+        self.k = k if draft is not None else 0
+        self.bs = 16
+        self.max_len = min(target.cfg.max_position, kv_blocks * self.bs)
+        self.budget = max_batch_tokens
+        prompt = [int(t) for t in prompt]
+        if not prompt or len(prompt) >= self.max_len:
+            raise ValueError(f"prompt of {len(prompt)} tokens; this server fits 1 to {self.max_len - 1}")
+        self.tkv = tkv or gpu.KvCache(ctx, target.cfg, kv_blocks)
+        self.dkv = None
+        if draft is not None:
+            self.dkv = dkv or gpu.KvCache(ctx, draft.cfg, kv_blocks + max_seqs)
+        self.tpool, self.dpool = BlockPool(kv_blocks), BlockPool(kv_blocks + max_seqs)
+        self.tb, self.db = [], []
+        self.tokens = list(prompt)
+        self.computed = 0
+        self.dcomp = 0
+        self.generated = []
+        self.stats = GenStats()
+
+    def decoding(self) -> bool:
+        return len(self.tokens) - self.computed == 1
+
+    def step(self) -> list:
+        """One engine step (src/engine.rs:374-393); returns the emitted ids."""
+        k = self.k
+        left = len(self.tokens) - self.computed
+        spec = left == 1 and k > 0 and len(self.tokens) + k < self.max_len and self.budget > k
+        n = k + 1 if spec else min(left, self.budget)
+        if not self.tpool.grow(self.tb, self.computed + n) or (
+                spec and not self.dpool.grow(self.db, len(self.tokens) + k - 1)):
             raise RuntimeError("out of cache blocks")
         if spec:
-            seq = gpu.SpecSeq(tail=np.array(tokens[dcomp:], np.uint32), draft_pos=dcomp, pos=computed,
-                              blocks=np.array(tb, np.uint32), draft_blocks=np.array(db, np.uint32))
-            toks, acc = gpu.spec_step(ctx, target, tkv, draft, dkv, [seq], k)
-            t_us = gpu.last_step_times(ctx)
+            seq = gpu.SpecSeq(tail=np.array(self.tokens[self.dcomp:], np.uint32), draft_pos=self.dcomp,
+                              pos=self.computed, blocks=np.array(self.tb, np.uint32),
+                              draft_blocks=np.array(self.db, np.uint32))
+            toks, acc = gpu.spec_step(self.ctx, self.target, self.tkv, self.draft, self.dkv, [seq], k)
+            t_us = gpu.last_step_times(self.ctx)
+            st = self.stats
             st.draft_us.append(float(t_us[0]))
             st.verify_us.append(float(t_us[1]))
             emitted = [int(x) for x in toks[0]]
@@ -86,19 +97,40 @@ def generate(ctx: gpu.Context, target: gpu.Model, draft: gpu.Model | None, promp
             st.accepted += a
             st.spec_steps += 1
             st.accepted_per_step.append(a)
-            base = len(tokens)
-            computed = base + a
-            dcomp = min(base + k - 1, base + a)
+            base = len(self.tokens)
+            self.computed = base + a
+            self.dcomp = min(base + k - 1, base + a)
         else:
-            last = computed + n == len(tokens)
-            o = gpu.forward(ctx, target, tkv, [(tokens[computed:computed + n], computed, tb,
-                                               gpu.LOGITS_LAST if last else gpu.LOGITS_NONE)], logits=False)
-            computed += n
+            last = self.computed + n == len(self.tokens)
+            o = gpu.forward(self.ctx, self.target, self.tkv,
+                            [(self.tokens[self.computed:self.computed + n], self.computed, self.tb,
+                              gpu.LOGITS_LAST if last else gpu.LOGITS_NONE)], logits=False)
+            self.computed += n
             emitted = [int(o.argmax[0])] if last else []
-        now = time.perf_counter()
+        out = []
         for t in emitted:
-            tokens.append(t)
+            if len(self.tokens) >= self.max_len:
+                break
+            self.tokens.append(t)
+            self.generated.append(t)
             out.append(t)
-            st.token_times.append(now)
-            if len(out) >= max_tokens or len(tokens) >= max_len:
-                return np.array(out, np.uint32)
+        return out
+
+    def prefill(self) -> list:
+        """Steps until the prompt is processed and the first token exists."""
+        out = []
+        while not out:
+            out = self.step()
+        return out
+
+
+def generate(ctx: gpu.Context, target: gpu.Model, draft: gpu.Model | None, prompt, max_tokens: int, k: int,
+             kv_blocks: int = 1024, max_batch_tokens: int = 512, stats: GenStats | None = None, **kw):
+    """The generated ids (the first from the prompt's prefill), stopping at
+    max_tokens or the context limit (src/engine.rs:633-636)."""
+    r = Runner(ctx, target, draft, prompt, k, kv_blocks, max_batch_tokens, **kw)
+    while len(r.generated) < max_tokens and len(r.tokens) < r.max_len:
+        r.step()
+    if stats is not None:
+        stats.__dict__.update(r.stats.__dict__)
+    return np.array(r.generated[:max_tokens], np.uint32)

@@ -99,6 +99,8 @@ def lib():
             "or_forward": (C.c_int32, [C.c_void_p, C.c_void_p, C.POINTER(OrChunk), C.c_int32, f32p, f32p]),
             "or_generate": (C.c_int32, [C.c_void_p, C.c_void_p, u32p, C.c_int32, C.c_int32, C.c_int32,
                                         C.c_int32, C.c_int32, u32p, i32p, i64p]),
+            "or_spec_step": (C.c_int32, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, u32p, C.c_int32, i32p,
+                                         i32p, u32p, C.c_int32, u32p, C.c_int32, C.c_int32, u32p, i32p]),
             "or_verify": (C.c_int32, [C.c_void_p, C.c_void_p, u32p, C.c_int32, C.c_int32, C.c_uint32, u32p,
                                       C.c_int32, u32p, i32p, f32p]),
         }
@@ -244,6 +246,25 @@ def verify(target: Model, kv: KvCache, blocks, pos: int, last: int, drafts):
     if n < 0:
         raise RuntimeError("oracle verify failed")
     return out[:n], acc.value, logits
+
+
+def spec_step(target: Model, tkv: KvCache, draft: Model, dkv: KvCache, tokens, computed: int, draft_computed: int,
+              blocks, draft_blocks, k: int):
+    """One greedy speculative step from an existing state. Returns
+    (emitted ids, accepted, computed, draft_computed)."""
+    tokens = np.ascontiguousarray(tokens, dtype=np.uint32)
+    blocks = np.ascontiguousarray(blocks, dtype=np.uint32)
+    draft_blocks = np.ascontiguousarray(draft_blocks, dtype=np.uint32)
+    out = np.zeros(k + 1, np.uint32)
+    acc = C.c_int32(0)
+    c = C.c_int32(computed)
+    dc = C.c_int32(draft_computed)
+    n = lib().or_spec_step(target.h, tkv.h, draft.h, dkv.h, ptr(tokens, u32p), len(tokens), C.byref(c), C.byref(dc),
+                           ptr(blocks, u32p), len(blocks), ptr(draft_blocks, u32p), len(draft_blocks), k,
+                           ptr(out, u32p), C.byref(acc))
+    if n < 0:
+        raise RuntimeError("oracle spec step failed")
+    return out[:n], acc.value, c.value, dc.value
 
 
 def quantize(kind: int, w: np.ndarray, importance: np.ndarray | None = None) -> Matrix:

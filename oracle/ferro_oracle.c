@@ -840,6 +840,46 @@ int32_t or_verify(const or_model* target, or_kv* kv, const uint32_t* blocks, int
     return n;
 }
 
+int32_t or_spec_step(const or_model* target, or_kv* tkv, const or_model* draft, or_kv* dkv, const uint32_t* tokens,
+                     int32_t len, int32_t* computed, int32_t* draft_computed, const uint32_t* blocks, int32_t n_blocks,
+                     const uint32_t* draft_blocks, int32_t n_draft_blocks, int32_t k, uint32_t* out,
+                     int32_t* accepted) {
+    int32_t V = target->cfg.vocab;
+    if (k <= 0 || *computed != len - 1 || *draft_computed > len - 1) return -1;
+    float* logits = (float*)malloc((size_t)V * 4);
+    uint32_t* drafts = (uint32_t*)malloc((size_t)k * 4);
+    int32_t dc = *draft_computed;
+    /* propose: src/engine.rs:656-717 */
+    for (int32_t round = 0; round < k; round++) {
+        or_chunk ch;
+        uint32_t one;
+        if (round == 0) {
+            ch = (or_chunk){tokens + dc, len - dc, dc, draft_blocks, n_draft_blocks, OR_LOGITS_LAST};
+        } else {
+            one = drafts[round - 1];
+            ch = (or_chunk){&one, 1, len + round - 1, draft_blocks, n_draft_blocks, OR_LOGITS_LAST};
+        }
+        if (or_forward(draft, dkv, &ch, 1, logits, NULL) != 1) {
+            free(logits);
+            free(drafts);
+            return -1;
+        }
+        if (round == 0) dc = len;
+        drafts[round] = or_argmax(logits, V);
+    }
+    free(logits);
+    dc = len + k - 1;
+    int32_t acc = 0;
+    int32_t ne = or_verify(target, tkv, blocks, n_blocks, *computed, tokens[*computed], drafts, k, out, &acc, NULL);
+    free(drafts);
+    if (ne < 0) return -1;
+    /* rollback: src/engine.rs:613-615 */
+    *computed = len + acc;
+    *draft_computed = dc < len + acc ? dc : len + acc;
+    if (accepted) *accepted = acc;
+    return ne;
+}
+
 typedef struct {
     uint32_t* ids;
     int32_t n, cap;
@@ -877,8 +917,7 @@ int32_t or_generate(const or_model* target, const or_model* draft, const uint32_
     or_kv* dkv = draft ? or_kv_create(draft->cfg.layers, draft->cfg.kv_heads, draft->cfg.head_dim, bs,
                                       kv_blocks + max_seqs)
                        : NULL;
-    float* logits = (float*)malloc((size_t)(k + 1) * V * 4);
-    uint32_t* drafts = (uint32_t*)malloc((size_t)(k + 1) * 4);
+    float* logits = (float*)malloc((size_t)V * 4);
     uint32_t emit[64];
     int32_t rc = 0, done = 0;
     while (!done) {
@@ -895,29 +934,9 @@ int32_t or_generate(const or_model* target, const or_model* draft, const uint32_
         }
         int32_t ne = 0;
         if (spec) {
-            /* propose: src/engine.rs:656-717 */
-            for (int32_t round = 0; round < k; round++) {
-                or_chunk ch;
-                uint32_t one;
-                if (round == 0) {
-                    ch = (or_chunk){tokens + draft_computed, len - draft_computed, draft_computed, db.ids, db.n,
-                                    OR_LOGITS_LAST};
-                } else {
-                    one = drafts[round - 1];
-                    ch = (or_chunk){&one, 1, len + round - 1, db.ids, db.n, OR_LOGITS_LAST};
-                }
-                if (or_forward(draft, dkv, &ch, 1, logits, NULL) != 1) {
-                    rc = -1;
-                    break;
-                }
-                if (round == 0) draft_computed = len;
-                drafts[round] = or_argmax(logits, V);
-            }
-            if (rc) break;
-            draft_computed = len + k - 1;
             int32_t accepted = 0;
-            ne = or_verify(target, tkv, tb.ids, tb.n, computed, tokens[computed], drafts, k, emit, &accepted,
-                           logits);
+            ne = or_spec_step(target, tkv, draft, dkv, tokens, len, &computed, &draft_computed, tb.ids, tb.n,
+                              db.ids, db.n, k, emit, &accepted);
             if (ne < 0) {
                 rc = -1;
                 break;
@@ -926,9 +945,6 @@ int32_t or_generate(const or_model* target, const or_model* draft, const uint32_
             acc_total += accepted;
             if (accepted_out && spec_steps < max_tokens) accepted_out[spec_steps] = accepted;
             spec_steps++;
-            int32_t base = len;
-            computed = base + accepted;
-            if (draft_computed > base + accepted) draft_computed = base + accepted;
         } else {
             int32_t last = computed + n == len;
             or_chunk ch = {tokens + computed, n, computed, tb.ids, tb.n, last ? OR_LOGITS_LAST : OR_LOGITS_NONE};
@@ -962,7 +978,6 @@ int32_t or_generate(const or_model* target, const or_model* draft, const uint32_
     or_kv_destroy(tkv);
     or_kv_destroy(dkv);
     free(logits);
-    free(drafts);
     (void)nsteps;
     return rc ? -1 : generated;
 }

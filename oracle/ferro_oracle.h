@@ -140,6 +140,19 @@ int32_t or_verify(const or_model* target, or_kv* kv, const uint32_t* blocks,
                   const uint32_t* drafts, int32_t k, uint32_t* out,
                   int32_t* accepted, float* logits_out);
 
+/* One greedy speculative step of the reference engine for one sequence
+ * from an existing state (Engine::propose + the verify pass + accept,
+ * src/engine.rs:499-717): tokens[0..len) is the sequence, *computed ==
+ * len - 1, *draft_computed <= len - 1; both caches must already hold the
+ * positions below those counters and the block tables must cover len + k
+ * (target) and len + k - 1 (draft) slots. Writes the emitted ids to out
+ * (<= k+1), updates the counters as the reference does and returns the
+ * emitted count (or -1). */
+int32_t or_spec_step(const or_model* target, or_kv* tkv, const or_model* draft, or_kv* dkv,
+                     const uint32_t* tokens, int32_t len, int32_t* computed, int32_t* draft_computed,
+                     const uint32_t* blocks, int32_t n_blocks, const uint32_t* draft_blocks,
+                     int32_t n_draft_blocks, int32_t k, uint32_t* out, int32_t* accepted);
+
 #ifdef __cplusplus
 }
 #endif
