@@ -75,9 +75,8 @@ uint16_t or_f32_to_bf16(float x) {
     return (uint16_t)((b + round) >> 16);
 }
 
-void or_set_threads(int32_t n) {
-    if (n > 0) omp_set_num_threads(n);
-}
+/* n > 0: use n threads; n <= 0: all available processors. */
+void or_set_threads(int32_t n) { omp_set_num_threads(n > 0 ? n : omp_get_num_procs()); }
 
 /* ------------------------------------------------------------------ */
 /* dot / hsum8: src/kernels.rs:191-213 (8 lanes, fixed lane sum)       */
