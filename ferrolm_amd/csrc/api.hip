@@ -6,6 +6,8 @@
 #include "internal.h"
 
 #include <algorithm>
+#include <cstdlib>
+#include <functional>
 #include <cmath>
 #include <cstring>
 #include <string>
@@ -29,8 +31,6 @@ int fail(int code, const std::string& msg) {
         if (e_ != hipSuccess) return fail(FG_E_DEVICE, std::string(#x) + ": " + hipGetErrorString(e_)); \
     } while (0)
 
-constexpr int ATT_QMAX = 64;   // queries per attention work item (k_attn)
-constexpr int SPLIT_POS = 128; // context positions per attention work item
 
 template <class F>
 void parallel_for(int n, F f) {
@@ -97,7 +97,36 @@ struct fg_ctx {
         double us = 0, bytes = 0;
     };
     Rec rec[12];
+    // HIP graphs of the speculative step (draft rounds, verify pass), reused
+    // while the launch shapes stay the same.
+    struct ProfItem {
+        int cls;
+        double bytes;
+        hipEvent_t a, b;
+    };
+    bool capturing = false;
+    std::vector<ProfItem> capture_prof;
+    struct GraphSet {
+        std::vector<int64_t> sig;
+        hipGraphExec_t exec[2] = {nullptr, nullptr};
+        std::vector<ProfItem> prof;
+    } gs;
+    bool graphs = true;
 };
+
+static void drop_graphs(fg_ctx* c) {
+    for (auto& e : c->gs.exec)
+        if (e) {
+            (void)hipGraphExecDestroy(e);
+            e = nullptr;
+        }
+    for (auto& p : c->gs.prof) {
+        (void)hipEventDestroy(p.a);
+        (void)hipEventDestroy(p.b);
+    }
+    c->gs.prof.clear();
+    c->gs.sig.clear();
+}
 
 // Algorithmic bytes of one GEMV launch over m rows: codes + group scales
 // (or bf16 weights), f32 activations in, f32 products out.
@@ -116,24 +145,22 @@ static hipEvent_t prof_event(fg_ctx* c) {
     return c->pev[c->pev_used++];
 }
 
-// launch_gemv with optional event bracketing.
-static void gemv(fg_ctx* c, const DMat& w, const Pieces& x, int m, const GemvPlan& gp, float* out) {
-    if (!c->prof) {
-        launch_gemv(c->stream, w, x, m, gp, out);
+// launch_gemv, timed by its own dispatch while profiling (fg_profile). The
+// speculative step launches directly (no graph) while profiling is on.
+static void gemv(fg_ctx* c, int epi, const DMat& w, const GemvArgs& a) {
+    if (!c->prof || c->capturing) {
+        launch_gemv(c->stream, epi, w, a);
         return;
     }
+    const int pg = a.p_total == 1 ? 0 : a.p_total == 2 ? 1 : 2;
     const size_t i0 = c->pev_used;
-    hipEvent_t a = prof_event(c), b = prof_event(c);
-    if (!a || !b) {
-        launch_gemv(c->stream, w, x, m, gp, out);
+    hipEvent_t e0 = prof_event(c), e1 = prof_event(c);
+    if (!e0 || !e1) {
+        launch_gemv(c->stream, epi, w, a);
         return;
     }
-    (void)hipEventRecord(a, c->stream);
-    launch_gemv(c->stream, w, x, m, gp, out);
-    (void)hipEventRecord(b, c->stream);
-    const int p_total = (m + 3) / 4;
-    const int pg = p_total == 1 ? 0 : p_total == 2 ? 1 : 2;
-    c->pending.push_back({w.kind * 4 + pg, gemv_bytes(w, m), i0});
+    launch_gemv(c->stream, epi, w, a, e0, e1);
+    c->pending.push_back({w.kind * 4 + pg, gemv_bytes(w, a.m), i0});
 }
 
 struct DLayer {
@@ -203,7 +230,15 @@ static inline int qcode(const uint8_t* q, int kind, int K, int r, int k) {
     return (c < 16 ? (b & 15) : (b >> 4)) - 8;
 }
 
-static int repack(const fg_matrix& src, DMat& d, std::vector<uint8_t>& w, std::vector<float>& s) {
+// Device row r of the gate/up matrix (interleaved in blocks of 32, see
+// internal.h) and the source row it holds.
+static inline int src_row(int r, int inter) {
+    if (inter <= 0) return r;
+    const int blk = r / 64, within = r % 64;
+    return within < 32 ? blk * 32 + within : inter + blk * 32 + within - 32;
+}
+
+static int repack(const fg_matrix& src, DMat& d, std::vector<uint8_t>& w, std::vector<float>& s, int inter) {
     if (src.rows <= 0 || src.cols <= 0 || src.rows % 32 || (src.format != FG_BF16 && src.cols % 32))
         return fail(FG_E_SHAPE, "matrix rows must be a multiple of 32 (and cols of 32 when quantized)");
     if (src.format == FG_BF16 && !src.bf16) return fail(FG_E_ARG, "bf16 matrix without data");
@@ -223,7 +258,7 @@ static int repack(const fg_matrix& src, DMat& d, std::vector<uint8_t>& w, std::v
         parallel_for(d.n_tiles, [&](int t) {
             for (int kb = 0; kb < KB; kb++)
                 for (int l = 0; l < 64; l++) {
-                    const int n = t * 16 + l % 16, k0 = kb * 32 + 8 * (l / 16);
+                    const int n = src_row(t * 16 + l % 16, inter), k0 = kb * 32 + 8 * (l / 16);
                     uint16_t* o = out + (((size_t)t * KB + kb) * 64 + l) * 8;
                     for (int sl = 0; sl < 8; sl++) o[sl] = k0 + sl < K ? src.bf16[(size_t)n * K + k0 + sl] : 0;
                 }
@@ -238,7 +273,7 @@ static int repack(const fg_matrix& src, DMat& d, std::vector<uint8_t>& w, std::v
     parallel_for(d.n_tiles, [&](int t) {
         for (int kb = 0; kb < G; kb++)
             for (int r = 0; r < 16; r++) {
-                const int n = t * 16 + r, p = n / 32, c = n % 32;
+                const int n = src_row(t * 16 + r, inter), p = n / 32, c = n % 32;
                 float v = src.s[((size_t)p * G + kb) * 32 + c];
                 if (q4) v *= 0.0625f;
                 s[(((size_t)t * KC + kb / 4) * 16 + r) * 4 + kb % 4] = v;
@@ -250,7 +285,7 @@ static int repack(const fg_matrix& src, DMat& d, std::vector<uint8_t>& w, std::v
         parallel_for(d.n_tiles, [&](int t) {
             for (int kb = 0; kb < G; kb++)
                 for (int l = 0; l < 64; l++) {
-                    const int n = t * 16 + l % 16, k0 = kb * 32 + 8 * (l / 16);
+                    const int n = src_row(t * 16 + l % 16, inter), k0 = kb * 32 + 8 * (l / 16);
                     uint32_t word = 0;
                     for (int sl = 0; sl < 8; sl++) {
                         const int code = qcode(src.q, INT4, K, n, k0 + sl);
@@ -266,7 +301,7 @@ static int repack(const fg_matrix& src, DMat& d, std::vector<uint8_t>& w, std::v
         parallel_for(d.n_tiles, [&](int t) {
             for (int kb = 0; kb < G; kb++)
                 for (int l = 0; l < 64; l++) {
-                    const int n = t * 16 + l % 16, k0 = kb * 32 + 8 * (l / 16);
+                    const int n = src_row(t * 16 + l % 16, inter), k0 = kb * 32 + 8 * (l / 16);
                     int8_t* o = out + (((size_t)t * (KB / 2) + kb / 2) * 64 + l) * 16 + (kb % 2) * 8;
                     for (int sl = 0; sl < 8; sl++) o[sl] = (int8_t)qcode(src.q, INT8, K, n, k0 + sl);
                 }
@@ -275,10 +310,12 @@ static int repack(const fg_matrix& src, DMat& d, std::vector<uint8_t>& w, std::v
     return 0;
 }
 
-static int upload_mat(const fg_matrix& src, DMat& d, std::vector<void*>* allocs) {
+static int upload_mat(const fg_matrix& src, DMat& d, std::vector<void*>* allocs, int inter = 0) {
     std::vector<uint8_t> w;
     std::vector<float> s;
-    int rc = repack(src, d, w, s);
+    if (inter > 0 && (inter % 32 || src.rows != 2 * inter))
+        return fail(FG_E_SHAPE, "intermediate size must be a multiple of 32");
+    int rc = repack(src, d, w, s, inter);
     if (rc) return rc;
     d.w_bytes = w.size();
     d.s_bytes = s.size() * 4;
@@ -349,18 +386,20 @@ struct ChunkIn {
 
 struct Plan {
     int t = 0, S = 0, G = 0, W = 0, T = 0;
-    std::vector<int32_t> pos, slot, row_group, g_row0, g_nrows, g_table, g_wi0, g_nsplit, wi_group, wi_split, sel;
+    std::vector<int32_t> pos, slot, row_group, g_row0, g_nrows, g_table, g_wi0, g_nsplit, g_crow0, g_cpos0, wi_group,
+        wi_split, sel;
     std::vector<uint32_t> tables, tokens;
     bool host_tokens = true;
     // offsets (in int32 words) of each array inside the packed metadata
-    size_t o_pos, o_slot, o_rg, o_grow0, o_gnrows, o_gtable, o_gwi0, o_gnsplit, o_wig, o_wis, o_tables, o_sel, o_tok,
-        words;
+    size_t o_pos, o_slot, o_rg, o_grow0, o_gnrows, o_gtable, o_gwi0, o_gnsplit, o_gcrow0, o_gcpos0, o_wig, o_wis,
+        o_tables, o_sel, o_tok, words;
 };
 
 static int build_plan(const fg_config& c, const fg_kv& kv, int max_pos, const ChunkIn* ch, int nch, Plan& P) {
     const int bs = kv.block_size;
     const int group = c.heads / c.kv_heads;
-    const int rg = std::max(1, std::min(16, ATT_QMAX / group));
+    const int rg = std::max(1, std::min(16, attn_qmax(c.head_dim) / group));
+    const int span = attn_span(c.head_dim);
     P = Plan();
     for (int ci = 0; ci < nch; ci++) {
         const ChunkIn& k = ch[ci];
@@ -396,8 +435,10 @@ static int build_plan(const fg_config& c, const fg_kv& kv, int max_pos, const Ch
             P.g_table.push_back(toff);
             P.g_wi0.push_back((int)P.wi_group.size());
             const int L = k.pos + r0 + nr;
-            const int ns = (L + SPLIT_POS - 1) / SPLIT_POS;
+            const int ns = (L + span - 1) / span;
             P.g_nsplit.push_back(ns);
+            P.g_crow0.push_back(row_base);
+            P.g_cpos0.push_back(k.pos);
             for (int s = 0; s < ns; s++) {
                 P.wi_group.push_back(gi);
                 P.wi_split.push_back(s);
@@ -427,6 +468,8 @@ static int build_plan(const fg_config& c, const fg_kv& kv, int max_pos, const Ch
     P.o_gtable = place(P.G);
     P.o_gwi0 = place(P.G);
     P.o_gnsplit = place(P.G);
+    P.o_gcrow0 = place(P.G);
+    P.o_gcpos0 = place(P.G);
     P.o_wig = place(P.W);
     P.o_wis = place(P.W);
     P.o_tables = place(P.T);
@@ -448,6 +491,8 @@ static void pack_plan(const Plan& P, int32_t* h) {
     cp(P.o_gtable, P.g_table);
     cp(P.o_gwi0, P.g_wi0);
     cp(P.o_gnsplit, P.g_nsplit);
+    cp(P.o_gcrow0, P.g_crow0);
+    cp(P.o_gcpos0, P.g_cpos0);
     cp(P.o_wig, P.wi_group);
     cp(P.o_wis, P.wi_split);
     if (!P.tables.empty()) memcpy(h + P.o_tables, P.tables.data(), P.tables.size() * 4);
@@ -457,62 +502,62 @@ static void pack_plan(const Plan& P, int32_t* h) {
 
 // Workspace of one forward pass over a plan.
 struct Work {
-    float *x, *rinv, *part, *q, *att, *apart, *hsel, *rsel, *lpart, *logits;
-    void* pa;
-    float* pxs;
+    float *x, *ss, *qkv, *apart, *logits;
+    void* pa[2];   // activation pieces, ping-pong: each kernel reads one and writes the other
+    float* pxs[2];
     float2* best;
     uint32_t* am;
-    int kb_max, passes, splits_max, nblk, lm_splits;
-    size_t part_floats;
+    int passes, lm_passes;
 };
 
 static int kind_of(const DMat& m) { return m.kind; }
+static int qkv_dim(const fg_config& c) { return (c.heads + 2 * c.kv_heads) * c.head_dim; }
 
 static size_t layout_work(const fg_model* m, const Plan& P, Work& w, void* base) {
     const fg_config& c = m->cfg;
-    const int t = P.t, H = c.hidden, qd = c.heads * c.head_dim, I = c.intermediate;
+    const int t = P.t, H = c.hidden, S = std::max(P.S, 1);
     Carver cv(base);
-    w.kb_max = 0;
-    w.splits_max = 1;
-    size_t pf = 0;
+    int kb_max = m->lm_head.kb;
     for (const DLayer& l : m->layers)
-        for (const DMat* d : {&l.wqkv, &l.wo, &l.w_gate_up, &l.w_down}) {
-            w.kb_max = std::max(w.kb_max, d->kb);
-            const GemvPlan gp = plan_gemv(*d, t);
-            w.splits_max = std::max(w.splits_max, gp.splits);
-            pf = std::max(pf, (size_t)gp.splits * t * d->rows);
-        }
-    w.kb_max = std::max(w.kb_max, m->lm_head.kb);
-    w.passes = std::max((t + 3) / 4, (P.S + 3) / 4);
-    w.part_floats = pf;
-    const GemvPlan lp = plan_gemv(m->lm_head, std::max(P.S, 1));
-    w.lm_splits = lp.splits;
-    w.nblk = std::max(1, std::min(64, (c.vocab + 4095) / 4096));
+        for (const DMat* d : {&l.wqkv, &l.wo, &l.w_gate_up, &l.w_down}) kb_max = std::max(kb_max, d->kb);
+    w.passes = (t + 3) / 4;
+    w.lm_passes = (S + 3) / 4;
+    const int passes = std::max(w.passes, w.lm_passes);
     w.x = cv.take<float>((size_t)t * H);
-    w.rinv = cv.take<float>(t);
-    w.pa = cv.take<uint8_t>((size_t)w.kb_max * w.passes * 64 * 16);
-    w.pxs = cv.take<float>((size_t)w.kb_max * w.passes * 4);
-    w.part = cv.take<float>(pf);
-    w.q = cv.take<float>((size_t)t * qd);
-    w.att = cv.take<float>((size_t)t * qd);
-    w.apart = cv.take<float>((size_t)std::max(P.W, 1) * c.kv_heads * ATT_QMAX * (c.head_dim + 2));
-    w.hsel = cv.take<float>((size_t)std::max(P.S, 1) * H);
-    w.rsel = cv.take<float>(std::max(P.S, 1));
-    w.lpart = cv.take<float>((size_t)lp.splits * std::max(P.S, 1) * c.vocab);
-    w.logits = cv.take<float>((size_t)std::max(P.S, 1) * c.vocab);
-    w.best = cv.take<float2>((size_t)std::max(P.S, 1) * w.nblk);
-    w.am = cv.take<uint32_t>(std::max(P.S, 1));
-    (void)I;
+    w.ss = cv.take<float>((size_t)(H / 32) * t);
+    for (int i = 0; i < 2; i++) {
+        w.pa[i] = cv.take<uint8_t>((size_t)kb_max * passes * 64 * 16);
+        w.pxs[i] = cv.take<float>((size_t)kb_max * passes * 4);
+    }
+    w.qkv = cv.take<float>((size_t)t * qkv_dim(c));
+    w.apart = cv.take<float>((size_t)std::max(P.W, 1) * c.kv_heads * attn_qmax(c.head_dim) * (c.head_dim + 2));
+    w.logits = cv.take<float>((size_t)S * c.vocab);
+    w.best = cv.take<float2>((size_t)(c.vocab / 32) * S);
+    w.am = cv.take<uint32_t>(S);
     return cv.off + 256;
 }
 
-static Pieces pieces_for(const Work& w, int kb, int passes) {
+static Pieces pieces(const Work& w, int i, int kb, int passes) {
     Pieces p;
-    p.a = w.pa;
-    p.xs = w.pxs;
+    p.a = w.pa[i];
+    p.xs = w.pxs[i];
     p.kb = kb;
     p.passes = passes;
     return p;
+}
+
+static GemvArgs gemv_args(const DMat& d, const Pieces& in, int m) {
+    GemvArgs a;
+    a.W = (const uint8_t*)d.w;
+    a.S = d.s;
+    a.kind = d.kind;
+    a.N = d.rows;
+    a.KB = d.kb;
+    a.XA = (const uint8_t*)in.a;
+    a.XS = in.xs;
+    a.m = m;
+    a.p_total = in.passes;
+    return a;
 }
 
 // Runs one forward pass. `meta` is the device copy of the plan's packed
@@ -525,21 +570,30 @@ static int run_forward(fg_ctx* ctx, const fg_model* m, fg_kv* kv, const Plan& P,
                        uint32_t* aux, int aux_stride, int aux_off, float* hidden_host) {
     const fg_config& c = m->cfg;
     hipStream_t st = ctx->stream;
-    const int t = P.t, H = c.hidden, hd = c.head_dim, nh = c.heads, nkv = c.kv_heads, I = c.intermediate;
-    const int qd = nh * hd;
-    const int passes = (t + 3) / 4;
+    const int t = P.t, H = c.hidden, hd = c.head_dim, nh = c.heads, nkv = c.kv_heads;
+    const int L = (int)m->layers.size();
     if (t == 0) return 0;
-    const int32_t* d_pos = meta + P.o_pos;
-    const int32_t* d_slot = meta + P.o_slot;
+    const int passes = w.passes;
+    int cur = 0;  // pieces buffer the next GEMV reads
 
-    launch_embed(st, tok_dev, tok_stride, m->embed, t, H, w.x);
-    if (hidden_host)
-        HIPCHK(hipMemcpyAsync(hidden_host, w.x, (size_t)t * H * 4, hipMemcpyDeviceToHost, st));
-    launch_residual_rms(st, w.x, nullptr, 1, t, H, c.rms_eps, w.rinv);
+    if (L > 0) {
+        Pieces p0 = pieces(w, cur, m->layers[0].wqkv.kb, passes);
+        launch_embed(st, tok_dev, tok_stride, m->embed, t, H, m->layers[0].attn_norm, w.x, w.ss,
+                     kind_of(m->layers[0].wqkv), p0);
+    } else {
+        Pieces p0 = pieces(w, cur, m->lm_head.kb, passes);
+        launch_embed(st, tok_dev, tok_stride, m->embed, t, H, nullptr, w.x, w.ss, BF16, p0);
+    }
+    if (hidden_host) HIPCHK(hipMemcpyAsync(hidden_host, w.x, (size_t)t * H * 4, hipMemcpyDeviceToHost, st));
 
     AttnArgs aa{};
-    aa.q = w.q;
-    aa.row_pos = d_pos;
+    aa.qkv = w.qkv;
+    aa.ld = qkv_dim(c);
+    aa.cos_t = m->cos_t;
+    aa.sin_t = m->sin_t;
+    aa.row_pos = meta + P.o_pos;
+    aa.row_slot = meta + P.o_slot;
+    aa.row_group = meta + P.o_rg;
     aa.wi_group = meta + P.o_wig;
     aa.wi_split = meta + P.o_wis;
     aa.g_row0 = meta + P.o_grow0;
@@ -547,64 +601,102 @@ static int run_forward(fg_ctx* ctx, const fg_model* m, fg_kv* kv, const Plan& P,
     aa.g_table = meta + P.o_gtable;
     aa.g_wi0 = meta + P.o_gwi0;
     aa.g_nsplit = meta + P.o_gnsplit;
+    aa.g_crow0 = meta + P.o_gcrow0;
+    aa.g_cpos0 = meta + P.o_gcpos0;
     aa.tables = (const uint32_t*)(meta + P.o_tables);
     aa.part = w.apart;
-    aa.out = w.att;
-    aa.row_group = meta + P.o_rg;
     aa.n_wi = P.W;
     aa.nh = nh;
     aa.nkv = nkv;
     aa.hd = hd;
     aa.bs = kv->block_size;
-    aa.split_pos = SPLIT_POS;
-    aa.qmax = ATT_QMAX;
     aa.scale = 1.0f / sqrtf((float)hd);
 
-    for (size_t li = 0; li < m->layers.size(); li++) {
+    for (int li = 0; li < L; li++) {
         const DLayer& l = m->layers[li];
-        float* kc = kv->k + li * kv->layer_floats();
-        float* vc = kv->v + li * kv->layer_floats();
-        // attention block
-        Pieces pa = pieces_for(w, l.wqkv.kb, passes);
-        launch_pieces(st, kind_of(l.wqkv), w.x, H, t, H, l.attn_norm, w.rinv, pa);
-        GemvPlan gp = plan_gemv(l.wqkv, t);
-        gemv(ctx, l.wqkv, pa, t, gp, w.part);
-        launch_rope_kv(st, w.part, gp.splits, t, l.bqkv, d_pos, d_slot, m->cos_t, m->sin_t, nh, nkv, hd,
-                       kv->block_size, w.q, kc, vc);
-        aa.kc = kc;
-        aa.vc = vc;
-        launch_attention(st, aa, t);
-        Pieces po = pieces_for(w, l.wo.kb, passes);
-        launch_pieces(st, kind_of(l.wo), w.att, qd, t, qd, nullptr, nullptr, po);
-        gp = plan_gemv(l.wo, t);
-        gemv(ctx, l.wo, po, t, gp, w.part);
-        launch_residual_rms(st, w.x, w.part, gp.splits, t, H, c.rms_eps, w.rinv);
-        // MLP block
-        Pieces pg = pieces_for(w, l.w_gate_up.kb, passes);
-        launch_pieces(st, kind_of(l.w_gate_up), w.x, H, t, H, l.mlp_norm, w.rinv, pg);
-        gp = plan_gemv(l.w_gate_up, t);
-        gemv(ctx, l.w_gate_up, pg, t, gp, w.part);
-        Pieces pd = pieces_for(w, l.w_down.kb, passes);
-        launch_silu_pieces(st, w.part, gp.splits, t, I, pd, nullptr, kind_of(l.w_down));
-        gp = plan_gemv(l.w_down, t);
-        gemv(ctx, l.w_down, pd, t, gp, w.part);
-        launch_residual_rms(st, w.x, w.part, gp.splits, t, H, c.rms_eps, w.rinv);
+        // q/k/v of the normed rows: rinv from the sum-of-squares partials
+        GemvArgs g = gemv_args(l.wqkv, pieces(w, cur, l.wqkv.kb, passes), t);
+        g.out = w.qkv;
+        g.ldo = qkv_dim(c);
+        g.bias = l.bqkv;
+        g.ss_in = w.ss;
+        g.ss_tiles = H / 32;
+        g.ss_m = t;
+        g.hidden = H;
+        g.eps = c.rms_eps;
+        gemv(ctx, EPI_QKV, l.wqkv, g);
+        // attention (RoPE, cache write) and the merge into wo's pieces
+        aa.kc = kv->k + li * kv->layer_floats();
+        aa.vc = kv->v + li * kv->layer_floats();
+        Pieces po = pieces(w, cur ^ 1, l.wo.kb, passes);
+        launch_attention(st, aa, t, kind_of(l.wo), po);
+        cur ^= 1;
+        // o projection + residual; pieces of mlp_norm * x for gate/up
+        g = gemv_args(l.wo, pieces(w, cur, l.wo.kb, passes), t);
+        g.x = w.x;
+        g.ldx = H;
+        g.ss_out = w.ss;
+        g.ss_m = t;
+        g.g_next = l.mlp_norm;
+        g.pa = w.pa[cur ^ 1];
+        g.pxs = w.pxs[cur ^ 1];
+        g.pa_kind = kind_of(l.w_gate_up);
+        g.pa_passes = passes;
+        g.pa_kb = l.w_gate_up.kb;
+        gemv(ctx, EPI_RESID, l.wo, g);
+        cur ^= 1;
+        // gate/up with SiLU; pieces of the activation for down
+        g = gemv_args(l.w_gate_up, pieces(w, cur, l.w_gate_up.kb, passes), t);
+        g.ss_in = w.ss;
+        g.ss_tiles = H / 32;
+        g.ss_m = t;
+        g.hidden = H;
+        g.eps = c.rms_eps;
+        g.pa = w.pa[cur ^ 1];
+        g.pxs = w.pxs[cur ^ 1];
+        g.pa_kind = kind_of(l.w_down);
+        g.pa_passes = passes;
+        g.pa_kb = l.w_down.kb;
+        gemv(ctx, EPI_SILU, l.w_gate_up, g);
+        cur ^= 1;
+        // down projection + residual; pieces of the next layer's attn_norm * x
+        g = gemv_args(l.w_down, pieces(w, cur, l.w_down.kb, passes), t);
+        g.x = w.x;
+        g.ldx = H;
+        g.ss_out = w.ss;
+        g.ss_m = t;
+        if (li + 1 < L) {
+            const DLayer& nl = m->layers[li + 1];
+            g.g_next = nl.attn_norm;
+            g.pa = w.pa[cur ^ 1];
+            g.pxs = w.pxs[cur ^ 1];
+            g.pa_kind = kind_of(nl.wqkv);
+            g.pa_passes = passes;
+            g.pa_kb = nl.wqkv.kb;
+        }
+        gemv(ctx, EPI_RESID, l.w_down, g);
+        cur ^= 1;
         if (hidden_host)
             HIPCHK(hipMemcpyAsync(hidden_host + (li + 1) * (size_t)t * H, w.x, (size_t)t * H * 4,
                                   hipMemcpyDeviceToHost, st));
     }
     HIPCHK(hipGetLastError());
     if (P.S == 0) return 0;
-    // final norm on the selected rows, lm_head, argmax
-    launch_gather_rows(st, w.x, meta + P.o_sel, P.S, H, w.hsel);
-    launch_residual_rms(st, w.hsel, nullptr, 1, P.S, H, c.rms_eps, w.rsel);
-    const int sp = (P.S + 3) / 4;
-    Pieces pl = pieces_for(w, m->lm_head.kb, sp);
-    launch_pieces(st, kind_of(m->lm_head), w.hsel, H, P.S, H, m->norm, w.rsel, pl);
-    const GemvPlan lp = plan_gemv(m->lm_head, P.S);
-    gemv(ctx, m->lm_head, pl, P.S, lp, w.lpart);
-    launch_argmax(st, w.lpart, lp.splits, P.S, c.vocab, logits_dev, w.best, w.nblk, am_out ? am_out : w.am, aux,
-                  aux_stride, aux_off);
+    // final norm of the selected rows (weight now, 1/rms in the epilogue), lm_head, argmax
+    const int32_t* sel = meta + P.o_sel;
+    Pieces pl = pieces(w, cur, m->lm_head.kb, w.lm_passes);
+    launch_pieces(st, kind_of(m->lm_head), w.x, H, P.S, H, m->norm, sel, pl);
+    GemvArgs g = gemv_args(m->lm_head, pl, P.S);
+    g.ss_in = w.ss;
+    g.ss_tiles = H / 32;
+    g.ss_m = t;
+    g.hidden = H;
+    g.eps = c.rms_eps;
+    g.rows_src = sel;
+    g.logits = logits_dev;
+    g.best = w.best;
+    gemv(ctx, EPI_ARGMAX, m->lm_head, g);
+    launch_argmax_final(st, w.best, c.vocab / 32, P.S, am_out ? am_out : w.am, aux, aux_stride, aux_off);
     HIPCHK(hipGetLastError());
     return 0;
 }
@@ -629,6 +721,8 @@ int fg_ctx_create(int device, fg_ctx** out) {
         return fail(FG_E_DEVICE, "stream creation failed");
     }
     for (auto& e : c->ev) HIPCHK(hipEventCreate(&e));
+    const char* ng = std::getenv("FERRO_NO_GRAPH");
+    c->graphs = !(ng && ng[0] == '1');
     *out = c;
     return 0;
 }
@@ -637,6 +731,7 @@ void fg_ctx_destroy(fg_ctx* c) {
     if (!c) return;
     (void)hipSetDevice(c->device);
     (void)hipStreamSynchronize(c->stream);
+    drop_graphs(c);
     if (c->ws) (void)hipFree(c->ws);
     if (c->dmeta) (void)hipFree(c->dmeta);
     if (c->hmeta) (void)hipHostFree(c->hmeta);
@@ -660,7 +755,9 @@ int fg_model_upload(fg_ctx* ctx, const fg_config* cfg, const fg_layer* layers, c
     if (c.heads <= 0 || c.kv_heads <= 0 || c.heads % c.kv_heads || c.head_dim % 16 || c.hidden % 16 ||
         c.head_dim > 128 || c.vocab <= 0 || c.layers < 0 || c.max_position <= 0)
         return fail(FG_E_SHAPE, "unsupported model shape");
-    if (c.heads / c.kv_heads > ATT_QMAX) return fail(FG_E_SHAPE, "GQA group too large");
+    if (c.heads / c.kv_heads > attn_qmax(c.head_dim)) return fail(FG_E_SHAPE, "GQA group too large");
+    if (c.hidden % 32 || c.intermediate % 32 || (c.heads * c.head_dim) % 32)
+        return fail(FG_E_SHAPE, "hidden, intermediate and q sizes must be multiples of 32");
     HIPCHK(hipSetDevice(ctx->device));
     fg_model* m = new fg_model();
     m->cfg = c;
@@ -685,7 +782,7 @@ int fg_model_upload(fg_ctx* ctx, const fg_config* cfg, const fg_layer* layers, c
         if (c.qkv_bias && (rc = upload_vec(s.bqkv, qkv, &d.bqkv, m->allocs))) return bad(rc);
         if ((rc = upload_mat(s.wqkv, d.wqkv, &m->allocs))) return bad(rc);
         if ((rc = upload_mat(s.wo, d.wo, &m->allocs))) return bad(rc);
-        if ((rc = upload_mat(s.w_gate_up, d.w_gate_up, &m->allocs))) return bad(rc);
+        if ((rc = upload_mat(s.w_gate_up, d.w_gate_up, &m->allocs, c.intermediate))) return bad(rc);
         if ((rc = upload_mat(s.w_down, d.w_down, &m->allocs))) return bad(rc);
         ref += d.wqkv.ref_bytes + d.wo.ref_bytes + d.w_gate_up.ref_bytes + d.w_down.ref_bytes;
     }
@@ -889,24 +986,80 @@ int fg_spec_step(fg_ctx* ctx, const fg_model* target, fg_kv* tkv, const fg_model
     if ((rc = ensure(&ctx->ws, &ctx->ws_cap, need, ctx->stream, false))) return rc;
     int32_t* dm = (int32_t*)ctx->dmeta;
     uint32_t* vtok = (uint32_t*)(dm + o_vtok);
-    HIPCHK(hipEventRecord(ctx->ev[0], ctx->stream));
-    for (int r = 0; r < k; r++) {
-        layout_work(draft, plans[r], w, ctx->ws);
-        const int32_t* meta = dm + base[r];
-        const uint32_t* tok = r == 0 ? (const uint32_t*)(meta + plans[r].o_tok) : vtok + r;
-        const int stride = r == 0 ? 1 : K1;
-        // the draft's greedy proposal d_{r+1} goes to verify row s, column r+1
-        if ((rc = run_forward(ctx, draft, dkv, plans[r], meta, tok, stride, w, nullptr,
-                              (uint32_t*)(dm + o_am), vtok, K1, r + 1, nullptr)))
-            return rc;
+    // The two phases as launch sequences (captured into graphs when enabled).
+    auto draft_phase = [&]() -> int {
+        for (int r = 0; r < k; r++) {
+            layout_work(draft, plans[r], w, ctx->ws);
+            const int32_t* meta = dm + base[r];
+            const uint32_t* tok = r == 0 ? (const uint32_t*)(meta + plans[r].o_tok) : vtok + r;
+            const int stride = r == 0 ? 1 : K1;
+            // the draft's greedy proposal d_{r+1} goes to verify row s, column r+1
+            int e = run_forward(ctx, draft, dkv, plans[r], meta, tok, stride, w, nullptr, (uint32_t*)(dm + o_am),
+                                vtok, K1, r + 1, nullptr);
+            if (e) return e;
+        }
+        return 0;
+    };
+    auto verify_phase = [&]() -> int {
+        layout_work(target, plans[k], w, ctx->ws);
+        int e = run_forward(ctx, target, tkv, plans[k], dm + base[k], vtok, 1, w, nullptr, (uint32_t*)(dm + o_am),
+                            nullptr, 0, 0, nullptr);
+        if (e) return e;
+        launch_accept(ctx->stream, (const uint32_t*)(dm + o_am), vtok, n_seqs, k, (uint32_t*)(dm + o_out),
+                      dm + o_cnt, dm + o_acc);
+        return 0;
+    };
+    bool use_graph = ctx->graphs && !ctx->prof;
+    if (use_graph) {
+        std::vector<int64_t> sig = {n_seqs, k, (int64_t)(uintptr_t)target, (int64_t)(uintptr_t)draft,
+                                    (int64_t)(uintptr_t)tkv, (int64_t)(uintptr_t)dkv, (int64_t)(uintptr_t)ctx->ws,
+                                    (int64_t)(uintptr_t)ctx->dmeta, ctx->prof ? 1 : 0};
+        for (int r = 0; r <= k; r++) {
+            const Plan& P = plans[r];
+            for (int64_t v : {(int64_t)P.t, (int64_t)P.S, (int64_t)P.G, (int64_t)P.W, (int64_t)P.T, (int64_t)P.words})
+                sig.push_back(v);
+        }
+        if (sig != ctx->gs.sig || !ctx->gs.exec[0] || !ctx->gs.exec[1]) {
+            drop_graphs(ctx);
+            std::function<int()> phases[2] = {draft_phase, verify_phase};
+            for (int g = 0; g < 2 && use_graph; g++) {
+                HIPCHK(hipStreamBeginCapture(ctx->stream, hipStreamCaptureModeThreadLocal));
+                ctx->capturing = true;
+                ctx->capture_prof.clear();
+                const int e = phases[g]();
+                ctx->capturing = false;
+                hipGraph_t graph = nullptr;
+                const hipError_t ce = hipStreamEndCapture(ctx->stream, &graph);
+                if (e) {
+                    if (graph) (void)hipGraphDestroy(graph);
+                    drop_graphs(ctx);
+                    return e;
+                }
+                if (ce != hipSuccess || !graph ||
+                    hipGraphInstantiate(&ctx->gs.exec[g], graph, nullptr, nullptr, 0) != hipSuccess) {
+                    if (graph) (void)hipGraphDestroy(graph);
+                    (void)hipGetLastError();
+                    drop_graphs(ctx);
+                    use_graph = false;  // launch directly this time
+                    break;
+                }
+                (void)hipGraphDestroy(graph);
+                for (auto& p : ctx->capture_prof) ctx->gs.prof.push_back(p);
+                ctx->capture_prof.clear();
+            }
+            if (use_graph) ctx->gs.sig = sig;
+        }
     }
-    HIPCHK(hipEventRecord(ctx->ev[1], ctx->stream));
-    layout_work(target, plans[k], w, ctx->ws);
-    if ((rc = run_forward(ctx, target, tkv, plans[k], dm + base[k], vtok, 1, w, nullptr, (uint32_t*)(dm + o_am),
-                          nullptr, 0, 0, nullptr)))
+    HIPCHK(hipEventRecord(ctx->ev[0], ctx->stream));
+    if (use_graph)
+        HIPCHK(hipGraphLaunch(ctx->gs.exec[0], ctx->stream));
+    else if ((rc = draft_phase()))
         return rc;
-    launch_accept(ctx->stream, (const uint32_t*)(dm + o_am), vtok, n_seqs, k, (uint32_t*)(dm + o_out), dm + o_cnt,
-                  dm + o_acc);
+    HIPCHK(hipEventRecord(ctx->ev[1], ctx->stream));
+    if (use_graph)
+        HIPCHK(hipGraphLaunch(ctx->gs.exec[1], ctx->stream));
+    else if ((rc = verify_phase()))
+        return rc;
     HIPCHK(hipGetLastError());
     HIPCHK(hipEventRecord(ctx->ev[2], ctx->stream));
     HIPCHK(hipMemcpyAsync(h + o_out, dm + o_out, (words - o_out) * 4, hipMemcpyDeviceToHost, ctx->stream));
@@ -986,41 +1139,41 @@ void fg_mat_destroy(fg_mat* m) {
     delete m;
 }
 
-// Workspace for a lone product: pieces, partials, (x, y when staged).
-static size_t layout_mat(const DMat& d, int m, const GemvPlan& gp, Pieces& p, float** part, float** xbuf,
-                         float** ybuf, void* base) {
+// Workspace for a lone product: pieces, staged x and y.
+static size_t layout_mat(const DMat& d, int m, Pieces& p, float** xbuf, float** ybuf, float** bbuf, void* base) {
     Carver cv(base);
     p.kb = d.kb;
     p.passes = (m + 3) / 4;
     p.a = cv.take<uint8_t>((size_t)d.kb * p.passes * 64 * 16);
     p.xs = cv.take<float>((size_t)d.kb * p.passes * 4);
-    *part = cv.take<float>((size_t)gp.splits * m * d.rows);
     *xbuf = cv.take<float>((size_t)m * d.cols);
     *ybuf = cv.take<float>((size_t)m * d.rows);
+    *bbuf = cv.take<float>((size_t)d.rows);
     return cv.off + 256;
+}
+
+static void matmul_launch(fg_ctx* ctx, const DMat& d, Pieces& p, const float* x, int m, const float* bias, float* y) {
+    launch_pieces(ctx->stream, d.kind, x, d.cols, m, d.cols, nullptr, nullptr, p);
+    GemvArgs g = gemv_args(d, p, m);
+    g.out = y;
+    g.ldo = d.rows;
+    g.bias = bias;
+    gemv(ctx, EPI_STORE, d, g);
 }
 
 int fg_matmul(fg_ctx* ctx, const fg_mat* w, const float* x, int32_t m, const float* bias, float* y) {
     if (!ctx || !w || !x || !y || m <= 0) return fail(FG_E_ARG, "bad argument");
     HIPCHK(hipSetDevice(ctx->device));
     const DMat& d = w->m;
-    const GemvPlan gp = plan_gemv(d, m);
     Pieces p;
-    float *part, *xb, *yb;
-    const size_t need = layout_mat(d, m, gp, p, &part, &xb, &yb, nullptr) + (size_t)d.rows * 4 + 256;
+    float *xb, *yb, *bb;
     int rc;
-    if ((rc = ensure(&ctx->ws, &ctx->ws_cap, need, ctx->stream, false))) return rc;
-    layout_mat(d, m, gp, p, &part, &xb, &yb, ctx->ws);
-    float* bb = nullptr;
-    if (bias) {
-        bb = yb + (size_t)m * d.rows;
-        bb = (float*)(((uintptr_t)bb + 255) & ~(uintptr_t)255);
-        HIPCHK(hipMemcpyAsync(bb, bias, (size_t)d.rows * 4, hipMemcpyHostToDevice, ctx->stream));
-    }
+    if ((rc = ensure(&ctx->ws, &ctx->ws_cap, layout_mat(d, m, p, &xb, &yb, &bb, nullptr), ctx->stream, false)))
+        return rc;
+    layout_mat(d, m, p, &xb, &yb, &bb, ctx->ws);
+    if (bias) HIPCHK(hipMemcpyAsync(bb, bias, (size_t)d.rows * 4, hipMemcpyHostToDevice, ctx->stream));
     HIPCHK(hipMemcpyAsync(xb, x, (size_t)m * d.cols * 4, hipMemcpyHostToDevice, ctx->stream));
-    launch_pieces(ctx->stream, d.kind, xb, d.cols, m, d.cols, nullptr, nullptr, p);
-    launch_gemv(ctx->stream, d, p, m, gp, part);
-    launch_reduce(ctx->stream, part, gp.splits, m, d.rows, bb, yb);
+    matmul_launch(ctx, d, p, xb, m, bias ? bb : nullptr, yb);
     HIPCHK(hipGetLastError());
     HIPCHK(hipMemcpyAsync(y, yb, (size_t)m * d.rows * 4, hipMemcpyDeviceToHost, ctx->stream));
     HIPCHK(hipStreamSynchronize(ctx->stream));
@@ -1030,16 +1183,13 @@ int fg_matmul(fg_ctx* ctx, const fg_mat* w, const float* x, int32_t m, const flo
 int fg_matmul_device(fg_ctx* ctx, const fg_mat* w, const float* x_dev, int32_t m, float* y_dev) {
     if (!ctx || !w || !x_dev || !y_dev || m <= 0) return fail(FG_E_ARG, "bad argument");
     const DMat& d = w->m;
-    const GemvPlan gp = plan_gemv(d, m);
     Pieces p;
-    float *part, *xb, *yb;
-    const size_t need = layout_mat(d, m, gp, p, &part, &xb, &yb, nullptr);
+    float *xb, *yb, *bb;
     int rc;
-    if ((rc = ensure(&ctx->ws, &ctx->ws_cap, need, ctx->stream, false))) return rc;
-    layout_mat(d, m, gp, p, &part, &xb, &yb, ctx->ws);
-    launch_pieces(ctx->stream, d.kind, x_dev, d.cols, m, d.cols, nullptr, nullptr, p);
-    gemv(ctx, d, p, m, gp, part);
-    launch_reduce(ctx->stream, part, gp.splits, m, d.rows, nullptr, y_dev);
+    if ((rc = ensure(&ctx->ws, &ctx->ws_cap, layout_mat(d, m, p, &xb, &yb, &bb, nullptr), ctx->stream, false)))
+        return rc;
+    layout_mat(d, m, p, &xb, &yb, &bb, ctx->ws);
+    matmul_launch(ctx, d, p, x_dev, m, nullptr, y_dev);
     HIPCHK(hipGetLastError());
     return 0;
 }

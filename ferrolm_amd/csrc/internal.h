@@ -9,10 +9,11 @@ namespace fg {
 // ---------------------------------------------------------------------------
 // Device weight layout (repacked at upload from the reference's formats).
 //
-// A matrix of N output rows x K inputs is cut into tiles of 16 rows and
+// A matrix of N output rows x K inputs is cut into n-tiles of 16 rows and
 // k-blocks of 32 inputs (one quantization group). K is padded with zeros to
-// a multiple of 128 (4 k-blocks). One tile x k-block is exactly one MFMA
-// B-operand: lane l (0..63) holds row n = l % 16, inputs 8*(l/16) .. +7.
+// a multiple of 128 (4 k-blocks, a "chunk"). One n-tile x k-block is exactly
+// one MFMA B-operand: lane l (0..63) holds row n = l % 16, inputs
+// 8*(l/16) .. +7.
 //
 //   BF16: [tile][kb][lane][8 x bf16]            16 B per lane per k-block
 //   INT8: [tile][kb/2][lane][2 kb x 8 x int8]   16 B per lane per 2 k-blocks
@@ -23,8 +24,12 @@ namespace fg {
 //         holding 16 x code.
 //   scales (INT8/INT4): [tile][kb/4][16 rows][4 kb] f32; INT4 scales are
 //         stored divided by 16 (exact) to undo the 16 x code above.
-// Each (tile, 4 k-blocks) chunk is contiguous, so a wave's 16-byte loads
-// cover 1 KB of consecutive memory.
+// Each (tile, chunk) is contiguous, so a wave's 16-byte loads cover 1 KB of
+// consecutive memory.
+//
+// Row order: the stacked gate/up matrix is stored interleaved in blocks of
+// 32, [gate 32c..32c+31, up 32c..32c+31] for c = 0.., so one 64-row output
+// tile holds the gate and up values of 32 intermediate channels.
 // ---------------------------------------------------------------------------
 enum { BF16 = 0, INT8 = 1, INT4 = 2 };
 
@@ -54,53 +59,90 @@ struct Pieces {
     int kb = 0, passes = 0;
 };
 
-struct GemvPlan {
-    int splits = 1;
+// GEMV epilogues.
+enum Epi {
+    EPI_STORE = 0,   // y (+ bias) -> out
+    EPI_QKV = 1,     // y * rinv (+ bias) -> out: the q/k/v projection of a normed input
+    EPI_RESID = 2,   // x += y; sum of squares per (k-block, row); pieces of g * x for the next consumer
+    EPI_SILU = 3,    // silu(gate * rinv) * (up * rinv) -> pieces for the down projection
+    EPI_ARGMAX = 4,  // logits y * rinv (optionally stored) -> per 32-column tile (max, index)
 };
 
-// Kernel launchers (kernels.hip).
-void launch_embed(hipStream_t st, const uint32_t* tokens, int stride, const uint16_t* embed, int m, int H, float* x);
-void launch_residual_rms(hipStream_t st, float* x, const float* partials, int splits, int m, int H, float eps,
-                         float* rinv);
+struct GemvArgs {
+    const uint8_t* W = nullptr;
+    const float* S = nullptr;
+    int kind = 0, N = 0, KB = 0;
+    const uint8_t* XA = nullptr;  // input pieces
+    const float* XS = nullptr;
+    int m = 0, p_total = 0;
+    // STORE / QKV
+    float* out = nullptr;
+    int ldo = 0;
+    const float* bias = nullptr;
+    // 1/rms of the input rows from sum-of-squares partials ss_in[tile][ss_m]
+    const float* ss_in = nullptr;
+    int ss_tiles = 0, ss_m = 0, hidden = 0;
+    float eps = 0;
+    const int32_t* rows_src = nullptr;  // local row -> row of ss_in (nullptr: identity)
+    // RESID / SILU
+    float* x = nullptr;
+    int ldx = 0;
+    float* ss_out = nullptr;
+    const float* g_next = nullptr;  // norm weight applied to the next consumer's input (nullptr: none)
+    void* pa = nullptr;             // next consumer's pieces (nullptr: none)
+    float* pxs = nullptr;
+    int pa_kind = 0, pa_passes = 0, pa_kb = 0;  // pa_kb: the consumer's padded k-blocks
+    // ARGMAX
+    float* logits = nullptr;
+    float2* best = nullptr;
+};
+
+// start/stop (optional) are recorded by the dispatch itself (hipExtLaunchKernelGGL),
+// so their interval is the kernel's own execution time.
+void launch_gemv(hipStream_t st, int epi, const DMat& w, const GemvArgs& a, hipEvent_t start = nullptr,
+                 hipEvent_t stop = nullptr);
+
 void launch_pieces(hipStream_t st, int consumer_kind, const float* x, int ldx, int m, int K, const float* g,
-                   const float* rinv, Pieces& out);
-void launch_silu_pieces(hipStream_t st, const float* partials, int splits, int m, int I, Pieces& out,
-                        float* act_out, int consumer_kind);
-GemvPlan plan_gemv(const DMat& w, int m);
-void launch_gemv(hipStream_t st, const DMat& w, const Pieces& x, int m, const GemvPlan& plan, float* partials);
-void launch_reduce(hipStream_t st, const float* partials, int splits, int m, int N, const float* bias, float* y);
-void launch_rope_kv(hipStream_t st, const float* partials, int splits, int m, const float* bias,
-                    const int32_t* row_pos, const int32_t* row_slot, const float* cos_t, const float* sin_t,
-                    int nh, int nkv, int hd, int bs, float* q_out, float* kc, float* vc);
+                   const int32_t* rows_src, Pieces& out);
+void launch_embed(hipStream_t st, const uint32_t* tokens, int stride, const uint16_t* embed, int m, int H,
+                  const float* g, float* x, float* ss, int consumer_kind, Pieces& out);
 
 struct AttnArgs {
-    const float* q;          // [m][nh*hd]
-    const float* kc;         // layer K cache
-    const float* vc;
-    const int32_t* row_pos;  // [m]
-    const int32_t* wi_group; // work item -> group
-    const int32_t* wi_split; // work item -> split index within group
-    const int32_t* g_row0;   // group -> first row
+    const float* qkv;  // [m][ld] q, k, v of the new rows (q and k not yet rotated)
+    int ld;
+    float* kc;  // layer K cache [block][kv_head][bs][hd]
+    float* vc;
+    const float* cos_t;
+    const float* sin_t;
+    const int32_t* row_pos;   // [m]
+    const int32_t* row_slot;  // [m]
+    const int32_t* row_group; // [m] -> group
+    const int32_t* wi_group;  // work item -> group
+    const int32_t* wi_split;  // work item -> split index within the group
+    const int32_t* g_row0;    // group -> first row
     const int32_t* g_nrows;
-    const int32_t* g_table;  // group -> offset of its block table in tables[]
-    const int32_t* g_wi0;    // group -> first work item
+    const int32_t* g_table;   // group -> offset of its block table in tables[]
+    const int32_t* g_wi0;     // group -> first work item
     const int32_t* g_nsplit;
+    const int32_t* g_crow0;   // group -> first row of its chunk
+    const int32_t* g_cpos0;   // group -> position of its chunk's first row
     const uint32_t* tables;
-    float* part;             // [wi][nkv][qmax][hd+2]
-    float* out;              // [m][nh*hd]
-    const int32_t* row_group;// [m] -> group
-    int n_wi, nh, nkv, hd, bs, split_pos, qmax;
+    float* part;  // [wi][nkv][attn_qmax(hd)][hd+2]
+    int n_wi, nh, nkv, hd, bs;
     float scale;
 };
-void launch_attention(hipStream_t st, const AttnArgs& a, int m);
+// Attention over the paged cache (RoPE, K/V write of the new rows), then the
+// split merge straight into the output projection's pieces.
+void launch_attention(hipStream_t st, const AttnArgs& a, int m, int consumer_kind, Pieces& out);
 
-void launch_argmax(hipStream_t st, const float* partials, int splits, int rows, int V, float* logits_out,
-                   float2* block_best, int nblk, uint32_t* argmax_out, uint32_t* aux, int aux_stride,
-                   int aux_off);
-void launch_gather_rows(hipStream_t st, const float* x, const int32_t* rows, int n, int H, float* out);
+void launch_argmax_final(hipStream_t st, const float2* best, int tiles, int rows, uint32_t* argmax_out,
+                         uint32_t* aux, int aux_stride, int aux_off);
 void launch_accept(hipStream_t st, const uint32_t* argmax, const uint32_t* drafts, int n_seqs, int k,
                    uint32_t* out_tokens, int32_t* out_count, int32_t* out_accepted);
-void launch_copy_tokens(hipStream_t st, const uint32_t* src, int n, int src_stride, uint32_t* dst,
-                        int dst_stride);
+
+// Positions per attention work item and queries per work item (rows of a
+// group x GQA group), by head dim.
+int attn_span(int hd);
+int attn_qmax(int hd);
 
 }  // namespace fg

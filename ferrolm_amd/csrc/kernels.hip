@@ -1,18 +1,29 @@
 // HIP kernels for gfx950 (MI355X): the verify-path hot ops.
 //
+// One transformer layer is six launches: the q/k/v GEMV, attention, the
+// split merge (into the output projection's operand), and the o, gate/up
+// and down GEMVs. Each GEMV workgroup owns a 32- or 64-row output tile over
+// the whole input, so its epilogue sees finished outputs and does the
+// elementwise work of the reference in place (residual add, the RMSNorm
+// sum of squares, SiLU * up) and writes the next GEMV's operand directly.
+//
 // Reference counterparts (Rust, /root/reference):
-//   k_embed           Model::forward embedding gather      src/model.rs:295-298
-//   k_residual_rms    kernels::add + rms_norm's mean square src/kernels.rs:597-607,665-669
-//   k_pieces          rms_norm's scaling + operand prep    src/kernels.rs:597-607
-//   k_gemv            kernels::matmul / quant::panels_of   src/kernels.rs:249-376, src/quant.rs:175-454
-//   k_silu_pieces     kernels::silu_mul                    src/kernels.rs:650-663
-//   k_rope_kv         rope + KvCache::write                src/model.rs:314-321,451-459; src/kv.rs:48-56
-//   k_attn/_merge     Model::attention + kernels::attend   src/model.rs:395-432; src/kernels.rs:703-756
-//   k_argmax1/2       sampler::argmax                      src/sampler.rs:41-51
-//   k_accept          Engine::execute greedy accept        src/engine.rs:563-616
+//   k_embed         embedding gather + first rms_norm input  src/model.rs:295-299; src/kernels.rs:597-607
+//   k_gemv          kernels::matmul / quant::panels_of        src/kernels.rs:249-376; src/quant.rs:175-454
+//     EPI_QKV       rms_norm scaling + qkv bias               src/kernels.rs:597-607,268-274
+//     EPI_RESID     kernels::add + rms_norm's mean square     src/kernels.rs:665-669,597-607
+//     EPI_SILU      kernels::silu_mul                         src/kernels.rs:650-663
+//     EPI_ARGMAX    final rms_norm + lm_head + argmax         src/model.rs:338-361; src/sampler.rs:41-51
+//   k_attn          rope + KvCache::write + attend            src/model.rs:314-322,395-459; src/kv.rs:48-56;
+//                                                             src/kernels.rs:703-756
+//   k_merge_pieces  the softmax normalisation of attend       src/kernels.rs:722-732
+//   k_accept        Engine::execute greedy accept             src/engine.rs:563-616
 #include "internal.h"
 
+#include <hip/hip_ext.h>
 #include <math.h>
+
+#include <algorithm>
 
 namespace fg {
 
@@ -26,7 +37,7 @@ typedef int8_t i8x8 __attribute__((ext_vector_type(8)));
 __device__ __forceinline__ float bf16_bits_to_f32(uint32_t h) { return __uint_as_float(h << 16); }
 
 __device__ __forceinline__ uint32_t f32_to_bf16_bits(float x) {
-    uint32_t b = __float_as_uint(x);
+    const uint32_t b = __float_as_uint(x);
     return (b + 0x7FFFu + ((b >> 16) & 1u)) >> 16;
 }
 
@@ -34,80 +45,22 @@ __device__ __forceinline__ uint32_t f32_to_bf16_bits(float x) {
 // sequence of operations as the reference's kernels::exp (src/kernels.rs:609-637).
 __device__ __forceinline__ float dev_exp(float x) {
     x = fminf(fmaxf(x, -87.0f), 88.0f);
-    float n = rintf(x * 1.44269504088896341f);
-    float r = fmaf(n, 2.1219444e-4f, fmaf(n, -0.6933594f, x));
+    const float n = rintf(x * 1.44269504088896341f);
+    const float r = fmaf(n, 2.1219444e-4f, fmaf(n, -0.6933594f, x));
     float p = 1.9875691e-4f;
     p = fmaf(p, r, 1.3982e-3f);
     p = fmaf(p, r, 8.333452e-3f);
     p = fmaf(p, r, 4.1665796e-2f);
     p = fmaf(p, r, 0.16666665f);
     p = fmaf(p, r, 0.5f);
-    float y = fmaf(p, r * r, r) + 1.0f;
+    const float y = fmaf(p, r * r, r) + 1.0f;
     return y * __int_as_float(((int)n + 127) << 23);
 }
 
-// Sum over a 256-thread block in a fixed order (deterministic).
-__device__ __forceinline__ float block_sum256(float v, float* red) {
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
-    const int w = threadIdx.x >> 6;
-    if ((threadIdx.x & 63) == 0) red[w] = v;
-    __syncthreads();
-    float t = (red[0] + red[1]) + (red[2] + red[3]);
-    __syncthreads();
-    return t;
-}
-
 // ---------------------------------------------------------------------------
-// Embedding gather: x[r] = embed[token[r]] as f32.
-// ---------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void k_embed(const uint32_t* __restrict__ tok, int stride,
-                                               const uint16_t* __restrict__ E, int H, float* __restrict__ x) {
-    const int r = blockIdx.x;
-    const uint16_t* e = E + (size_t)tok[(size_t)r * stride] * H;
-    float* xr = x + (size_t)r * H;
-    for (int i = threadIdx.x; i < H; i += 256) xr[i] = bf16_bits_to_f32(e[i]);
-}
-
-void launch_embed(hipStream_t st, const uint32_t* tokens, int stride, const uint16_t* embed, int m, int H, float* x) {
-    if (m <= 0) return;
-    hipLaunchKernelGGL(k_embed, dim3(m), dim3(256), 0, st, tokens, stride, embed, H, x);
-}
-
-// ---------------------------------------------------------------------------
-// Residual add of a split GEMV's partial sums, then the RMSNorm factor
-// rinv = 1/sqrt(mean(x^2) + eps) of the updated row. One block per row.
-// ---------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void k_residual_rms(float* __restrict__ x, const float* __restrict__ part,
-                                                      int splits, int m, int H, float eps,
-                                                      float* __restrict__ rinv) {
-    __shared__ float red[4];
-    const int r = blockIdx.x;
-    float* xr = x + (size_t)r * H;
-    float ss = 0.0f;
-    for (int i = threadIdx.x; i < H; i += 256) {
-        float v = xr[i];
-        if (part) {
-            float p = 0.0f;
-            for (int s = 0; s < splits; s++) p += part[((size_t)s * m + r) * H + i];
-            v += p;
-            xr[i] = v;
-        }
-        ss = fmaf(v, v, ss);
-    }
-    ss = block_sum256(ss, red);
-    if (threadIdx.x == 0 && rinv) rinv[r] = 1.0f / sqrtf(ss / (float)H + eps);
-}
-
-void launch_residual_rms(hipStream_t st, float* x, const float* partials, int splits, int m, int H, float eps,
-                         float* rinv) {
-    if (m <= 0) return;
-    hipLaunchKernelGGL(k_residual_rms, dim3(m), dim3(256), 0, st, x, partials, splits, m, H, eps, rinv);
-}
-
-// ---------------------------------------------------------------------------
-// Activation pieces (see Pieces in internal.h). One wave per (k-block,
-// pass); lane l covers (row, piece) = (4*pass + (l%16)/4, l%4) at inputs
-// 8*(l/16)..+7 of the k-block.
+// Activation pieces (see Pieces in internal.h). Called by a whole wave: lane
+// l holds v[0..7] = inputs 8*(l/16)..+7 of k-block kb for (row, piece) =
+// (4*pass + (l%16)/4, l%4).
 // ---------------------------------------------------------------------------
 template <int CK>
 __device__ __forceinline__ void write_pieces(const float (&v)[8], int kb, int pass, int passes, int row, int piece,
@@ -154,23 +107,33 @@ __device__ __forceinline__ void write_pieces(const float (&v)[8], int kb, int pa
     }
 }
 
+__device__ __forceinline__ void write_pieces_kind(int kind, const float (&v)[8], int kb, int pass, int passes,
+                                                  int row, int piece, int lane, void* out, float* xs) {
+    if (kind == BF16)
+        write_pieces<BF16>(v, kb, pass, passes, row, piece, lane, out, xs);
+    else
+        write_pieces<INT8>(v, kb, pass, passes, row, piece, lane, out, xs);
+}
+
+// Pieces of g * x[rows_src[row]] (g, rows_src optional). One wave per
+// (k-block, pass).
 template <int CK>
 __global__ __launch_bounds__(64) void k_pieces(const float* __restrict__ x, int ldx, int m, int K,
-                                               const float* __restrict__ g, const float* __restrict__ rinv,
+                                               const float* __restrict__ g, const int32_t* __restrict__ rows_src,
                                                void* __restrict__ out, float* __restrict__ xs, int passes) {
     const int kb = blockIdx.x, pass = blockIdx.y, lane = threadIdx.x;
     const int c = lane & 15, row = pass * 4 + (c >> 2), piece = c & 3;
     const int k0 = kb * 32 + (lane >> 4) * 8;
     float v[8];
     const bool rv = row < m;
-    const float ri = (rv && rinv) ? rinv[row] : 1.0f;
+    const int src = rv ? (rows_src ? rows_src[row] : row) : 0;
 #pragma unroll
     for (int s = 0; s < 8; s++) {
         const int k = k0 + s;
         float t = 0.0f;
         if (rv && k < K) {
-            t = x[(size_t)row * ldx + k];
-            if (g) t = g[k] * (t * ri);  // rms_norm's o = g * (v * r)
+            t = x[(size_t)src * ldx + k];
+            if (g) t = g[k] * t;
         }
         v[s] = t;
     }
@@ -178,52 +141,71 @@ __global__ __launch_bounds__(64) void k_pieces(const float* __restrict__ x, int 
 }
 
 void launch_pieces(hipStream_t st, int consumer_kind, const float* x, int ldx, int m, int K, const float* g,
-                   const float* rinv, Pieces& out) {
+                   const int32_t* rows_src, Pieces& out) {
+    if (m <= 0) return;
     dim3 grid(out.kb, out.passes);
     if (consumer_kind == BF16)
-        hipLaunchKernelGGL(k_pieces<BF16>, grid, dim3(64), 0, st, x, ldx, m, K, g, rinv, out.a, out.xs, out.passes);
+        hipLaunchKernelGGL(k_pieces<BF16>, grid, dim3(64), 0, st, x, ldx, m, K, g, rows_src, out.a, out.xs,
+                           out.passes);
     else
-        hipLaunchKernelGGL(k_pieces<INT8>, grid, dim3(64), 0, st, x, ldx, m, K, g, rinv, out.a, out.xs, out.passes);
+        hipLaunchKernelGGL(k_pieces<INT8>, grid, dim3(64), 0, st, x, ldx, m, K, g, rows_src, out.a, out.xs,
+                           out.passes);
 }
-
-// SiLU(gate) * up from the gate/up GEMV's partial sums, straight into the
-// down projection's pieces: o = g / (1 + exp(-g)) * u (src/kernels.rs:650-663).
-template <int CK>
-__global__ __launch_bounds__(64) void k_silu_pieces(const float* __restrict__ part, int splits, int m, int I,
-                                                    void* __restrict__ out, float* __restrict__ xs, int passes,
-                                                    float* __restrict__ act_out) {
-    const int kb = blockIdx.x, pass = blockIdx.y, lane = threadIdx.x;
-    const int c = lane & 15, row = pass * 4 + (c >> 2), piece = c & 3;
-    const int k0 = kb * 32 + (lane >> 4) * 8;
-    const size_t ld = (size_t)2 * I;
-    float v[8];
-#pragma unroll
-    for (int s = 0; s < 8; s++) {
-        const int k = k0 + s;
-        float t = 0.0f;
-        if (row < m && k < I) {
-            float gs = 0.0f, us = 0.0f;
-            for (int sp = 0; sp < splits; sp++) {
-                const float* pr = part + ((size_t)sp * m + row) * ld;
-                gs += pr[k];
-                us += pr[I + k];
-            }
-            t = gs / (1.0f + dev_exp(-gs)) * us;
-            if (act_out && piece == 0) act_out[(size_t)row * I + k] = t;
-        }
-        v[s] = t;
-    }
-    write_pieces<CK>(v, kb, pass, passes, row, piece, lane, out, xs);
-}
-
-void launch_silu_pieces(hipStream_t st, const float* partials, int splits, int m, int I, Pieces& out,
-                        float* act_out, int consumer_kind);
 
 // ---------------------------------------------------------------------------
-// GEMV / skinny GEMM: partial[split][row][n] = sum over the split's k-blocks
-// of x[row] . W[n]. One wave per NT tiles of 16 outputs; the wave keeps the
-// activation operand of a 4-k-block chunk in registers and streams the
-// tiles' weights through the MFMA B-operand.
+// Embedding gather (x = embed[token] as f32), the sum of squares of each
+// (k-block, row) for the first RMSNorm, and the first projection's pieces
+// of g * x. One wave per (k-block, pass).
+// ---------------------------------------------------------------------------
+template <int CK>
+__global__ __launch_bounds__(64) void k_embed(const uint32_t* __restrict__ tok, int stride,
+                                              const uint16_t* __restrict__ E, int m, int H,
+                                              const float* __restrict__ g, float* __restrict__ x,
+                                              float* __restrict__ ss, void* __restrict__ out,
+                                              float* __restrict__ xs, int passes) {
+    const int kb = blockIdx.x, pass = blockIdx.y, lane = threadIdx.x;
+    const int c = lane & 15, row = pass * 4 + (c >> 2), piece = c & 3, q = lane >> 4;
+    const int k0 = kb * 32 + q * 8;
+    float v[8];
+    const bool rv = row < m;
+    const uint16_t* e = rv ? E + (size_t)tok[(size_t)row * stride] * H : E;
+#pragma unroll
+    for (int s = 0; s < 8; s++) v[s] = (rv && k0 + s < H) ? bf16_bits_to_f32(e[k0 + s]) : 0.0f;
+    float sq = 0.0f;
+#pragma unroll
+    for (int s = 0; s < 8; s++) sq = fmaf(v[s], v[s], sq);
+    sq += __shfl_xor(sq, 16);
+    sq += __shfl_xor(sq, 32);
+    if (rv && piece == 0) {
+#pragma unroll
+        for (int s = 0; s < 8; s++)
+            if (k0 + s < H) x[(size_t)row * H + k0 + s] = v[s];
+        if (q == 0 && kb * 32 < H) ss[(size_t)kb * m + row] = sq;
+    }
+    float gv[8];
+#pragma unroll
+    for (int s = 0; s < 8; s++) gv[s] = (k0 + s < H && g) ? g[k0 + s] * v[s] : v[s];
+    write_pieces<CK>(gv, kb, pass, passes, row, piece, lane, out, xs);
+}
+
+void launch_embed(hipStream_t st, const uint32_t* tokens, int stride, const uint16_t* embed, int m, int H,
+                  const float* g, float* x, float* ss, int consumer_kind, Pieces& out) {
+    if (m <= 0) return;
+    dim3 grid(out.kb, out.passes);
+    if (consumer_kind == BF16)
+        hipLaunchKernelGGL(k_embed<BF16>, grid, dim3(64), 0, st, tokens, stride, embed, m, H, g, x, ss, out.a,
+                           out.xs, out.passes);
+    else
+        hipLaunchKernelGGL(k_embed<INT8>, grid, dim3(64), 0, st, tokens, stride, embed, m, H, g, x, ss, out.a,
+                           out.xs, out.passes);
+}
+
+// ---------------------------------------------------------------------------
+// GEMV / skinny GEMM over up to 16 activation rows per workgroup (grid.z
+// walks groups of 4 passes). A workgroup owns NT n-tiles (16*NT output
+// rows) and the whole input: its waves split the 4-k-block chunks, keep the
+// activation operand of U chunks in registers, stream the weights through
+// the MFMA B-operand and reduce across waves in LDS.
 //   int4/int8: v_mfma_i32_16x16x32_i8, one MFMA per (tile, k-block, pass),
 //     then the group's scale: acc += (D0 + D1/128 + D2/128^2 + D3/128^3) *
 //     s_w[n][kb] * s_x[row][kb].
@@ -232,460 +214,562 @@ void launch_silu_pieces(hipStream_t st, const float* partials, int splits, int m
 // D layout of a 16x16 MFMA: lane l holds rows 4*(l/16)+r (r = 0..3, the
 // four pieces of activation row l/16 of the pass) of column l%16 (output n).
 // ---------------------------------------------------------------------------
-template <int KIND, int NT, int PASSES>
-__global__ __launch_bounds__(256) void k_gemv(const uint8_t* __restrict__ W, const float* __restrict__ S,
-                                              const uint8_t* __restrict__ XA, const float* __restrict__ XS,
-                                              float* __restrict__ out, int N, int KB, int n_tiles,
-                                              int kb_per_split, int m, int p_total) {
-    constexpr bool Q = KIND != BF16;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int tile0 = (blockIdx.x * 4 + wave) * NT;
-    if (tile0 >= n_tiles) return;
-    const int split = blockIdx.y;
-    const int kb0 = split * kb_per_split;
-    const int kb1 = min(kb0 + kb_per_split, KB);
-    const int pass0 = blockIdx.z * PASSES;
-    const int np = min(PASSES, p_total - pass0);
-    const int KC = KB >> 2;
+constexpr int YS = 64;  // row stride of the output tile in LDS
 
-    float accq[NT][PASSES];
-    f32x4 accb[NT][PASSES];
+template <int KIND, int NT, int EPI, int PG>
+__global__ __launch_bounds__(1024) void k_gemv(const GemvArgs a) {
+    constexpr bool Q = KIND != BF16;
+    constexpr int U = PG == 1 ? 4 : 1;
+    constexpr bool NEED_R = EPI == EPI_QKV || EPI == EPI_SILU || EPI == EPI_ARGMAX;
+    __shared__ float red[32 * 4 * 64];
+    __shared__ float yt[16 * YS];
+    __shared__ float rs[16];
+    __shared__ float rtmp[16 * 17];
+
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, W = blockDim.x >> 6;
+    const int tile0 = blockIdx.x * NT;
+    const int pass0 = blockIdx.z * PG;
+    const int np = min(PG, a.p_total - pass0);
+    const int KB = a.KB, KC = KB >> 2;
+    const int c0 = wave * KC / W, c1 = (wave + 1) * KC / W;
+
+    if (NEED_R) {
+        // partial sums of the input rows' squares, folded after the main loop
+        for (int idx = threadIdx.x; idx < 256; idx += blockDim.x) {
+            const int r = idx >> 4, j = idx & 15, row = pass0 * 4 + r;
+            float s = 0.0f;
+            if (r < np * 4 && row < a.m) {
+                const int src = a.rows_src ? a.rows_src[row] : row;
+                for (int t = j; t < a.ss_tiles; t += 16) s += a.ss_in[(size_t)t * a.ss_m + src];
+            }
+            rtmp[r * 17 + j] = s;
+        }
+    }
+
+    // epilogue inputs, fetched now so their latency hides under the main loop
+    // (element it of this thread: idx = threadIdx.x + it * blockDim.x)
+    constexpr int COLS = NT * 16;
+    constexpr int EPI_IT = (16 * COLS + 63) / 64;
+    const int rows = np * 4;
+    float pre[EPI_IT];
+    float gpre[8];
+#pragma unroll
+    for (int it = 0; it < EPI_IT; it++) {
+        const int idx = threadIdx.x + it * blockDim.x;
+        pre[it] = 0.0f;
+        if (idx < rows * COLS) {
+            const int r = idx / COLS, cc = idx % COLS, row = pass0 * 4 + r;
+            if (EPI == EPI_RESID && row < a.m) pre[it] = a.x[(size_t)row * a.ldx + blockIdx.x * 32 + cc];
+            if ((EPI == EPI_QKV || EPI == EPI_STORE) && a.bias) pre[it] = a.bias[tile0 * 16 + cc];
+        }
+    }
+#pragma unroll
+    for (int s = 0; s < 8; s++)
+        gpre[s] = (EPI == EPI_RESID && a.g_next) ? a.g_next[blockIdx.x * 32 + (lane >> 4) * 8 + s] : 1.0f;
+
+    float accq[NT][PG];
+    f32x4 accb[NT][PG];
 #pragma unroll
     for (int t = 0; t < NT; t++)
 #pragma unroll
-        for (int p = 0; p < PASSES; p++) {
+        for (int p = 0; p < PG; p++) {
             accq[t][p] = 0.0f;
             accb[t][p] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
         }
     const i32x4 izero = {0, 0, 0, 0};
     const float inv128 = 0.0078125f;
 
-    for (int kb = kb0; kb < kb1; kb += 4) {
-        long aq[4][PASSES];
-        bf16x8 ab[4][PASSES];
-        float sx[4][PASSES];
+    for (int c = c0; c < c1; c += U) {
+        long aq[U][4][PG];
+        bf16x8 ab[U][4][PG];
+        float sx[U][4][PG];
+        u32x4 wq[U][NT][2];
+        bf16x8 wb[U][NT][4];
+        float4 sv[U][NT];
 #pragma unroll
-        for (int j = 0; j < 4; j++)
-#pragma unroll
-            for (int p = 0; p < PASSES; p++) {
-                if (p < np) {
-                    const size_t idx = ((size_t)(kb + j) * p_total + pass0 + p) * 64 + lane;
-                    if (Q) {
-                        aq[j][p] = ((const long*)XA)[idx];
-                        sx[j][p] = XS[(size_t)(kb + j) * p_total * 4 + (pass0 + p) * 4 + (lane >> 4)];
-                    } else {
-                        ab[j][p] = ((const bf16x8*)XA)[idx];
-                    }
-                }
-            }
-#pragma unroll
-        for (int t = 0; t < NT; t++) {
-            const int tile = tile0 + t;
-            if (tile >= n_tiles) break;
-            if (KIND == INT4 || KIND == INT8) {
-                const float4 sv = ((const float4*)S)[((size_t)tile * KC + (kb >> 2)) * 16 + (lane & 15)];
-                const float svj[4] = {sv.x, sv.y, sv.z, sv.w};
-                long bq[4];
-                if (KIND == INT4) {
-                    const u32x4 wv = ((const u32x4*)W)[((size_t)tile * KC + (kb >> 2)) * 64 + lane];
-#pragma unroll
-                    for (int j = 0; j < 4; j++) {
-                        const uint32_t w = wv[j];
-                        const uint32_t lo = (w << 4) & 0xF0F0F0F0u, hi = w & 0xF0F0F0F0u;
-                        bq[j] = (long)(((uint64_t)hi << 32) | lo);
-                    }
-                } else {
-                    const u32x4 w01 = ((const u32x4*)W)[((size_t)tile * (KB >> 1) + (kb >> 1)) * 64 + lane];
-                    const u32x4 w23 = ((const u32x4*)W)[((size_t)tile * (KB >> 1) + (kb >> 1) + 1) * 64 + lane];
-                    bq[0] = (long)(((uint64_t)w01[1] << 32) | w01[0]);
-                    bq[1] = (long)(((uint64_t)w01[3] << 32) | w01[2]);
-                    bq[2] = (long)(((uint64_t)w23[1] << 32) | w23[0]);
-                    bq[3] = (long)(((uint64_t)w23[3] << 32) | w23[2]);
-                }
+        for (int u = 0; u < U; u++) {
+            const int cc = c + u;
+            if (cc < c1) {
+                const int kb = cc * 4;
 #pragma unroll
                 for (int j = 0; j < 4; j++)
 #pragma unroll
-                    for (int p = 0; p < PASSES; p++) {
+                    for (int p = 0; p < PG; p++)
                         if (p < np) {
-                            const i32x4 d = __builtin_amdgcn_mfma_i32_16x16x32_i8(aq[j][p], bq[j], izero, 0, 0, 0);
-                            float comb = fmaf((float)d[3], inv128, (float)d[2]);
-                            comb = fmaf(comb, inv128, (float)d[1]);
-                            comb = fmaf(comb, inv128, (float)d[0]);
-                            accq[t][p] = fmaf(comb, svj[j] * sx[j][p], accq[t][p]);
+                            const size_t idx = ((size_t)(kb + j) * a.p_total + pass0 + p) * 64 + lane;
+                            if (Q) {
+                                aq[u][j][p] = ((const long*)a.XA)[idx];
+                                sx[u][j][p] = a.XS[(size_t)(kb + j) * a.p_total * 4 + (pass0 + p) * 4 + (lane >> 4)];
+                            } else {
+                                ab[u][j][p] = ((const bf16x8*)a.XA)[idx];
+                            }
                         }
+#pragma unroll
+                for (int t = 0; t < NT; t++) {
+                    const size_t tile = tile0 + t;
+                    if (KIND == INT4) {
+                        wq[u][t][0] = ((const u32x4*)a.W)[(tile * KC + cc) * 64 + lane];
+                    } else if (KIND == INT8) {
+                        wq[u][t][0] = ((const u32x4*)a.W)[(tile * (KB >> 1) + 2 * cc) * 64 + lane];
+                        wq[u][t][1] = ((const u32x4*)a.W)[(tile * (KB >> 1) + 2 * cc + 1) * 64 + lane];
+                    } else {
+#pragma unroll
+                        for (int j = 0; j < 4; j++) wb[u][t][j] = ((const bf16x8*)a.W)[(tile * KB + kb + j) * 64 + lane];
                     }
-            } else {
-                bf16x8 wb[4];
+                    if (Q) sv[u][t] = ((const float4*)a.S)[(tile * KC + cc) * 16 + (lane & 15)];
+                }
+            }
+        }
 #pragma unroll
-                for (int j = 0; j < 4; j++) wb[j] = ((const bf16x8*)W)[((size_t)tile * KB + kb + j) * 64 + lane];
+        for (int u = 0; u < U; u++) {
+            if (c + u >= c1) break;
 #pragma unroll
-                for (int j = 0; j < 4; j++)
+            for (int t = 0; t < NT; t++) {
+                if (Q) {
+                    const float svj[4] = {sv[u][t].x, sv[u][t].y, sv[u][t].z, sv[u][t].w};
+                    long bq[4];
+                    if (KIND == INT4) {
 #pragma unroll
-                    for (int p = 0; p < PASSES; p++)
-                        if (p < np)
-                            accb[t][p] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ab[j][p], wb[j], accb[t][p], 0, 0, 0);
+                        for (int j = 0; j < 4; j++) {
+                            const uint32_t w = wq[u][t][0][j];
+                            const uint32_t lo = (w << 4) & 0xF0F0F0F0u, hi = w & 0xF0F0F0F0u;
+                            bq[j] = (long)(((uint64_t)hi << 32) | lo);
+                        }
+                    } else {
+                        bq[0] = (long)(((uint64_t)wq[u][t][0][1] << 32) | wq[u][t][0][0]);
+                        bq[1] = (long)(((uint64_t)wq[u][t][0][3] << 32) | wq[u][t][0][2]);
+                        bq[2] = (long)(((uint64_t)wq[u][t][1][1] << 32) | wq[u][t][1][0]);
+                        bq[3] = (long)(((uint64_t)wq[u][t][1][3] << 32) | wq[u][t][1][2]);
+                    }
+#pragma unroll
+                    for (int j = 0; j < 4; j++)
+#pragma unroll
+                        for (int p = 0; p < PG; p++)
+                            if (p < np) {
+                                const i32x4 d = __builtin_amdgcn_mfma_i32_16x16x32_i8(aq[u][j][p], bq[j], izero, 0, 0, 0);
+                                float comb = fmaf((float)d[3], inv128, (float)d[2]);
+                                comb = fmaf(comb, inv128, (float)d[1]);
+                                comb = fmaf(comb, inv128, (float)d[0]);
+                                accq[t][p] = fmaf(comb, svj[j] * sx[u][j][p], accq[t][p]);
+                            }
+                } else {
+#pragma unroll
+                    for (int j = 0; j < 4; j++)
+#pragma unroll
+                        for (int p = 0; p < PG; p++)
+                            if (p < np)
+                                accb[t][p] =
+                                    __builtin_amdgcn_mfma_f32_16x16x32_bf16(ab[u][j][p], wb[u][t][j], accb[t][p], 0, 0, 0);
+                }
             }
         }
     }
+
+    // reduce across waves
 #pragma unroll
-    for (int t = 0; t < NT; t++) {
-        const int tile = tile0 + t;
-        if (tile >= n_tiles) break;
+    for (int t = 0; t < NT; t++)
 #pragma unroll
-        for (int p = 0; p < PASSES; p++) {
-            const int row = (pass0 + p) * 4 + (lane >> 4);
-            if (p < np && row < m) {
-                const float v = Q ? accq[t][p] : ((accb[t][p][0] + accb[t][p][1]) + accb[t][p][2]) + accb[t][p][3];
-                out[((size_t)split * m + row) * N + tile * 16 + (lane & 15)] = v;
+        for (int p = 0; p < PG; p++)
+            if (p < np)
+                red[((wave * NT + t) * 4 + p) * 64 + lane] =
+                    Q ? accq[t][p] : ((accb[t][p][0] + accb[t][p][1]) + accb[t][p][2]) + accb[t][p][3];
+    __syncthreads();
+    if (NEED_R && threadIdx.x < 16) {
+        float s = 0.0f;
+        for (int j = 0; j < 16; j++) s += rtmp[threadIdx.x * 17 + j];
+        rs[threadIdx.x] = 1.0f / sqrtf(s / (float)a.hidden + a.eps);
+    }
+    for (int idx = threadIdx.x; idx < NT * np * 64; idx += blockDim.x) {
+        const int t = idx / (np * 64), rem = idx % (np * 64), p = rem >> 6, l = rem & 63;
+        float v = 0.0f;
+        for (int w = 0; w < W; w++) v += red[((w * NT + t) * 4 + p) * 64 + l];
+        yt[(p * 4 + (l >> 4)) * YS + t * 16 + (l & 15)] = v;
+    }
+    __syncthreads();
+
+    if (EPI == EPI_STORE || EPI == EPI_QKV) {
+#pragma unroll
+        for (int it = 0; it < EPI_IT; it++) {
+            const int idx = threadIdx.x + it * blockDim.x;
+            if (idx < rows * COLS) {
+                const int r = idx / COLS, cc = idx % COLS, row = pass0 * 4 + r, col = tile0 * 16 + cc;
+                if (row < a.m) {
+                    float v = yt[r * YS + cc];
+                    if (EPI == EPI_QKV) v *= rs[r];
+                    if (a.bias) v += pre[it];
+                    a.out[(size_t)row * a.ldo + col] = v;
+                }
             }
         }
-    }
-}
-
-static int nt_for(int kind) { return kind == INT4 ? 4 : 2; }
-
-GemvPlan plan_gemv(const DMat& w, int m) {
-    GemvPlan p;
-    const int nt = nt_for(w.kind);
-    const int p_total = (m + 3) / 4;
-    const int pg = (p_total + 3) / 4;
-    const int groups = (w.n_tiles + nt * 4 - 1) / (nt * 4);
-    const int waves = groups * 4 * pg;
-    const int chunks = w.kb / 4;
-    const int want = 2048;
-    int splits = want / (waves > 0 ? waves : 1);
-    splits = splits < 1 ? 1 : splits;
-    splits = splits > 16 ? 16 : splits;
-    splits = splits > chunks ? chunks : splits;
-    const int cps = (chunks + splits - 1) / splits;
-    p.splits = (chunks + cps - 1) / cps;
-    return p;
-}
-
-template <int KIND, int NT>
-static void gemv_dispatch(hipStream_t st, const DMat& w, const Pieces& x, int m, int splits, float* out) {
-    const int p_total = x.passes;
-    const int chunks = w.kb / 4;
-    const int cps = (chunks + splits - 1) / splits;
-    const int groups = (w.n_tiles + NT * 4 - 1) / (NT * 4);
-    const uint8_t* W = (const uint8_t*)w.w;
-    const uint8_t* XA = (const uint8_t*)x.a;
-    if (p_total == 1) {
-        hipLaunchKernelGGL((k_gemv<KIND, NT, 1>), dim3(groups, splits, 1), dim3(256), 0, st, W, w.s, XA, x.xs, out,
-                           w.rows, w.kb, w.n_tiles, cps * 4, m, p_total);
-    } else if (p_total == 2) {
-        hipLaunchKernelGGL((k_gemv<KIND, NT, 2>), dim3(groups, splits, 1), dim3(256), 0, st, W, w.s, XA, x.xs, out,
-                           w.rows, w.kb, w.n_tiles, cps * 4, m, p_total);
-    } else {
-        hipLaunchKernelGGL((k_gemv<KIND, NT, 4>), dim3(groups, splits, (p_total + 3) / 4), dim3(256), 0, st, W, w.s,
-                           XA, x.xs, out, w.rows, w.kb, w.n_tiles, cps * 4, m, p_total);
-    }
-}
-
-void launch_gemv(hipStream_t st, const DMat& w, const Pieces& x, int m, const GemvPlan& plan, float* partials) {
-    if (m <= 0) return;
-    if (w.kind == INT4)
-        gemv_dispatch<INT4, 4>(st, w, x, m, plan.splits, partials);
-    else if (w.kind == INT8)
-        gemv_dispatch<INT8, 2>(st, w, x, m, plan.splits, partials);
-    else
-        gemv_dispatch<BF16, 2>(st, w, x, m, plan.splits, partials);
-}
-
-void launch_silu_pieces(hipStream_t st, const float* partials, int splits, int m, int I, Pieces& out,
-                        float* act_out, int consumer_kind) {
-    dim3 grid(out.kb, out.passes);
-    if (consumer_kind == BF16)
-        hipLaunchKernelGGL(k_silu_pieces<BF16>, grid, dim3(64), 0, st, partials, splits, m, I, out.a, out.xs,
-                           out.passes, act_out);
-    else
-        hipLaunchKernelGGL(k_silu_pieces<INT8>, grid, dim3(64), 0, st, partials, splits, m, I, out.a, out.xs,
-                           out.passes, act_out);
-}
-
-// Sum of partials (+ bias, added after the product as the reference does,
-// src/kernels.rs:268-274).
-__global__ __launch_bounds__(256) void k_reduce(const float* __restrict__ part, int splits, int m, int N,
-                                                const float* __restrict__ bias, float* __restrict__ y) {
-    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
-    if (i >= (size_t)m * N) return;
-    float v = 0.0f;
-    for (int s = 0; s < splits; s++) v += part[(size_t)s * m * N + i];
-    if (bias) v += bias[i % N];
-    y[i] = v;
-}
-
-void launch_reduce(hipStream_t st, const float* partials, int splits, int m, int N, const float* bias, float* y) {
-    const size_t n = (size_t)m * N;
-    if (!n) return;
-    hipLaunchKernelGGL(k_reduce, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, partials, splits, m, N, bias, y);
-}
-
-// ---------------------------------------------------------------------------
-// RoPE on q and k heads (rotate-half, src/model.rs:451-459) from the qkv
-// GEMV's partials (+ bias), q to q_out, k and v into the paged cache slot
-// (KvCache::write, src/kv.rs:48-56). Grid (rows, nh + 2*nkv), hd/2 threads.
-// ---------------------------------------------------------------------------
-__global__ void k_rope_kv(const float* __restrict__ part, int splits, int m, const float* __restrict__ bias,
-                          const int32_t* __restrict__ row_pos, const int32_t* __restrict__ row_slot,
-                          const float* __restrict__ cos_t, const float* __restrict__ sin_t, int nh, int nkv, int hd,
-                          int bs, float* __restrict__ q_out, float* __restrict__ kc, float* __restrict__ vc) {
-    const int r = blockIdx.x, h = blockIdx.y, i = threadIdx.x, half = hd >> 1;
-    const int N = (nh + 2 * nkv) * hd;
-    const int ca = h * hd + i, cb = ca + half;
-    float a = 0.0f, b = 0.0f;
-    for (int s = 0; s < splits; s++) {
-        const float* pr = part + ((size_t)s * m + r) * N;
-        a += pr[ca];
-        b += pr[cb];
-    }
-    if (bias) {
-        a += bias[ca];
-        b += bias[cb];
-    }
-    if (h < nh + nkv) {
-        const int pos = row_pos[r];
-        const float c = cos_t[(size_t)pos * half + i], sn = sin_t[(size_t)pos * half + i];
-        const float a2 = __fadd_rn(__fmul_rn(a, c), __fmul_rn(-b, sn));
-        const float b2 = __fadd_rn(__fmul_rn(b, c), __fmul_rn(a, sn));
-        a = a2;
-        b = b2;
-    }
-    if (h < nh) {
-        float* q = q_out + (size_t)r * nh * hd + (size_t)h * hd;
-        q[i] = a;
-        q[i + half] = b;
         return;
     }
-    const int slot = row_slot[r];
-    const int blk = slot / bs, o = slot % bs;
-    const bool is_k = h < nh + nkv;
-    const int kh = is_k ? h - nh : h - nh - nkv;
-    float* dst = (is_k ? kc : vc) + (((size_t)blk * nkv + kh) * bs + o) * hd;
-    dst[i] = a;
-    dst[i + half] = b;
+    if (EPI == EPI_RESID) {
+        // 32 output columns: one k-block of the next consumer
+        const int col0 = blockIdx.x * 32;
+#pragma unroll
+        for (int it = 0; it < EPI_IT; it++) {
+            const int idx = threadIdx.x + it * blockDim.x;
+            if (idx < rows * 32) {
+                const int r = idx >> 5, cc = idx & 31, row = pass0 * 4 + r;
+                float v = 0.0f;
+                if (row < a.m) {
+                    v = pre[it] + yt[r * YS + cc];
+                    a.x[(size_t)row * a.ldx + col0 + cc] = v;
+                }
+                yt[r * YS + cc] = v;
+            }
+        }
+        __syncthreads();
+        if (threadIdx.x < rows) {
+            const int row = pass0 * 4 + threadIdx.x;
+            if (row < a.m) {
+                float s = 0.0f;
+                for (int cc = 0; cc < 32; cc++) s = fmaf(yt[threadIdx.x * YS + cc], yt[threadIdx.x * YS + cc], s);
+                a.ss_out[(size_t)blockIdx.x * a.ss_m + row] = s;
+            }
+        }
+    } else if (EPI == EPI_SILU) {
+        // columns 0..31 gate, 32..63 up of 32 intermediate channels
+        for (int idx = threadIdx.x; idx < rows * 32; idx += blockDim.x) {
+            const int r = idx >> 5, cc = idx & 31;
+            const float gt = yt[r * YS + cc] * rs[r], up = yt[r * YS + 32 + cc] * rs[r];
+            yt[r * YS + cc] = gt / (1.0f + dev_exp(-gt)) * up;
+        }
+        __syncthreads();
+    } else if (EPI == EPI_ARGMAX) {
+        for (int idx = threadIdx.x; idx < rows * 32; idx += blockDim.x) {
+            const int r = idx >> 5, cc = idx & 31, row = pass0 * 4 + r, col = tile0 * 16 + cc;
+            const float v = yt[r * YS + cc] * rs[r];
+            if (row < a.m && a.logits) a.logits[(size_t)row * a.N + col] = v;
+            yt[r * YS + cc] = v != v ? -INFINITY : v;
+        }
+        __syncthreads();
+        if (threadIdx.x < rows) {
+            const int row = pass0 * 4 + threadIdx.x;
+            if (row < a.m) {
+                float bv = yt[threadIdx.x * YS];
+                int bi = 0;
+                for (int cc = 1; cc < 32; cc++)
+                    if (yt[threadIdx.x * YS + cc] > bv) {
+                        bv = yt[threadIdx.x * YS + cc];
+                        bi = cc;
+                    }
+                a.best[(size_t)blockIdx.x * a.m + row] = make_float2(bv, __int_as_float(tile0 * 16 + bi));
+            }
+        }
+        return;
+    }
+    // EPI_RESID / EPI_SILU: the next consumer's pieces for k-block blockIdx.x
+    if (!a.pa) return;
+    for (int p = wave; p < np; p += W) {
+        const int c = lane & 15, r = p * 4 + (c >> 2), piece = c & 3, q = lane >> 4;
+        const int row = pass0 * 4 + r;
+        float v[8];
+#pragma unroll
+        for (int s = 0; s < 8; s++) {
+            const int cc = q * 8 + s;
+            float t = row < a.m ? yt[r * YS + cc] : 0.0f;
+            if (EPI == EPI_RESID && a.g_next) t = gpre[s] * t;
+            v[s] = t;
+        }
+        write_pieces_kind(a.pa_kind, v, blockIdx.x, pass0 + p, a.pa_passes, row, piece, lane, a.pa, a.pxs);
+    }
+    // the consumer's zero padding past the last k-block
+    if (blockIdx.x == gridDim.x - 1)
+        for (int kb2 = gridDim.x; kb2 < a.pa_kb; kb2++)
+            for (int p = wave; p < np; p += W) {
+                const int c = lane & 15;
+                const float z[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+                write_pieces_kind(a.pa_kind, z, kb2, pass0 + p, a.pa_passes, pass0 * 4 + p * 4 + (c >> 2), c & 3, lane,
+                                  a.pa, a.pxs);
+            }
 }
 
-void launch_rope_kv(hipStream_t st, const float* partials, int splits, int m, const float* bias,
-                    const int32_t* row_pos, const int32_t* row_slot, const float* cos_t, const float* sin_t, int nh,
-                    int nkv, int hd, int bs, float* q_out, float* kc, float* vc) {
-    if (m <= 0) return;
-    hipLaunchKernelGGL(k_rope_kv, dim3(m, nh + 2 * nkv), dim3(hd / 2), 0, st, partials, splits, m, bias, row_pos,
-                       row_slot, cos_t, sin_t, nh, nkv, hd, bs, q_out, kc, vc);
+template <class K>
+static void launch_timed(K kernel, dim3 grid, dim3 block, hipStream_t st, const GemvArgs& a, hipEvent_t e0,
+                         hipEvent_t e1) {
+    if (e0 && e1)
+        hipExtLaunchKernelGGL(kernel, grid, block, 0, st, e0, e1, 0, a);
+    else
+        hipLaunchKernelGGL(kernel, grid, block, 0, st, a);
+}
+
+template <int KIND, int NT, int EPI>
+static void gemv_pg(hipStream_t st, const DMat& w, const GemvArgs& a, hipEvent_t e0, hipEvent_t e1) {
+    const int groups = w.n_tiles / NT;
+    const int KC = w.kb / 4;
+    const int maxw = NT == 4 ? 8 : 16;
+    if (a.p_total == 1) {
+        int W = (4096 + groups - 1) / groups;
+        W = std::max(1, std::min(std::min(W, maxw), KC));
+        launch_timed(k_gemv<KIND, NT, EPI, 1>, dim3(groups, 1, 1), dim3(64 * W), st, a, e0, e1);
+    } else {
+        const int pg = (a.p_total + 3) / 4;
+        int W = (4096 + groups * pg - 1) / (groups * pg);
+        W = std::max(1, std::min(std::min(W, maxw), KC));
+        launch_timed(k_gemv<KIND, NT, EPI, 4>, dim3(groups, 1, pg), dim3(64 * W), st, a, e0, e1);
+    }
+}
+
+template <int KIND>
+static void gemv_kind(hipStream_t st, int epi, const DMat& w, const GemvArgs& a, hipEvent_t e0, hipEvent_t e1) {
+    switch (epi) {
+        case EPI_STORE: gemv_pg<KIND, 2, EPI_STORE>(st, w, a, e0, e1); break;
+        case EPI_QKV: gemv_pg<KIND, 2, EPI_QKV>(st, w, a, e0, e1); break;
+        case EPI_RESID: gemv_pg<KIND, 2, EPI_RESID>(st, w, a, e0, e1); break;
+        case EPI_SILU: gemv_pg<KIND, 4, EPI_SILU>(st, w, a, e0, e1); break;
+        case EPI_ARGMAX: gemv_pg<KIND, 2, EPI_ARGMAX>(st, w, a, e0, e1); break;
+    }
+}
+
+void launch_gemv(hipStream_t st, int epi, const DMat& w, const GemvArgs& a, hipEvent_t start, hipEvent_t stop) {
+    if (a.m <= 0) return;
+    if (w.kind == INT4)
+        gemv_kind<INT4>(st, epi, w, a, start, stop);
+    else if (w.kind == INT8)
+        gemv_kind<INT8>(st, epi, w, a, start, stop);
+    else
+        gemv_kind<BF16>(st, epi, w, a, start, stop);
 }
 
 // ---------------------------------------------------------------------------
 // Paged attention, split over the context (flash-decoding). A work item is
-// (row group, split of split_pos positions) x kv head: the rows of a group
-// are consecutive rows of one sequence (<= 16), their queries (rows x GQA
-// group) share every K/V block the item reads, and each row is causally
-// limited to positions <= its own. Partials (running max, sum, weighted
-// values) are merged by k_attn_merge.
+// (row group, span of P positions) x kv head: the rows of a group are
+// consecutive rows of one chunk (<= 16), their queries (rows x GQA group)
+// share the span's keys/values, loaded into LDS in one pass, and each row is
+// causally limited to positions <= its own. q and the chunk's new keys are
+// rotated here (rotate-half RoPE, src/model.rs:451-459); the new keys/values
+// come from the q/k/v rows and are written to the cache slot of their row by
+// the one item that covers it (KvCache::write, src/kv.rs:48-56). Each item
+// writes per query the span's max score, sum of exponentials and weighted
+// values; k_merge_pieces combines the spans.
 // ---------------------------------------------------------------------------
-constexpr int ATT_QMAX = 64;
-
-template <int HD>
+template <int HD, int P, int QM>
 __global__ __launch_bounds__(256) void k_attn(AttnArgs a) {
-    constexpr int QPW = ATT_QMAX / 4;
-    constexpr int DPL = (HD + 63) / 64;
-    constexpr int HQ = HD / 4;
-    __shared__ float qs[ATT_QMAX][HD];
-    __shared__ float ks[16][HD + 1];
-    __shared__ float vs[16][HD];
-    __shared__ int lim[ATT_QMAX];
+    constexpr int HALF = HD / 2;
+    __shared__ float ks[P][HD + 1];
+    __shared__ float vs[P][HD];
+    __shared__ float qs[QM][HD];
+    __shared__ float pr[QM][P];
+    __shared__ int lim[QM];
 
     const int wi = blockIdx.x, h = blockIdx.y;
     const int g = a.wi_group[wi], sidx = a.wi_split[wi];
     const int row0 = a.g_row0[g], nrows = a.g_nrows[g];
+    const int crow0 = a.g_crow0[g], cpos0 = a.g_cpos0[g];
     const uint32_t* table = a.tables + a.g_table[g];
     const int G = a.nh / a.nkv;
     const int Q = nrows * G;
     const int Lmax = a.row_pos[row0 + nrows - 1] + 1;
-    const int p0 = sidx * a.split_pos;
-    const int p1 = min(p0 + a.split_pos, Lmax);
+    const int p0 = sidx * P;
+    const int p1 = min(p0 + P, Lmax);
+    const int qd = a.nh * HD, kvd = a.nkv * HD;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
 
-    for (int i = threadIdx.x; i < Q * HD; i += 256) {
-        const int q = i / HD, d = i % HD, r = q / G, j = q % G;
-        qs[q][d] = a.q[(size_t)(row0 + r) * a.nh * HD + (size_t)(h * G + j) * HD + d];
-    }
-    for (int q = threadIdx.x; q < Q; q += 256) lim[q] = a.row_pos[row0 + q / G];
-    __syncthreads();
-
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int pp = lane & 15, qq = lane >> 4;
-    float mrun[QPW], lrun[QPW], o[QPW][DPL];
+    __shared__ uint32_t blks[P / 16];
+    if (tid < P / 16) blks[tid] = p0 + 16 * tid < p1 ? table[(p0 >> 4) + tid] : 0u;
+    for (int q = tid; q < Q; q += 256) lim[q] = a.row_pos[row0 + q / G];
+    // q, rotated: 4 (d, d + HALF) pairs per item
+    for (int i = tid; i < Q * (HALF / 4); i += 256) {
+        const int q = i / (HALF / 4), d = (i % (HALF / 4)) * 4, r = q / G, j = q % G, row = row0 + r;
+        const int pos = a.row_pos[row];
+        const float* src = a.qkv + (size_t)row * a.ld + (size_t)(h * G + j) * HD;
+        const float4 x1 = *(const float4*)(src + d), x2 = *(const float4*)(src + d + HALF);
+        const float4 c = *(const float4*)(a.cos_t + (size_t)pos * HALF + d);
+        const float4 sn = *(const float4*)(a.sin_t + (size_t)pos * HALF + d);
+        const float a1[4] = {x1.x, x1.y, x1.z, x1.w}, a2[4] = {x2.x, x2.y, x2.z, x2.w};
+        const float cc[4] = {c.x, c.y, c.z, c.w}, ss[4] = {sn.x, sn.y, sn.z, sn.w};
 #pragma unroll
-    for (int i = 0; i < QPW; i++) {
-        mrun[i] = -INFINITY;
-        lrun[i] = 0.0f;
-#pragma unroll
-        for (int d = 0; d < DPL; d++) o[i][d] = 0.0f;
-    }
-
-    for (int base = p0; base < p1; base += 16) {
-        const uint32_t blk = table[base >> 4];
-        const float4* kb = (const float4*)(a.kc + ((size_t)blk * a.nkv + h) * 16 * HD);
-        const float4* vb = (const float4*)(a.vc + ((size_t)blk * a.nkv + h) * 16 * HD);
-        for (int i = threadIdx.x; i < 16 * HD / 4; i += 256) {
-            const float4 k4 = kb[i], v4 = vb[i];
-            const int e = i * 4, row = e / HD, col = e % HD;
-            ks[row][col] = k4.x;
-            ks[row][col + 1] = k4.y;
-            ks[row][col + 2] = k4.z;
-            ks[row][col + 3] = k4.w;
-            *(float4*)&vs[row][col] = v4;
+        for (int e = 0; e < 4; e++) {
+            qs[q][d + e] = __fadd_rn(__fmul_rn(a1[e], cc[e]), __fmul_rn(-a2[e], ss[e]));
+            qs[q][d + HALF + e] = __fadd_rn(__fmul_rn(a2[e], cc[e]), __fmul_rn(a1[e], ss[e]));
         }
-        __syncthreads();
+    }
+    __syncthreads();
+    // keys (rotated when new) and values of the span, 16-byte loads
+    constexpr int KI = P * (HALF / 4);
 #pragma unroll
-        for (int qi = 0; qi < QPW; qi++) {
-            const int q = wave + 4 * qi;
-            if (q >= Q) break;
-            float part = 0.0f;
-#pragma unroll 8
-            for (int e = 0; e < HQ; e++) part = fmaf(qs[q][qq * HQ + e], ks[pp][qq * HQ + e], part);
-            part += __shfl_xor(part, 16);
-            part += __shfl_xor(part, 32);
-            float sc = part * a.scale;
-            const int pos = base + pp;
-            if (pos >= p1 || pos > lim[q]) sc = -INFINITY;
-            float bm = sc;
-            bm = fmaxf(bm, __shfl_xor(bm, 1));
-            bm = fmaxf(bm, __shfl_xor(bm, 2));
-            bm = fmaxf(bm, __shfl_xor(bm, 4));
-            bm = fmaxf(bm, __shfl_xor(bm, 8));
-            const float mnew = fmaxf(mrun[qi], bm);
-            if (mnew == -INFINITY) continue;
-            const float corr = mrun[qi] == -INFINITY ? 0.0f : dev_exp(mrun[qi] - mnew);
-            const float pr = sc == -INFINITY ? 0.0f : dev_exp(sc - mnew);
-            float bsum = pr;
-            bsum += __shfl_xor(bsum, 1);
-            bsum += __shfl_xor(bsum, 2);
-            bsum += __shfl_xor(bsum, 4);
-            bsum += __shfl_xor(bsum, 8);
-            lrun[qi] = fmaf(lrun[qi], corr, bsum);
-            float prj[16];
+    for (int it = 0; it < (KI + 255) / 256; it++) {
+        const int i = tid + it * 256;
+        if (i < KI) {
+            const int o = i / (HALF / 4), d = (i % (HALF / 4)) * 4, p = p0 + o;
+            float k1[4] = {0, 0, 0, 0}, k2[4] = {0, 0, 0, 0};
+            if (p < p1) {
+                if (p < cpos0) {
+                    const float* kp = a.kc + (((size_t)blks[o >> 4] * a.nkv + h) * 16 + (p & 15)) * HD;
+                    const float4 u = *(const float4*)(kp + d), w = *(const float4*)(kp + d + HALF);
+                    k1[0] = u.x; k1[1] = u.y; k1[2] = u.z; k1[3] = u.w;
+                    k2[0] = w.x; k2[1] = w.y; k2[2] = w.z; k2[3] = w.w;
+                } else {
+                    const float* src = a.qkv + (size_t)(crow0 + p - cpos0) * a.ld + qd + h * HD;
+                    const float4 u = *(const float4*)(src + d), w = *(const float4*)(src + d + HALF);
+                    const float4 c = *(const float4*)(a.cos_t + (size_t)p * HALF + d);
+                    const float4 sn = *(const float4*)(a.sin_t + (size_t)p * HALF + d);
+                    const float a1[4] = {u.x, u.y, u.z, u.w}, a2[4] = {w.x, w.y, w.z, w.w};
+                    const float cc[4] = {c.x, c.y, c.z, c.w}, ss[4] = {sn.x, sn.y, sn.z, sn.w};
 #pragma unroll
-            for (int j = 0; j < 16; j++) prj[j] = __shfl(pr, j);
-#pragma unroll
-            for (int dd = 0; dd < DPL; dd++) {
-                const int d = lane + 64 * dd;
-                if (d < HD) {
-                    float acc = o[qi][dd] * corr;
-#pragma unroll
-                    for (int j = 0; j < 16; j++) acc = fmaf(prj[j], vs[j][d], acc);
-                    o[qi][dd] = acc;
+                    for (int e = 0; e < 4; e++) {
+                        k1[e] = __fadd_rn(__fmul_rn(a1[e], cc[e]), __fmul_rn(-a2[e], ss[e]));
+                        k2[e] = __fadd_rn(__fmul_rn(a2[e], cc[e]), __fmul_rn(a1[e], ss[e]));
+                    }
                 }
             }
-            mrun[qi] = mnew;
-        }
-        __syncthreads();
-    }
 #pragma unroll
-    for (int qi = 0; qi < QPW; qi++) {
-        const int q = wave + 4 * qi;
-        if (q >= Q) break;
-        float* dst = a.part + (((size_t)wi * a.nkv + h) * ATT_QMAX + q) * (HD + 2);
+            for (int e = 0; e < 4; e++) {
+                ks[o][d + e] = k1[e];
+                ks[o][d + HALF + e] = k2[e];
+            }
+        }
+    }
+    constexpr int VI = P * (HD / 4);
+#pragma unroll
+    for (int it = 0; it < (VI + 255) / 256; it++) {
+        const int i = tid + it * 256;
+        if (i < VI) {
+            const int o = i / (HD / 4), d = (i % (HD / 4)) * 4, p = p0 + o;
+            float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            if (p < p1)
+                v = p < cpos0 ? *(const float4*)(a.vc + (((size_t)blks[o >> 4] * a.nkv + h) * 16 + (p & 15)) * HD + d)
+                              : *(const float4*)(a.qkv + (size_t)(crow0 + p - cpos0) * a.ld + qd + kvd + h * HD + d);
+            *(float4*)&vs[o][d] = v;
+        }
+    }
+    __syncthreads();
+    // this group's new rows in the span go to the cache
+    {
+        const int n0 = max(max(p0, cpos0), cpos0 + row0 - crow0);
+        const int n1 = min(p1, cpos0 + row0 + nrows - crow0);
+        for (int i = tid; i < (n1 - n0) * HD; i += 256) {
+            const int p = n0 + i / HD, d = i % HD, o = p - p0;
+            const size_t at = (((size_t)blks[o >> 4] * a.nkv + h) * 16 + (p & 15)) * HD + d;
+            a.kc[at] = ks[o][d];
+            a.vc[at] = vs[o][d];
+        }
+    }
+    // scores
+    for (int i = tid; i < Q * P; i += 256) {
+        const int q = i / P, o = i % P, p = p0 + o;
+        float sc = -INFINITY;
+        if (p < p1 && p <= lim[q]) {
+            float acc = 0.0f;
+#pragma unroll 16
+            for (int e = 0; e < HD; e++) acc = fmaf(qs[q][e], ks[o][e], acc);
+            sc = acc * a.scale;
+        }
+        pr[q][o] = sc;
+    }
+    __syncthreads();
+    // softmax statistics of each query over the span (one wave per query)
+    for (int q = wave; q < Q; q += 4) {
+        const float sc = lane < P ? pr[q][lane] : -INFINITY;
+        float mx = sc;
+        for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+        const float e = (sc == -INFINITY) ? 0.0f : dev_exp(sc - mx);
+        float sum = e;
+        for (int o = 32; o > 0; o >>= 1) sum += __shfl_xor(sum, o);
+        if (lane < P) pr[q][lane] = e;
         if (lane == 0) {
-            dst[0] = mrun[qi];
-            dst[1] = lrun[qi];
+            float* dst = a.part + (((size_t)wi * a.nkv + h) * QM + q) * (HD + 2);
+            dst[0] = mx;
+            dst[1] = sum;
         }
+    }
+    __syncthreads();
+    // weighted values
+    for (int i = tid; i < Q * HD; i += 256) {
+        const int q = i / HD, d = i % HD;
+        float acc = 0.0f;
+#pragma unroll 16
+        for (int o = 0; o < P; o++) acc = fmaf(pr[q][o], vs[o][d], acc);
+        a.part[(((size_t)wi * a.nkv + h) * QM + q) * (HD + 2) + 2 + d] = acc;
+    }
+}
+
+// Merge of the spans of each (row, head) into the attention output, written
+// as the output projection's pieces. One wave per (k-block, pass); the four
+// lanes of a (row, 8 dims) pair (one per piece) share the spans and combine
+// their sums in a fixed order.
+template <int HD, int QM, int CK>
+__global__ __launch_bounds__(64) void k_merge_pieces(AttnArgs a, int m, void* __restrict__ out, float* __restrict__ xs,
+                                                     int passes) {
+    const int kb = blockIdx.x, pass = blockIdx.y, lane = threadIdx.x;
+    const int c = lane & 15, row = pass * 4 + (c >> 2), piece = c & 3;
+    const int k0 = kb * 32 + (lane >> 4) * 8;
+    float v[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    if (row < m && k0 < a.nh * HD) {
+        const int hq = k0 / HD, d0 = k0 % HD;
+        const int g = a.row_group[row];
+        const int G = a.nh / a.nkv, h = hq / G, j = hq % G;
+        const int qi = (row - a.g_row0[g]) * G + j;
+        const int wi0 = a.g_wi0[g], ns = a.g_nsplit[g];
+        const size_t stride = (size_t)a.nkv * QM * (HD + 2);
+        const float* base = a.part + ((size_t)wi0 * a.nkv * QM + (size_t)h * QM + qi) * (HD + 2);
+        float M = -INFINITY;
+#pragma unroll 4
+        for (int s = piece; s < ns; s += 4) M = fmaxf(M, base[s * stride]);
+        M = fmaxf(M, __shfl_xor(M, 1));
+        M = fmaxf(M, __shfl_xor(M, 2));
+        float L = 0.0f, O[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+#pragma unroll 4
+        for (int s = piece; s < ns; s += 4) {
+            const float* p = base + s * stride;
+            const float ms = p[0];
+            if (ms == -INFINITY) continue;
+            const float w = dev_exp(ms - M);
+            L = fmaf(p[1], w, L);
 #pragma unroll
-        for (int dd = 0; dd < DPL; dd++)
-            if (lane + 64 * dd < HD) dst[2 + lane + 64 * dd] = o[qi][dd];
+            for (int e = 0; e < 8; e++) O[e] = fmaf(p[2 + d0 + e], w, O[e]);
+        }
+        L += __shfl_xor(L, 1);
+        L += __shfl_xor(L, 2);
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            O[e] += __shfl_xor(O[e], 1);
+            O[e] += __shfl_xor(O[e], 2);
+            v[e] = O[e] / L;
+        }
     }
+    write_pieces<CK>(v, kb, pass, passes, row, piece, lane, out, xs);
 }
 
-template <int HD>
-__global__ void k_attn_merge(AttnArgs a) {
-    const int row = blockIdx.x, hq = blockIdx.y, d = threadIdx.x;
-    const int g = a.row_group[row];
-    const int G = a.nh / a.nkv;
-    const int h = hq / G, j = hq % G;
-    const int q = (row - a.g_row0[g]) * G + j;
-    const int wi0 = a.g_wi0[g], ns = a.g_nsplit[g];
-    float M = -INFINITY;
-    for (int s = 0; s < ns; s++) M = fmaxf(M, a.part[(((size_t)(wi0 + s) * a.nkv + h) * ATT_QMAX + q) * (HD + 2)]);
-    float L = 0.0f, O = 0.0f;
-    for (int s = 0; s < ns; s++) {
-        const float* p = a.part + (((size_t)(wi0 + s) * a.nkv + h) * ATT_QMAX + q) * (HD + 2);
-        const float ms = p[0];
-        if (ms == -INFINITY) continue;
-        const float w = dev_exp(ms - M);
-        L = fmaf(p[1], w, L);
-        O = fmaf(p[2 + d], w, O);
-    }
-    a.out[(size_t)row * a.nh * HD + (size_t)hq * HD + d] = O / L;
+template <int HD, int P, int QM>
+static void attention_hd(hipStream_t st, const AttnArgs& a, int m, int ck, Pieces& out) {
+    hipLaunchKernelGGL((k_attn<HD, P, QM>), dim3(a.n_wi, a.nkv), dim3(256), 0, st, a);
+    if (ck == BF16)
+        hipLaunchKernelGGL((k_merge_pieces<HD, QM, BF16>), dim3(out.kb, out.passes), dim3(64), 0, st, a, m, out.a,
+                           out.xs, out.passes);
+    else
+        hipLaunchKernelGGL((k_merge_pieces<HD, QM, INT8>), dim3(out.kb, out.passes), dim3(64), 0, st, a, m, out.a,
+                           out.xs, out.passes);
 }
 
-void launch_attention(hipStream_t st, const AttnArgs& a, int m) {
+int attn_span(int hd) { return hd >= 128 ? 32 : 64; }
+int attn_qmax(int hd) { return hd >= 64 ? 32 : 64; }
+
+void launch_attention(hipStream_t st, const AttnArgs& a, int m, int consumer_kind, Pieces& out) {
     if (m <= 0 || a.n_wi <= 0) return;
     switch (a.hd) {
-        case 16:
-            hipLaunchKernelGGL(k_attn<16>, dim3(a.n_wi, a.nkv), dim3(256), 0, st, a);
-            hipLaunchKernelGGL(k_attn_merge<16>, dim3(m, a.nh), dim3(16), 0, st, a);
-            break;
-        case 32:
-            hipLaunchKernelGGL(k_attn<32>, dim3(a.n_wi, a.nkv), dim3(256), 0, st, a);
-            hipLaunchKernelGGL(k_attn_merge<32>, dim3(m, a.nh), dim3(32), 0, st, a);
-            break;
-        case 64:
-            hipLaunchKernelGGL(k_attn<64>, dim3(a.n_wi, a.nkv), dim3(256), 0, st, a);
-            hipLaunchKernelGGL(k_attn_merge<64>, dim3(m, a.nh), dim3(64), 0, st, a);
-            break;
-        case 128:
-            hipLaunchKernelGGL(k_attn<128>, dim3(a.n_wi, a.nkv), dim3(256), 0, st, a);
-            hipLaunchKernelGGL(k_attn_merge<128>, dim3(m, a.nh), dim3(128), 0, st, a);
-            break;
+        case 16: attention_hd<16, 64, 64>(st, a, m, consumer_kind, out); break;
+        case 32: attention_hd<32, 64, 64>(st, a, m, consumer_kind, out); break;
+        case 64: attention_hd<64, 64, 32>(st, a, m, consumer_kind, out); break;
+        case 128: attention_hd<128, 32, 32>(st, a, m, consumer_kind, out); break;
     }
 }
 
 // ---------------------------------------------------------------------------
-// Logits (sum of the lm_head GEMV's partials) and their argmax: first index
-// of the maximum, NaN never wins (sampler::argmax, src/sampler.rs:41-51).
+// Argmax over the per-tile (max, index) pairs: first index of the maximum,
+// NaN never wins (sampler::argmax, src/sampler.rs:41-51).
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ bool better(float v, int i, float bv, int bi) { return v > bv || (v == bv && i < bi); }
 
-__global__ __launch_bounds__(256) void k_argmax1(const float* __restrict__ part, int splits, int rows, int V,
-                                                 float* __restrict__ logits_out, float2* __restrict__ best,
-                                                 int nblk) {
-    __shared__ float sv[256];
-    __shared__ int si[256];
-    const int r = blockIdx.x, b = blockIdx.y;
-    const int per = (V + nblk - 1) / nblk;
-    const int i0 = b * per, i1 = min(i0 + per, V);
-    float bv = -INFINITY;
-    int bi = 0x7FFFFFFF;
-    for (int i = i0 + threadIdx.x; i < i1; i += 256) {
-        float v = 0.0f;
-        for (int s = 0; s < splits; s++) v += part[((size_t)s * rows + r) * V + i];
-        if (logits_out) logits_out[(size_t)r * V + i] = v;
-        if (v != v) v = -INFINITY;
-        if (better(v, i, bv, bi)) {
-            bv = v;
-            bi = i;
-        }
-    }
-    sv[threadIdx.x] = bv;
-    si[threadIdx.x] = bi;
-    __syncthreads();
-    for (int o = 128; o > 0; o >>= 1) {
-        if (threadIdx.x < o && better(sv[threadIdx.x + o], si[threadIdx.x + o], sv[threadIdx.x], si[threadIdx.x])) {
-            sv[threadIdx.x] = sv[threadIdx.x + o];
-            si[threadIdx.x] = si[threadIdx.x + o];
-        }
-        __syncthreads();
-    }
-    if (threadIdx.x == 0) best[(size_t)r * nblk + b] = make_float2(sv[0], __int_as_float(si[0]));
-}
-
-__global__ __launch_bounds__(64) void k_argmax2(const float2* __restrict__ best, int nblk,
-                                                uint32_t* __restrict__ am, uint32_t* __restrict__ aux,
-                                                int aux_stride, int aux_off) {
+__global__ __launch_bounds__(64) void k_argmax_final(const float2* __restrict__ best, int tiles, int rows,
+                                                     uint32_t* __restrict__ am, uint32_t* __restrict__ aux,
+                                                     int aux_stride, int aux_off) {
     const int r = blockIdx.x;
     float bv = -INFINITY;
     int bi = 0x7FFFFFFF;
-    for (int b = threadIdx.x; b < nblk; b += 64) {
-        const float2 e = best[(size_t)r * nblk + b];
+    for (int t = threadIdx.x; t < tiles; t += 64) {
+        const float2 e = best[(size_t)t * rows + r];
         const int i = __float_as_int(e.y);
         if (better(e.x, i, bv, bi)) {
             bv = e.x;
@@ -707,25 +791,11 @@ __global__ __launch_bounds__(64) void k_argmax2(const float2* __restrict__ best,
     }
 }
 
-void launch_argmax(hipStream_t st, const float* partials, int splits, int rows, int V, float* logits_out,
-                   float2* block_best, int nblk, uint32_t* argmax_out, uint32_t* aux, int aux_stride, int aux_off) {
+void launch_argmax_final(hipStream_t st, const float2* best, int tiles, int rows, uint32_t* argmax_out,
+                         uint32_t* aux, int aux_stride, int aux_off) {
     if (rows <= 0) return;
-    hipLaunchKernelGGL(k_argmax1, dim3(rows, nblk), dim3(256), 0, st, partials, splits, rows, V, logits_out,
-                       block_best, nblk);
-    hipLaunchKernelGGL(k_argmax2, dim3(rows), dim3(64), 0, st, block_best, nblk, argmax_out, aux, aux_stride,
+    hipLaunchKernelGGL(k_argmax_final, dim3(rows), dim3(64), 0, st, best, tiles, rows, argmax_out, aux, aux_stride,
                        aux_off);
-}
-
-__global__ __launch_bounds__(256) void k_gather_rows(const float* __restrict__ x, const int32_t* __restrict__ rows,
-                                                     int H, float* __restrict__ out) {
-    const int i = blockIdx.x;
-    const float* src = x + (size_t)rows[i] * H;
-    for (int c = threadIdx.x; c < H; c += 256) out[(size_t)i * H + c] = src[c];
-}
-
-void launch_gather_rows(hipStream_t st, const float* x, const int32_t* rows, int n, int H, float* out) {
-    if (n <= 0) return;
-    hipLaunchKernelGGL(k_gather_rows, dim3(n), dim3(256), 0, st, x, rows, H, out);
 }
 
 // Greedy accept-prefix: proposals d_1..d_k against the target's argmax of
@@ -736,20 +806,20 @@ __global__ void k_accept(const uint32_t* __restrict__ am, const uint32_t* __rest
                          int k, uint32_t* __restrict__ out, int32_t* __restrict__ cnt, int32_t* __restrict__ acc) {
     const int s = blockIdx.x * blockDim.x + threadIdx.x;
     if (s >= n_seqs) return;
-    const uint32_t* a = am + (size_t)s * (k + 1);
+    const uint32_t* am_s = am + (size_t)s * (k + 1);
     const uint32_t* d = verify_tokens + (size_t)s * (k + 1) + 1;
     uint32_t* o = out + (size_t)s * (k + 1);
     int n = 0, ac = 0;
     for (int j = 0; j < k; j++) {
-        if (a[j] == d[j]) {
+        if (am_s[j] == d[j]) {
             o[n++] = d[j];
             ac++;
         } else {
-            o[n++] = a[j];
+            o[n++] = am_s[j];
             break;
         }
     }
-    if (ac == k) o[n++] = a[k];
+    if (ac == k) o[n++] = am_s[k];
     cnt[s] = n;
     acc[s] = ac;
 }
@@ -759,16 +829,6 @@ void launch_accept(hipStream_t st, const uint32_t* argmax, const uint32_t* draft
     if (n_seqs <= 0) return;
     hipLaunchKernelGGL(k_accept, dim3((n_seqs + 63) / 64), dim3(64), 0, st, argmax, drafts, n_seqs, k, out_tokens,
                        out_count, out_accepted);
-}
-
-__global__ void k_copy_tokens(const uint32_t* __restrict__ src, int n, int ss, uint32_t* __restrict__ dst, int ds) {
-    const int i = blockIdx.x * blockDim.x + threadIdx.x;
-    if (i < n) dst[(size_t)i * ds] = src[(size_t)i * ss];
-}
-
-void launch_copy_tokens(hipStream_t st, const uint32_t* src, int n, int src_stride, uint32_t* dst, int dst_stride) {
-    if (n <= 0) return;
-    hipLaunchKernelGGL(k_copy_tokens, dim3((n + 63) / 64), dim3(64), 0, st, src, n, src_stride, dst, dst_stride);
 }
 
 }  // namespace fg
