@@ -217,9 +217,10 @@ void launch_embed(hipStream_t st, const uint32_t* tokens, int stride, const uint
 constexpr int YS = 64;  // row stride of the output tile in LDS
 
 template <int KIND, int NT, int EPI, int PG>
-__global__ __launch_bounds__(1024) void k_gemv(const GemvArgs a) {
+__global__ __launch_bounds__(512) void k_gemv(const GemvArgs a) {
     constexpr bool Q = KIND != BF16;
-    constexpr int U = PG == 1 ? 4 : 1;
+    // chunks loaded ahead per wave: about 16 B x 4 per lane and tile of weights in flight
+    constexpr int U = PG == 1 ? (KIND == BF16 ? 1 : KIND == INT8 ? 2 : 4) : 1;
     constexpr bool NEED_R = EPI == EPI_QKV || EPI == EPI_SILU || EPI == EPI_ARGMAX;
     __shared__ float red[32 * 4 * 64];
     __shared__ float yt[16 * YS];
@@ -498,10 +499,9 @@ template <int KIND, int NT, int EPI>
 static void gemv_pg(hipStream_t st, const DMat& w, const GemvArgs& a, hipEvent_t e0, hipEvent_t e1) {
     const int groups = w.n_tiles / NT;
     const int KC = w.kb / 4;
-    const int maxw = NT == 4 ? 8 : 16;
+    const int maxw = 8;  // waves per group: launch bounds of k_gemv
     if (a.p_total == 1) {
-        int W = (4096 + groups - 1) / groups;
-        W = std::max(1, std::min(std::min(W, maxw), KC));
+        const int W = std::max(1, std::min(maxw, KC));
         launch_timed(k_gemv<KIND, NT, EPI, 1>, dim3(groups, 1, 1), dim3(64 * W), st, a, e0, e1);
     } else {
         const int pg = (a.p_total + 3) / 4;
