@@ -66,16 +66,19 @@ template <int CK>
 __device__ __forceinline__ void write_pieces(const float (&v)[8], int kb, int pass, int passes, int row, int piece,
                                              int lane, void* out, float* xs) {
     if (CK == BF16) {
+        // all four pieces are formed and this lane's is selected (no branches)
         u16x8 o;
 #pragma unroll
         for (int s = 0; s < 8; s++) {
             float r = v[s];
-            uint32_t h = 0;
-            for (int p = 0; p <= piece; p++) {
-                h = f32_to_bf16_bits(r);
+            uint32_t h = f32_to_bf16_bits(r), sel = h;
+#pragma unroll
+            for (int p = 1; p < 4; p++) {
                 r = r - bf16_bits_to_f32(h);
+                h = f32_to_bf16_bits(r);
+                sel = p == piece ? h : sel;
             }
-            o[s] = (uint16_t)h;
+            o[s] = (uint16_t)sel;
         }
         ((u16x8*)out)[((size_t)kb * passes + pass) * 64 + lane] = o;
     } else {
@@ -95,12 +98,14 @@ __device__ __forceinline__ void write_pieces(const float (&v)[8], int kb, int pa
 #pragma unroll
         for (int s = 0; s < 8; s++) {
             float r = ldexpf(v[s], -e);  // exact
-            float a = rintf(r);
-            for (int p = 0; p < piece; p++) {
+            float a = rintf(r), sel = a;
+#pragma unroll
+            for (int p = 1; p < 4; p++) {
                 r = (r - a) * 128.0f;  // both exact
                 a = rintf(r);
+                sel = p == piece ? a : sel;
             }
-            o[s] = (int8_t)(int)a;
+            o[s] = (int8_t)(int)sel;
         }
         ((i8x8*)out)[((size_t)kb * passes + pass) * 64 + lane] = o;
         if (lane < 16 && (lane & 3) == 0) xs[(size_t)kb * passes * 4 + row] = ldexpf(1.0f, e);
@@ -220,12 +225,14 @@ template <int KIND, int NT, int EPI, int PG>
 __global__ __launch_bounds__(512) void k_gemv(const GemvArgs a) {
     constexpr bool Q = KIND != BF16;
     // chunks loaded ahead per wave: about 16 B x 4 per lane and tile of weights in flight
-    constexpr int U = PG == 1 ? (KIND == BF16 ? 1 : KIND == INT8 ? 2 : 4) : 1;
+    constexpr int U = PG == 1 ? (KIND == INT4 ? 4 : 2) : 1;
     constexpr bool NEED_R = EPI == EPI_QKV || EPI == EPI_SILU || EPI == EPI_ARGMAX;
     __shared__ float red[32 * 4 * 64];
-    __shared__ float yt[16 * YS];
+    __shared__ __align__(16) float yt[16 * YS];
     __shared__ float rs[16];
     __shared__ float rtmp[16 * 17];
+    __shared__ __align__(16) float et[16 * YS];  // epilogue inputs: x tile (EPI_RESID) or bias
+    __shared__ __align__(16) float gs[32];       // g_next of this group's 32 columns (EPI_RESID)
 
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, W = blockDim.x >> 6;
     const int tile0 = blockIdx.x * NT;
@@ -234,26 +241,45 @@ __global__ __launch_bounds__(512) void k_gemv(const GemvArgs a) {
     const int KB = a.KB, KC = KB >> 2;
     const int c0 = wave * KC / W, c1 = (wave + 1) * KC / W;
 
+    // 1/rms of the input rows from the producers' sum-of-squares partials
+    // ss_in[tile][row]: slot (row r, j) sums tiles j, j + 16, ... The fast path
+    // only issues the loads here, into registers, and folds them after the main
+    // loop so that their latency hides under the weight stream.
+    constexpr int RL = 8;
+    const int rslots = np * 64;
+    const bool rfast = rslots <= (int)blockDim.x && a.ss_tiles <= 16 * RL;
+    float rv[RL];
+#pragma unroll
+    for (int i = 0; i < RL; i++) rv[i] = 0.0f;
     if (NEED_R) {
-        // partial sums of the input rows' squares, folded after the main loop
-        for (int idx = threadIdx.x; idx < 256; idx += blockDim.x) {
-            const int r = idx >> 4, j = idx & 15, row = pass0 * 4 + r;
-            float s = 0.0f;
-            if (r < np * 4 && row < a.m) {
+        if (rfast) {
+            const int r = threadIdx.x >> 4, j = threadIdx.x & 15, row = pass0 * 4 + r;
+            if ((int)threadIdx.x < rslots && row < a.m) {
                 const int src = a.rows_src ? a.rows_src[row] : row;
-                for (int t = j; t < a.ss_tiles; t += 16) s += a.ss_in[(size_t)t * a.ss_m + src];
+#pragma unroll
+                for (int i = 0; i < RL; i++)
+                    if (j + 16 * i < a.ss_tiles) rv[i] = a.ss_in[(size_t)(j + 16 * i) * a.ss_m + src];
             }
-            rtmp[r * 17 + j] = s;
+        } else {
+            for (int idx = threadIdx.x; idx < 256; idx += blockDim.x) {
+                const int r = idx >> 4, j = idx & 15, row = pass0 * 4 + r;
+                float v = 0.0f;
+                if (r < np * 4 && row < a.m) {
+                    const int src = a.rows_src ? a.rows_src[row] : row;
+                    for (int t = j; t < a.ss_tiles; t += 16) v += a.ss_in[(size_t)t * a.ss_m + src];
+                }
+                rtmp[r * 17 + j] = v;
+            }
         }
     }
 
-    // epilogue inputs, fetched now so their latency hides under the main loop
-    // (element it of this thread: idx = threadIdx.x + it * blockDim.x)
+    // epilogue inputs (the x tile of EPI_RESID, the bias), fetched now so their
+    // latency hides under the main loop; element it of this thread is
+    // idx = threadIdx.x + it * blockDim.x
     constexpr int COLS = NT * 16;
     constexpr int EPI_IT = (16 * COLS + 63) / 64;
     const int rows = np * 4;
     float pre[EPI_IT];
-    float gpre[8];
 #pragma unroll
     for (int it = 0; it < EPI_IT; it++) {
         const int idx = threadIdx.x + it * blockDim.x;
@@ -264,9 +290,8 @@ __global__ __launch_bounds__(512) void k_gemv(const GemvArgs a) {
             if ((EPI == EPI_QKV || EPI == EPI_STORE) && a.bias) pre[it] = a.bias[tile0 * 16 + cc];
         }
     }
-#pragma unroll
-    for (int s = 0; s < 8; s++)
-        gpre[s] = (EPI == EPI_RESID && a.g_next) ? a.g_next[blockIdx.x * 32 + (lane >> 4) * 8 + s] : 1.0f;
+    float gv = 1.0f;
+    if (EPI == EPI_RESID && a.g_next && threadIdx.x < 32) gv = a.g_next[blockIdx.x * 32 + threadIdx.x];
 
     float accq[NT][PG];
     f32x4 accb[NT][PG];
@@ -366,6 +391,33 @@ __global__ __launch_bounds__(512) void k_gemv(const GemvArgs a) {
         }
     }
 
+    // Park the prologue's values in LDS. Their loads completed with the main
+    // loop's; reading them back from LDS later keeps the epilogue from waiting
+    // on its own global stores (stores and loads share one counter). The empty
+    // asm statements pin the first use of each value here, so the compiler
+    // neither folds it into the load's branch nor hoists the LDS write above
+    // the weight loads (either would wait on the load before the stream starts).
+#pragma unroll
+    for (int i = 0; i < RL; i++) asm volatile("" : "+v"(rv[i]));
+#pragma unroll
+    for (int it = 0; it < EPI_IT; it++) asm volatile("" : "+v"(pre[it]));
+    asm volatile("" : "+v"(gv));
+    if (NEED_R && rfast) {
+        float v = 0.0f;
+#pragma unroll
+        for (int i = 0; i < RL; i++) v += rv[i];
+        for (int idx = threadIdx.x; idx < 256; idx += blockDim.x)
+            rtmp[(idx >> 4) * 17 + (idx & 15)] = idx == (int)threadIdx.x ? v : 0.0f;
+    }
+    if (EPI == EPI_RESID || ((EPI == EPI_QKV || EPI == EPI_STORE) && a.bias)) {
+#pragma unroll
+        for (int it = 0; it < EPI_IT; it++) {
+            const int idx = threadIdx.x + it * blockDim.x;
+            if (idx < rows * COLS) et[(idx / COLS) * YS + idx % COLS] = pre[it];
+        }
+    }
+    if (EPI == EPI_RESID && threadIdx.x < 32) gs[threadIdx.x] = gv;
+
     // reduce across waves
 #pragma unroll
     for (int t = 0; t < NT; t++)
@@ -397,47 +449,14 @@ __global__ __launch_bounds__(512) void k_gemv(const GemvArgs a) {
                 if (row < a.m) {
                     float v = yt[r * YS + cc];
                     if (EPI == EPI_QKV) v *= rs[r];
-                    if (a.bias) v += pre[it];
+                    if (a.bias) v += et[r * YS + cc];
                     a.out[(size_t)row * a.ldo + col] = v;
                 }
             }
         }
         return;
     }
-    if (EPI == EPI_RESID) {
-        // 32 output columns: one k-block of the next consumer
-        const int col0 = blockIdx.x * 32;
-#pragma unroll
-        for (int it = 0; it < EPI_IT; it++) {
-            const int idx = threadIdx.x + it * blockDim.x;
-            if (idx < rows * 32) {
-                const int r = idx >> 5, cc = idx & 31, row = pass0 * 4 + r;
-                float v = 0.0f;
-                if (row < a.m) {
-                    v = pre[it] + yt[r * YS + cc];
-                    a.x[(size_t)row * a.ldx + col0 + cc] = v;
-                }
-                yt[r * YS + cc] = v;
-            }
-        }
-        __syncthreads();
-        if (threadIdx.x < rows) {
-            const int row = pass0 * 4 + threadIdx.x;
-            if (row < a.m) {
-                float s = 0.0f;
-                for (int cc = 0; cc < 32; cc++) s = fmaf(yt[threadIdx.x * YS + cc], yt[threadIdx.x * YS + cc], s);
-                a.ss_out[(size_t)blockIdx.x * a.ss_m + row] = s;
-            }
-        }
-    } else if (EPI == EPI_SILU) {
-        // columns 0..31 gate, 32..63 up of 32 intermediate channels
-        for (int idx = threadIdx.x; idx < rows * 32; idx += blockDim.x) {
-            const int r = idx >> 5, cc = idx & 31;
-            const float gt = yt[r * YS + cc] * rs[r], up = yt[r * YS + 32 + cc] * rs[r];
-            yt[r * YS + cc] = gt / (1.0f + dev_exp(-gt)) * up;
-        }
-        __syncthreads();
-    } else if (EPI == EPI_ARGMAX) {
+    if (EPI == EPI_ARGMAX) {
         for (int idx = threadIdx.x; idx < rows * 32; idx += blockDim.x) {
             const int r = idx >> 5, cc = idx & 31, row = pass0 * 4 + r, col = tile0 * 16 + cc;
             const float v = yt[r * YS + cc] * rs[r];
@@ -460,30 +479,63 @@ __global__ __launch_bounds__(512) void k_gemv(const GemvArgs a) {
         }
         return;
     }
-    // EPI_RESID / EPI_SILU: the next consumer's pieces for k-block blockIdx.x
-    if (!a.pa) return;
+    // EPI_RESID / EPI_SILU: one wave per pass finishes the group's 32 output
+    // columns, one k-block of the next consumer. Lane l works on row
+    // 4p + (l%16)/4, columns 8(l/16)..+7, and writes piece l%4 of them.
     for (int p = wave; p < np; p += W) {
         const int c = lane & 15, r = p * 4 + (c >> 2), piece = c & 3, q = lane >> 4;
         const int row = pass0 * 4 + r;
+        const bool live = row < a.m;
+        const float4 y0 = *(const float4*)&yt[r * YS + q * 8], y1 = *(const float4*)&yt[r * YS + q * 8 + 4];
+        const float yv[8] = {y0.x, y0.y, y0.z, y0.w, y1.x, y1.y, y1.z, y1.w};
         float v[8];
+        if (EPI == EPI_RESID) {
+            // x += y, then the sum of squares of the row's 32 new values
+            const float4 e0 = *(const float4*)&et[r * YS + q * 8], e1 = *(const float4*)&et[r * YS + q * 8 + 4];
+            const float ev[8] = {e0.x, e0.y, e0.z, e0.w, e1.x, e1.y, e1.z, e1.w};
+            float ssq = 0.0f;
 #pragma unroll
-        for (int s = 0; s < 8; s++) {
-            const int cc = q * 8 + s;
-            float t = row < a.m ? yt[r * YS + cc] : 0.0f;
-            if (EPI == EPI_RESID && a.g_next) t = gpre[s] * t;
-            v[s] = t;
-        }
-        write_pieces_kind(a.pa_kind, v, blockIdx.x, pass0 + p, a.pa_passes, row, piece, lane, a.pa, a.pxs);
-    }
-    // the consumer's zero padding past the last k-block
-    if (blockIdx.x == gridDim.x - 1)
-        for (int kb2 = gridDim.x; kb2 < a.pa_kb; kb2++)
-            for (int p = wave; p < np; p += W) {
-                const int c = lane & 15;
-                const float z[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-                write_pieces_kind(a.pa_kind, z, kb2, pass0 + p, a.pa_passes, pass0 * 4 + p * 4 + (c >> 2), c & 3, lane,
-                                  a.pa, a.pxs);
+            for (int s = 0; s < 8; s++) {
+                v[s] = live ? ev[s] + yv[s] : 0.0f;
+                ssq = fmaf(v[s], v[s], ssq);
             }
+            if (live && piece == 0) {
+                float* xr = a.x + (size_t)row * a.ldx + blockIdx.x * 32 + q * 8;
+#pragma unroll
+                for (int s = 0; s < 8; s++) xr[s] = v[s];
+            }
+            ssq += __shfl_xor(ssq, 16);
+            ssq += __shfl_xor(ssq, 32);
+            if (live && q == 0 && piece == 0) a.ss_out[(size_t)blockIdx.x * a.ss_m + row] = ssq;
+            if (a.g_next) {
+                const float4 g0 = *(const float4*)&gs[q * 8], g1 = *(const float4*)&gs[q * 8 + 4];
+                const float gv8[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
+#pragma unroll
+                for (int s = 0; s < 8; s++) v[s] *= gv8[s];
+            }
+        } else {
+            // columns 0..31 gate, 32..63 up of 32 intermediate channels
+            const float4 u0 = *(const float4*)&yt[r * YS + 32 + q * 8], u1 = *(const float4*)&yt[r * YS + 36 + q * 8];
+            const float uv[8] = {u0.x, u0.y, u0.z, u0.w, u1.x, u1.y, u1.z, u1.w};
+            const float rr = rs[r];
+#pragma unroll
+            for (int s = 0; s < 8; s++) {
+                const float gt = yv[s] * rr, up = uv[s] * rr;
+                v[s] = live ? gt / (1.0f + dev_exp(-gt)) * up : 0.0f;
+            }
+        }
+        if (a.pa) write_pieces_kind(a.pa_kind, v, blockIdx.x, pass0 + p, a.pa_passes, row, piece, lane, a.pa, a.pxs);
+    }
+    // the consumer's zero padding past the last k-block, one wave per (k-block, pass)
+    if (a.pa && blockIdx.x == gridDim.x - 1) {
+        const float z[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+        const int c = lane & 15;
+        for (int idx = wave; idx < (a.pa_kb - (int)gridDim.x) * np; idx += W) {
+            const int kb2 = gridDim.x + idx / np, p = idx % np;
+            write_pieces_kind(a.pa_kind, z, kb2, pass0 + p, a.pa_passes, pass0 * 4 + p * 4 + (c >> 2), c & 3, lane,
+                              a.pa, a.pxs);
+        }
+    }
 }
 
 template <class K>
