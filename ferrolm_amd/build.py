@@ -2,7 +2,11 @@
 
 Run as `python -m ferrolm_amd.build` (or through __graft_entry__.build()).
 It compiles every time it is called. Packed FP32 instructions are disabled
-(-packed-fp32-ops) for every device compilation.
+(-packed-fp32-ops) for every device compilation, and floating-point
+contraction is off (-ffp-contract=off): a fused multiply-add happens only
+where the source writes fmaf, as in the reference's mul_add. Besides matching
+the reference's operation order, this keeps lanes that combine values across
+the wave (shuffle sums) bit-identical, which the activation pieces rely on.
 """
 from __future__ import annotations
 
@@ -32,7 +36,7 @@ def hipcc() -> str:
 
 def flags() -> list[str]:
     return [f"--offload-arch={ARCH}", "-O3", "-fPIC", "-std=c++17", "-Wall", "-Wno-unused-function",
-            "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+            "-ffp-contract=off", "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
             f"-I{ROOT / 'include'}", f"-I{CSRC}"]
 
 

@@ -385,14 +385,16 @@ struct ChunkIn {
 };
 
 struct Plan {
-    int t = 0, S = 0, G = 0, W = 0, T = 0;
-    std::vector<int32_t> pos, slot, row_group, g_row0, g_nrows, g_table, g_wi0, g_nsplit, g_crow0, g_cpos0, wi_group,
-        wi_split, sel;
-    std::vector<uint32_t> tables, tokens;
-    bool host_tokens = true;
+    int t = 0, S = 0, W = 0;
+    // wrec: one 16-word record per attention work item (a span of one row
+    // group): row0, nrows, crow0, cpos0 (first row and position of the
+    // group's chunk), p0, p1 (the span), 0, 0, then the physical ids of the
+    // span's cache blocks. mrec: per row, the row's first query index within
+    // its group, the group's first work item and its number of spans.
+    std::vector<int32_t> wrec, mrec, sel;
+    std::vector<uint32_t> tokens;
     // offsets (in int32 words) of each array inside the packed metadata
-    size_t o_pos, o_slot, o_rg, o_grow0, o_gnrows, o_gtable, o_gwi0, o_gnsplit, o_gcrow0, o_gcpos0, o_wig, o_wis,
-        o_tables, o_sel, o_tok, words;
+    size_t o_wrec, o_mrec, o_sel, o_tok, words;
 };
 
 static int build_plan(const fg_config& c, const fg_kv& kv, int max_pos, const ChunkIn* ch, int nch, Plan& P) {
@@ -400,6 +402,7 @@ static int build_plan(const fg_config& c, const fg_kv& kv, int max_pos, const Ch
     const int group = c.heads / c.kv_heads;
     const int rg = std::max(1, std::min(16, attn_qmax(c.head_dim) / group));
     const int span = attn_span(c.head_dim);
+    if (bs != 16 || span % bs || span / bs > 8) return fail(FG_E_SHAPE, "attention spans need 16-token blocks");
     P = Plan();
     for (int ci = 0; ci < nch; ci++) {
         const ChunkIn& k = ch[ci];
@@ -410,16 +413,10 @@ static int build_plan(const fg_config& c, const fg_kv& kv, int max_pos, const Ch
         if (k.pos + k.n > max_pos) return fail(FG_E_SHAPE, "position beyond max_position");
         if (!k.blocks) return fail(FG_E_ARG, "chunk without a block table");
         const int used = (k.pos + k.n + bs - 1) / bs;
-        const int toff = (int)P.tables.size();
-        for (int b = 0; b < used; b++) {
+        for (int b = 0; b < used; b++)
             if (k.blocks[b] >= (uint32_t)kv.blocks) return fail(FG_E_ARG, "block id beyond the cache");
-            P.tables.push_back(k.blocks[b]);
-        }
         const int row_base = P.t;
         for (int i = 0; i < k.n; i++) {
-            const int p = k.pos + i;
-            P.pos.push_back(p);
-            P.slot.push_back((int32_t)(k.blocks[p / bs] * (uint32_t)bs + p % bs));
             if (k.tokens) {
                 if (k.tokens[i] >= (uint32_t)c.vocab) return fail(FG_E_ARG, "token outside the vocabulary");
                 P.tokens.push_back(k.tokens[i]);
@@ -429,21 +426,21 @@ static int build_plan(const fg_config& c, const fg_kv& kv, int max_pos, const Ch
         }
         for (int r0 = 0; r0 < k.n; r0 += rg) {
             const int nr = std::min(rg, k.n - r0);
-            const int gi = (int)P.g_row0.size();
-            P.g_row0.push_back(row_base + r0);
-            P.g_nrows.push_back(nr);
-            P.g_table.push_back(toff);
-            P.g_wi0.push_back((int)P.wi_group.size());
-            const int L = k.pos + r0 + nr;
+            const int wi0 = P.W;
+            const int L = k.pos + r0 + nr;  // positions the group's last row sees
             const int ns = (L + span - 1) / span;
-            P.g_nsplit.push_back(ns);
-            P.g_crow0.push_back(row_base);
-            P.g_cpos0.push_back(k.pos);
-            for (int s = 0; s < ns; s++) {
-                P.wi_group.push_back(gi);
-                P.wi_split.push_back(s);
+            for (int sp = 0; sp < ns; sp++) {
+                const int p0 = sp * span, p1 = std::min(p0 + span, L);
+                const int32_t rec[8] = {row_base + r0, nr, row_base, k.pos, p0, p1, 0, 0};
+                P.wrec.insert(P.wrec.end(), rec, rec + 8);
+                for (int j = 0; j < 8; j++)
+                    P.wrec.push_back(p0 + bs * j < p1 ? (int32_t)k.blocks[p0 / bs + j] : 0);
+                P.W++;
             }
-            for (int i = 0; i < nr; i++) P.row_group.push_back(gi);
+            for (int i = 0; i < nr; i++) {
+                const int32_t rec[4] = {i * group, wi0, ns, 0};
+                P.mrec.insert(P.mrec.end(), rec, rec + 4);
+            }
         }
         if (k.logits == FG_LOGITS_LAST) P.sel.push_back(row_base + k.n - 1);
         if (k.logits == FG_LOGITS_ALL)
@@ -451,28 +448,14 @@ static int build_plan(const fg_config& c, const fg_kv& kv, int max_pos, const Ch
         P.t += k.n;
     }
     P.S = (int)P.sel.size();
-    P.G = (int)P.g_row0.size();
-    P.W = (int)P.wi_group.size();
-    P.T = (int)P.tables.size();
     size_t o = 0;
     auto place = [&](size_t n) {
         size_t r = o;
         o += (n + 63) / 64 * 64;
         return r;
     };
-    P.o_pos = place(P.t);
-    P.o_slot = place(P.t);
-    P.o_rg = place(P.t);
-    P.o_grow0 = place(P.G);
-    P.o_gnrows = place(P.G);
-    P.o_gtable = place(P.G);
-    P.o_gwi0 = place(P.G);
-    P.o_gnsplit = place(P.G);
-    P.o_gcrow0 = place(P.G);
-    P.o_gcpos0 = place(P.G);
-    P.o_wig = place(P.W);
-    P.o_wis = place(P.W);
-    P.o_tables = place(P.T);
+    P.o_wrec = place(P.wrec.size());
+    P.o_mrec = place(P.mrec.size());
     P.o_sel = place(P.S);
     P.o_tok = place(P.t);
     P.words = o;
@@ -483,19 +466,8 @@ static void pack_plan(const Plan& P, int32_t* h) {
     auto cp = [&](size_t off, const std::vector<int32_t>& v) {
         if (!v.empty()) memcpy(h + off, v.data(), v.size() * 4);
     };
-    cp(P.o_pos, P.pos);
-    cp(P.o_slot, P.slot);
-    cp(P.o_rg, P.row_group);
-    cp(P.o_grow0, P.g_row0);
-    cp(P.o_gnrows, P.g_nrows);
-    cp(P.o_gtable, P.g_table);
-    cp(P.o_gwi0, P.g_wi0);
-    cp(P.o_gnsplit, P.g_nsplit);
-    cp(P.o_gcrow0, P.g_crow0);
-    cp(P.o_gcpos0, P.g_cpos0);
-    cp(P.o_wig, P.wi_group);
-    cp(P.o_wis, P.wi_split);
-    if (!P.tables.empty()) memcpy(h + P.o_tables, P.tables.data(), P.tables.size() * 4);
+    cp(P.o_wrec, P.wrec);
+    cp(P.o_mrec, P.mrec);
     cp(P.o_sel, P.sel);
     if (!P.tokens.empty()) memcpy(h + P.o_tok, P.tokens.data(), P.tokens.size() * 4);
 }
@@ -591,19 +563,8 @@ static int run_forward(fg_ctx* ctx, const fg_model* m, fg_kv* kv, const Plan& P,
     aa.ld = qkv_dim(c);
     aa.cos_t = m->cos_t;
     aa.sin_t = m->sin_t;
-    aa.row_pos = meta + P.o_pos;
-    aa.row_slot = meta + P.o_slot;
-    aa.row_group = meta + P.o_rg;
-    aa.wi_group = meta + P.o_wig;
-    aa.wi_split = meta + P.o_wis;
-    aa.g_row0 = meta + P.o_grow0;
-    aa.g_nrows = meta + P.o_gnrows;
-    aa.g_table = meta + P.o_gtable;
-    aa.g_wi0 = meta + P.o_gwi0;
-    aa.g_nsplit = meta + P.o_gnsplit;
-    aa.g_crow0 = meta + P.o_gcrow0;
-    aa.g_cpos0 = meta + P.o_gcpos0;
-    aa.tables = (const uint32_t*)(meta + P.o_tables);
+    aa.wrec = meta + P.o_wrec;
+    aa.mrec = meta + P.o_mrec;
     aa.part = w.apart;
     aa.n_wi = P.W;
     aa.nh = nh;
@@ -1016,7 +977,7 @@ int fg_spec_step(fg_ctx* ctx, const fg_model* target, fg_kv* tkv, const fg_model
                                     (int64_t)(uintptr_t)ctx->dmeta, ctx->prof ? 1 : 0};
         for (int r = 0; r <= k; r++) {
             const Plan& P = plans[r];
-            for (int64_t v : {(int64_t)P.t, (int64_t)P.S, (int64_t)P.G, (int64_t)P.W, (int64_t)P.T, (int64_t)P.words})
+            for (int64_t v : {(int64_t)P.t, (int64_t)P.S, (int64_t)P.W, (int64_t)P.words})
                 sig.push_back(v);
         }
         if (sig != ctx->gs.sig || !ctx->gs.exec[0] || !ctx->gs.exec[1]) {

@@ -114,19 +114,13 @@ struct AttnArgs {
     float* vc;
     const float* cos_t;
     const float* sin_t;
-    const int32_t* row_pos;   // [m]
-    const int32_t* row_slot;  // [m]
-    const int32_t* row_group; // [m] -> group
-    const int32_t* wi_group;  // work item -> group
-    const int32_t* wi_split;  // work item -> split index within the group
-    const int32_t* g_row0;    // group -> first row
-    const int32_t* g_nrows;
-    const int32_t* g_table;   // group -> offset of its block table in tables[]
-    const int32_t* g_wi0;     // group -> first work item
-    const int32_t* g_nsplit;
-    const int32_t* g_crow0;   // group -> first row of its chunk
-    const int32_t* g_cpos0;   // group -> position of its chunk's first row
-    const uint32_t* tables;
+    // [n_wi][16] per work item: row0, nrows (the row group), crow0, cpos0 (first
+    // row and position of the group's chunk; rows of a chunk hold consecutive
+    // positions), p0, p1 (the span), 0, 0, then the span's cache block ids
+    const int32_t* wrec;
+    // [rows][4] per row: first query index within its group, the group's first
+    // work item, its number of spans, 0
+    const int32_t* mrec;
     float* part;  // [wi][nkv][attn_qmax(hd)][hd+2]
     int n_wi, nh, nkv, hd, bs;
     float scale;

@@ -60,7 +60,11 @@ __device__ __forceinline__ float dev_exp(float x) {
 // ---------------------------------------------------------------------------
 // Activation pieces (see Pieces in internal.h). Called by a whole wave: lane
 // l holds v[0..7] = inputs 8*(l/16)..+7 of k-block kb for (row, piece) =
-// (4*pass + (l%16)/4, l%4).
+// (4*pass + (l%16)/4, l%4). The four lanes of a (row, inputs) pair must hold
+// bit-identical v: each writes its own piece, and for int8 each derives the
+// block scale itself. Producers that combine values across lanes therefore
+// sum rounded values in a symmetric order (the library is built without
+// floating-point contraction, so a shuffle sum is never fused with a product).
 // ---------------------------------------------------------------------------
 template <int CK>
 __device__ __forceinline__ void write_pieces(const float (&v)[8], int kb, int pass, int passes, int row, int piece,
@@ -605,26 +609,25 @@ __global__ __launch_bounds__(256) void k_attn(AttnArgs a) {
     __shared__ float pr[QM][P];
     __shared__ int lim[QM];
 
+    static_assert(P <= 64 && P % 16 == 0, "a span covers at most four cache blocks");
     const int wi = blockIdx.x, h = blockIdx.y;
-    const int g = a.wi_group[wi], sidx = a.wi_split[wi];
-    const int row0 = a.g_row0[g], nrows = a.g_nrows[g];
-    const int crow0 = a.g_crow0[g], cpos0 = a.g_cpos0[g];
-    const uint32_t* table = a.tables + a.g_table[g];
+    // the work item's record: one 64-byte read, everything else is arithmetic
+    const int4* rec = (const int4*)(a.wrec + (size_t)wi * 16);
+    const int4 r0 = rec[0], r1 = rec[1], rb = rec[2];
+    const int row0 = r0.x, nrows = r0.y, crow0 = r0.z, cpos0 = r0.w;
+    const int p0 = r1.x, p1 = r1.y;
     const int G = a.nh / a.nkv;
     const int Q = nrows * G;
-    const int Lmax = a.row_pos[row0 + nrows - 1] + 1;
-    const int p0 = sidx * P;
-    const int p1 = min(p0 + P, Lmax);
     const int qd = a.nh * HD, kvd = a.nkv * HD;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-
-    __shared__ uint32_t blks[P / 16];
-    if (tid < P / 16) blks[tid] = p0 + 16 * tid < p1 ? table[(p0 >> 4) + tid] : 0u;
-    for (int q = tid; q < Q; q += 256) lim[q] = a.row_pos[row0 + q / G];
+    auto blk = [&](int j) -> size_t { return (uint32_t)(j == 0 ? rb.x : j == 1 ? rb.y : j == 2 ? rb.z : rb.w); };
+    // rows of a chunk hold consecutive positions: row r sees positions <= its own
+    const int pos_of_row0 = cpos0 + row0 - crow0;
+    for (int q = tid; q < Q; q += 256) lim[q] = pos_of_row0 + q / G;
     // q, rotated: 4 (d, d + HALF) pairs per item
     for (int i = tid; i < Q * (HALF / 4); i += 256) {
         const int q = i / (HALF / 4), d = (i % (HALF / 4)) * 4, r = q / G, j = q % G, row = row0 + r;
-        const int pos = a.row_pos[row];
+        const int pos = pos_of_row0 + r;
         const float* src = a.qkv + (size_t)row * a.ld + (size_t)(h * G + j) * HD;
         const float4 x1 = *(const float4*)(src + d), x2 = *(const float4*)(src + d + HALF);
         const float4 c = *(const float4*)(a.cos_t + (size_t)pos * HALF + d);
@@ -648,7 +651,7 @@ __global__ __launch_bounds__(256) void k_attn(AttnArgs a) {
             float k1[4] = {0, 0, 0, 0}, k2[4] = {0, 0, 0, 0};
             if (p < p1) {
                 if (p < cpos0) {
-                    const float* kp = a.kc + (((size_t)blks[o >> 4] * a.nkv + h) * 16 + (p & 15)) * HD;
+                    const float* kp = a.kc + ((blk(o >> 4) * a.nkv + h) * 16 + (p & 15)) * HD;
                     const float4 u = *(const float4*)(kp + d), w = *(const float4*)(kp + d + HALF);
                     k1[0] = u.x; k1[1] = u.y; k1[2] = u.z; k1[3] = u.w;
                     k2[0] = w.x; k2[1] = w.y; k2[2] = w.z; k2[3] = w.w;
@@ -681,7 +684,7 @@ __global__ __launch_bounds__(256) void k_attn(AttnArgs a) {
             const int o = i / (HD / 4), d = (i % (HD / 4)) * 4, p = p0 + o;
             float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
             if (p < p1)
-                v = p < cpos0 ? *(const float4*)(a.vc + (((size_t)blks[o >> 4] * a.nkv + h) * 16 + (p & 15)) * HD + d)
+                v = p < cpos0 ? *(const float4*)(a.vc + ((blk(o >> 4) * a.nkv + h) * 16 + (p & 15)) * HD + d)
                               : *(const float4*)(a.qkv + (size_t)(crow0 + p - cpos0) * a.ld + qd + kvd + h * HD + d);
             *(float4*)&vs[o][d] = v;
         }
@@ -693,7 +696,7 @@ __global__ __launch_bounds__(256) void k_attn(AttnArgs a) {
         const int n1 = min(p1, cpos0 + row0 + nrows - crow0);
         for (int i = tid; i < (n1 - n0) * HD; i += 256) {
             const int p = n0 + i / HD, d = i % HD, o = p - p0;
-            const size_t at = (((size_t)blks[o >> 4] * a.nkv + h) * 16 + (p & 15)) * HD + d;
+            const size_t at = ((blk(o >> 4) * a.nkv + h) * 16 + (p & 15)) * HD + d;
             a.kc[at] = ks[o][d];
             a.vc[at] = vs[o][d];
         }
@@ -750,32 +753,38 @@ __global__ __launch_bounds__(64) void k_merge_pieces(AttnArgs a, int m, void* __
     float v[8] = {0, 0, 0, 0, 0, 0, 0, 0};
     if (row < m && k0 < a.nh * HD) {
         const int hq = k0 / HD, d0 = k0 % HD;
-        const int g = a.row_group[row];
         const int G = a.nh / a.nkv, h = hq / G, j = hq % G;
-        const int qi = (row - a.g_row0[g]) * G + j;
-        const int wi0 = a.g_wi0[g], ns = a.g_nsplit[g];
+        const int4 mr = *(const int4*)(a.mrec + (size_t)row * 4);
+        const int qi = mr.x + j, wi0 = mr.y, ns = mr.z;
         const size_t stride = (size_t)a.nkv * QM * (HD + 2);
         const float* base = a.part + ((size_t)wi0 * a.nkv * QM + (size_t)h * QM + qi) * (HD + 2);
-        float M = -INFINITY;
-#pragma unroll 4
-        for (int s = piece; s < ns; s += 4) M = fmaxf(M, base[s * stride]);
-        M = fmaxf(M, __shfl_xor(M, 1));
-        M = fmaxf(M, __shfl_xor(M, 2));
-        float L = 0.0f, O[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+        // online merge of this lane's spans (every fourth), one read of each
+        float M = -INFINITY, L = 0.0f, O[8] = {0, 0, 0, 0, 0, 0, 0, 0};
 #pragma unroll 4
         for (int s = piece; s < ns; s += 4) {
             const float* p = base + s * stride;
-            const float ms = p[0];
-            if (ms == -INFINITY) continue;
-            const float w = dev_exp(ms - M);
-            L = fmaf(p[1], w, L);
+            const float2 st = *(const float2*)p;
+            const float2 o01 = *(const float2*)(p + 2 + d0), o23 = *(const float2*)(p + 4 + d0);
+            const float2 o45 = *(const float2*)(p + 6 + d0), o67 = *(const float2*)(p + 8 + d0);
+            const float ov[8] = {o01.x, o01.y, o23.x, o23.y, o45.x, o45.y, o67.x, o67.y};
+            const float nM = fmaxf(M, st.x);
+            const float fo = M == -INFINITY ? 0.0f : dev_exp(M - nM);
+            const float w = st.x == -INFINITY ? 0.0f : dev_exp(st.x - nM);
+            L = fmaf(st.y, w, L * fo);
 #pragma unroll
-            for (int e = 0; e < 8; e++) O[e] = fmaf(p[2 + d0 + e], w, O[e]);
+            for (int e = 0; e < 8; e++) O[e] = fmaf(ov[e], w, O[e] * fo);
+            M = nM;
         }
+        // the four lanes of the pair, in a fixed order
+        float MA = fmaxf(M, __shfl_xor(M, 1));
+        MA = fmaxf(MA, __shfl_xor(MA, 2));
+        const float f = M == -INFINITY ? 0.0f : dev_exp(M - MA);
+        L *= f;
         L += __shfl_xor(L, 1);
         L += __shfl_xor(L, 2);
 #pragma unroll
         for (int e = 0; e < 8; e++) {
+            O[e] *= f;
             O[e] += __shfl_xor(O[e], 1);
             O[e] += __shfl_xor(O[e], 2);
             v[e] = O[e] / L;
