@@ -38,6 +38,11 @@ sys.path.insert(0, str(ROOT))
 
 METRIC = "accepted tok/s + verify-step µs, 1.7B int4-AWQ target + 135M draft, k=3, bs=1"
 HBM_PEAK_GBS = 8000.0
+# HBM bytes per launch of the target int4 decode GEMVs, measured with rocprofv3 --pmc
+# FETCH_SIZE and WRITE_SIZE and scaled by a plain copy of known size (--copy-calib);
+# profiles/gemv_int4_cfg2_pmc.md has the commands and the per-GEMV figures. It is a
+# measurement of the current kernels, re-taken whenever they change.
+MEASURED_TRAFFIC = {"int4": 14_980_104}
 
 
 def log(msg: str) -> None:
@@ -54,11 +59,24 @@ def main() -> int:
     ap.add_argument("--cpu-seconds", type=float, default=20.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-profile", action="store_true")
+    ap.add_argument("--copy-calib", type=int, default=0, metavar="MIB",
+                    help="only run a plain device copy of MIB MiB and exit (calibrates rocprofv3 FETCH_SIZE/WRITE_SIZE)")
     a = ap.parse_args()
     if a.gpus != 1:
         print(f"bench.py measures one GPU only: this build has no multi-GPU path (--gpus {a.gpus} requested)",
               file=sys.stderr)
         return 2
+    if a.copy_calib > 0:
+        # one elementwise kernel that reads and writes exactly copy_calib MiB each
+        import torch
+        src = torch.ones(a.copy_calib << 18, dtype=torch.float32, device="cuda:0")
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            torch.neg(src, out=dst)
+        torch.cuda.synchronize()
+        log(f"copy calibration: 3 x torch.neg over {a.copy_calib} MiB")
+        return 0
+
     from ferrolm_amd import gpu, spec, synth
     from ferrolm_amd.weights import KIND_NAMES
 
@@ -129,7 +147,8 @@ def main() -> int:
         dom = max(dom, key=lambda x: x["us"])
         ach = dom["bytes"] / dom["us"] / 1e3
         roofline = {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                    "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": None,
+                    "frac": round(ach / HBM_PEAK_GBS, 4),
+                    "traffic": MEASURED_TRAFFIC.get(dom["kind"]) if a.config == 2 else None,
                     "kernel": f"k_gemv {dom['kind']} (target projections, m={k + 1})",
                     "bytes_per_launch": round(dom["bytes"] / dom["launches"]),
                     "us_per_launch": round(dom["us"] / dom["launches"], 3), "launches": dom["launches"]}

@@ -6,6 +6,7 @@
 #include "internal.h"
 
 #include <algorithm>
+#include <atomic>
 #include <cstdlib>
 #include <functional>
 #include <cmath>
@@ -97,35 +98,32 @@ struct fg_ctx {
         double us = 0, bytes = 0;
     };
     Rec rec[12];
-    // HIP graphs of the speculative step (draft rounds, verify pass), reused
-    // while the launch shapes stay the same.
-    struct ProfItem {
-        int cls;
-        double bytes;
-        hipEvent_t a, b;
-    };
-    bool capturing = false;
-    std::vector<ProfItem> capture_prof;
+    // HIP graphs of the speculative step (draft rounds, verify pass), one
+    // entry per launch signature, the least recently used replaced first.
     struct GraphSet {
         std::vector<int64_t> sig;
         hipGraphExec_t exec[2] = {nullptr, nullptr};
-        std::vector<ProfItem> prof;
-    } gs;
+        uint64_t used = 0;
+    };
+    static constexpr int kGraphSets = 8;
+    std::vector<GraphSet> gsets;
+    bool capturing = false;  // a step is being captured: no per-launch events
+    uint64_t gclock = 0;
     bool graphs = true;
 };
 
-static void drop_graphs(fg_ctx* c) {
-    for (auto& e : c->gs.exec)
+static void drop_set(fg_ctx::GraphSet& g) {
+    for (auto& e : g.exec)
         if (e) {
             (void)hipGraphExecDestroy(e);
             e = nullptr;
         }
-    for (auto& p : c->gs.prof) {
-        (void)hipEventDestroy(p.a);
-        (void)hipEventDestroy(p.b);
-    }
-    c->gs.prof.clear();
-    c->gs.sig.clear();
+    g.sig.clear();
+}
+
+static void drop_graphs(fg_ctx* c) {
+    for (auto& g : c->gsets) drop_set(g);
+    c->gsets.clear();
 }
 
 // Algorithmic bytes of one GEMV launch over m rows: codes + group scales
@@ -173,7 +171,13 @@ struct DLayer {
     DMat w_down;
 };
 
+// Every model and cache gets a process-wide serial number at creation; the
+// step-graph cache keys on these, never on addresses that a later object
+// could reuse.
+static std::atomic<uint64_t> g_serial{1};
+
 struct fg_model {
+    uint64_t serial = g_serial++;
     fg_config cfg{};
     std::vector<DLayer> layers;
     uint16_t* embed = nullptr;
@@ -188,6 +192,7 @@ struct fg_model {
 };
 
 struct fg_kv {
+    uint64_t serial = g_serial++;
     int layers = 0, kv_heads = 0, head_dim = 0, block_size = 0, blocks = 0;
     float* k = nullptr;  // [layer][blocks*bs*nkv*hd]
     float* v = nullptr;
@@ -386,6 +391,8 @@ struct ChunkIn {
 
 struct Plan {
     int t = 0, S = 0, W = 0;
+    int Wc = 0;  // work items launched: W rounded up to 16, the extra records empty, so
+                 // the launch shapes (and a captured step graph) last for 16 more spans
     // wrec: one 16-word record per attention work item (a span of one row
     // group): row0, nrows, crow0, cpos0 (first row and position of the
     // group's chunk), p0, p1 (the span), 0, 0, then the physical ids of the
@@ -448,6 +455,8 @@ static int build_plan(const fg_config& c, const fg_kv& kv, int max_pos, const Ch
         P.t += k.n;
     }
     P.S = (int)P.sel.size();
+    P.Wc = std::max(16, (P.W + 15) / 16 * 16);
+    P.wrec.resize((size_t)P.Wc * 16, 0);
     size_t o = 0;
     auto place = [&](size_t n) {
         size_t r = o;
@@ -502,7 +511,7 @@ static size_t layout_work(const fg_model* m, const Plan& P, Work& w, void* base)
         w.pxs[i] = cv.take<float>((size_t)kb_max * passes * 4);
     }
     w.qkv = cv.take<float>((size_t)t * qkv_dim(c));
-    w.apart = cv.take<float>((size_t)std::max(P.W, 1) * c.kv_heads * attn_qmax(c.head_dim) * (c.head_dim + 2));
+    w.apart = cv.take<float>((size_t)std::max(P.Wc, 1) * c.kv_heads * attn_qmax(c.head_dim) * (c.head_dim + 2));
     w.logits = cv.take<float>((size_t)S * c.vocab);
     w.best = cv.take<float2>((size_t)(c.vocab / 32) * S);
     w.am = cv.take<uint32_t>(S);
@@ -566,7 +575,7 @@ static int run_forward(fg_ctx* ctx, const fg_model* m, fg_kv* kv, const Plan& P,
     aa.wrec = meta + P.o_wrec;
     aa.mrec = meta + P.o_mrec;
     aa.part = w.apart;
-    aa.n_wi = P.W;
+    aa.n_wi = P.Wc;
     aa.nh = nh;
     aa.nkv = nkv;
     aa.hd = hd;
@@ -971,54 +980,64 @@ int fg_spec_step(fg_ctx* ctx, const fg_model* target, fg_kv* tkv, const fg_model
         return 0;
     };
     bool use_graph = ctx->graphs && !ctx->prof;
+    fg_ctx::GraphSet* gset = nullptr;
     if (use_graph) {
-        std::vector<int64_t> sig = {n_seqs, k, (int64_t)(uintptr_t)target, (int64_t)(uintptr_t)draft,
-                                    (int64_t)(uintptr_t)tkv, (int64_t)(uintptr_t)dkv, (int64_t)(uintptr_t)ctx->ws,
-                                    (int64_t)(uintptr_t)ctx->dmeta, ctx->prof ? 1 : 0};
+        // everything the captured launches bake in: object identities, the
+        // workspace and metadata allocations, and each plan's shapes
+        std::vector<int64_t> sig = {n_seqs, k, (int64_t)target->serial, (int64_t)draft->serial,
+                                    (int64_t)tkv->serial, (int64_t)dkv->serial, (int64_t)(uintptr_t)ctx->ws,
+                                    (int64_t)ctx->ws_cap, (int64_t)(uintptr_t)ctx->dmeta, (int64_t)ctx->dmeta_cap};
         for (int r = 0; r <= k; r++) {
             const Plan& P = plans[r];
-            for (int64_t v : {(int64_t)P.t, (int64_t)P.S, (int64_t)P.W, (int64_t)P.words})
-                sig.push_back(v);
+            for (int64_t v : {(int64_t)P.t, (int64_t)P.S, (int64_t)P.Wc, (int64_t)P.words}) sig.push_back(v);
         }
-        if (sig != ctx->gs.sig || !ctx->gs.exec[0] || !ctx->gs.exec[1]) {
-            drop_graphs(ctx);
+        for (auto& g : ctx->gsets)
+            if (g.sig == sig) gset = &g;
+        if (!gset) {
+            if ((int)ctx->gsets.size() < fg_ctx::kGraphSets) {
+                ctx->gsets.emplace_back();
+                gset = &ctx->gsets.back();
+            } else {
+                gset = &ctx->gsets[0];
+                for (auto& g : ctx->gsets)
+                    if (g.used < gset->used) gset = &g;
+                drop_set(*gset);
+            }
             std::function<int()> phases[2] = {draft_phase, verify_phase};
             for (int g = 0; g < 2 && use_graph; g++) {
                 HIPCHK(hipStreamBeginCapture(ctx->stream, hipStreamCaptureModeThreadLocal));
                 ctx->capturing = true;
-                ctx->capture_prof.clear();
                 const int e = phases[g]();
                 ctx->capturing = false;
                 hipGraph_t graph = nullptr;
                 const hipError_t ce = hipStreamEndCapture(ctx->stream, &graph);
                 if (e) {
                     if (graph) (void)hipGraphDestroy(graph);
-                    drop_graphs(ctx);
+                    drop_set(*gset);
                     return e;
                 }
                 if (ce != hipSuccess || !graph ||
-                    hipGraphInstantiate(&ctx->gs.exec[g], graph, nullptr, nullptr, 0) != hipSuccess) {
+                    hipGraphInstantiate(&gset->exec[g], graph, nullptr, nullptr, 0) != hipSuccess) {
                     if (graph) (void)hipGraphDestroy(graph);
                     (void)hipGetLastError();
-                    drop_graphs(ctx);
+                    drop_set(*gset);
                     use_graph = false;  // launch directly this time
                     break;
                 }
                 (void)hipGraphDestroy(graph);
-                for (auto& p : ctx->capture_prof) ctx->gs.prof.push_back(p);
-                ctx->capture_prof.clear();
             }
-            if (use_graph) ctx->gs.sig = sig;
+            if (use_graph) gset->sig = sig;
         }
+        if (use_graph) gset->used = ++ctx->gclock;
     }
     HIPCHK(hipEventRecord(ctx->ev[0], ctx->stream));
     if (use_graph)
-        HIPCHK(hipGraphLaunch(ctx->gs.exec[0], ctx->stream));
+        HIPCHK(hipGraphLaunch(gset->exec[0], ctx->stream));
     else if ((rc = draft_phase()))
         return rc;
     HIPCHK(hipEventRecord(ctx->ev[1], ctx->stream));
     if (use_graph)
-        HIPCHK(hipGraphLaunch(ctx->gs.exec[1], ctx->stream));
+        HIPCHK(hipGraphLaunch(gset->exec[1], ctx->stream));
     else if ((rc = verify_phase()))
         return rc;
     HIPCHK(hipGetLastError());

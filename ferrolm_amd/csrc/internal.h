@@ -116,7 +116,8 @@ struct AttnArgs {
     const float* sin_t;
     // [n_wi][16] per work item: row0, nrows (the row group), crow0, cpos0 (first
     // row and position of the group's chunk; rows of a chunk hold consecutive
-    // positions), p0, p1 (the span), 0, 0, then the span's cache block ids
+    // positions), p0, p1 (the span), 0, 0, then the span's cache block ids.
+    // A record with nrows 0 is an unused slot.
     const int32_t* wrec;
     // [rows][4] per row: first query index within its group, the group's first
     // work item, its number of spans, 0

@@ -610,12 +610,15 @@ __global__ __launch_bounds__(256) void k_attn(AttnArgs a) {
     __shared__ int lim[QM];
 
     static_assert(P <= 64 && P % 16 == 0, "a span covers at most four cache blocks");
-    const int wi = blockIdx.x, h = blockIdx.y;
+    // grid (kv head, work item): every real item is dispatched before the
+    // launch's unused capacity slots, which exit at once
+    const int h = blockIdx.x, wi = blockIdx.y;
     // the work item's record: one 64-byte read, everything else is arithmetic
     const int4* rec = (const int4*)(a.wrec + (size_t)wi * 16);
     const int4 r0 = rec[0], r1 = rec[1], rb = rec[2];
     const int row0 = r0.x, nrows = r0.y, crow0 = r0.z, cpos0 = r0.w;
     const int p0 = r1.x, p1 = r1.y;
+    if (nrows == 0) return;  // an unused slot of the launch's capacity
     const int G = a.nh / a.nkv;
     const int Q = nrows * G;
     const int qd = a.nh * HD, kvd = a.nkv * HD;
@@ -795,7 +798,7 @@ __global__ __launch_bounds__(64) void k_merge_pieces(AttnArgs a, int m, void* __
 
 template <int HD, int P, int QM>
 static void attention_hd(hipStream_t st, const AttnArgs& a, int m, int ck, Pieces& out) {
-    hipLaunchKernelGGL((k_attn<HD, P, QM>), dim3(a.n_wi, a.nkv), dim3(256), 0, st, a);
+    hipLaunchKernelGGL((k_attn<HD, P, QM>), dim3(a.nkv, a.n_wi), dim3(256), 0, st, a);
     if (ck == BF16)
         hipLaunchKernelGGL((k_merge_pieces<HD, QM, BF16>), dim3(out.kb, out.passes), dim3(64), 0, st, a, m, out.a,
                            out.xs, out.passes);

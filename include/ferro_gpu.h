@@ -7,7 +7,7 @@
  * Vec<f32>` (src/model.rs:269) and the engine's accept loop
  * (src/engine.rs:563-616). Each entry point below replaces one reference
  * interface, named at its declaration, so a Rust caller binds it with a
- * thin `extern "C"` block.
+ * thin `extern "C"` block that mirrors this header.
  *
  * Conventions
  *  - Every function returns 0 on success and a negative FG_E_* code on

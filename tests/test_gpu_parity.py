@@ -141,6 +141,24 @@ def test_speculative_greedy_matches_oracle(ctx, layers, k):
             assert st_o[1] == st_o[0]
 
 
+def test_speculative_graph_replay_across_capacity(ctx):
+    """A decode that crosses 1024 positions: the attention launch grows from
+    16 to 32 span slots, so the cached step graphs are replayed, a new pair is
+    captured, and that pair is replayed too; the tokens stay the target's own
+    greedy tokens (tests/engine.rs:134-160 at a longer context)."""
+    from ferrolm_amd.synth import random_model
+    from ferrolm_amd.weights import Config
+    cfg = Config(vocab=512, hidden=128, intermediate=256, layers=2, heads=4, kv_heads=2, head_dim=32,
+                 rms_eps=1e-5, max_position=2048)
+    hm = random_model(cfg, seed=7, std=0.05)
+    om = oracle.Model(hm)
+    tm = gpu.Model(ctx, hm)
+    prompt = [int(x) for x in np.random.default_rng(3).integers(3, 500, 1000)]
+    want, _, _ = oracle.generate(om, None, prompt, 48, 0, kv_blocks=80)
+    got = generate(ctx, tm, tm.truncated(1), prompt, 48, 3, kv_blocks=80)
+    assert np.array_equal(got, want)
+
+
 def test_quantized_forward_matches_oracle(ctx):
     hm = load_model(GOLDEN / "llama-gqa")
     for kind in [INT8, INT4]:

@@ -158,6 +158,45 @@ def test_quantization_error_bounds_and_zeros():
     assert codes.min() >= -8 and codes.max() <= 7
 
 
+@pytest.mark.parametrize("kind", [1, 2])
+def test_quantizer_known_answers_rounding_and_layout(kind):
+    """QMatrix::quantize (src/quant.rs:78-143) on a hand-built 64x64 matrix whose best
+    clip is 1.0 in every group, with scale 1, 2 or 3 by (row, group): values that are
+    code x scale quantize to those codes, the ties +-2.5 (int8) and +-0.5 (int4) x scale
+    round half away from zero (Rust f32::round), and codes and scales sit in the
+    documented layout: int8 one signed byte per row, int4 byte c = row c (low nibble) |
+    row c + 16 (high nibble), each offset by 8 (src/quant.rs:70-76, 146-156); scales
+    [panel][group][32 rows] (src/quant.rs:124)."""
+    hi = 127 if kind == 1 else 7
+    rows = cols = 64
+    r, k = np.meshgrid(np.arange(rows), np.arange(cols), indexing="ij")
+    codes = ((r * 3 + k * 5) % (2 * hi - 1) - (hi - 1)).astype(np.int64)
+    codes[:, 0] = hi      # every group holds its amax, so scale = amax / hi at clip 1.0
+    codes[:, 32] = -hi
+    scale = (1 + (r + k // 32) % 3).astype(np.float32)
+    w = (codes * scale).astype(np.float32)
+    tie = 2.5 if kind == 1 else 0.5
+    for (rr, kk, sign) in [(0, 1, 1), (0, 2, -1), (37, 40, 1)]:
+        w[rr, kk] = sign * tie * scale[rr, kk]
+        codes[rr, kk] = sign * int(tie + 0.5)
+    m = oracle.quantize(kind, w)
+    want_s = np.zeros(rows // 32 * 2 * 32, np.float32)
+    bpk = 32 if kind == 1 else 16
+    want_q = np.zeros(rows // 32 * cols * bpk, np.uint8)
+    for rr in range(rows):
+        p, c = divmod(rr, 32)
+        for g in range(2):
+            want_s[(p * 2 + g) * 32 + c] = 1 + (rr + g) % 3
+        for kk in range(cols):
+            base = (p * cols + kk) * bpk
+            if kind == 1:
+                want_q[base + c] = codes[rr, kk] & 0xFF
+            else:
+                want_q[base + c % 16] |= (codes[rr, kk] + 8) << (4 * (c // 16))
+    assert np.array_equal(m.s, want_s)
+    assert np.array_equal(m.q, want_q)
+
+
 def test_int8_close_and_int4_further():
     """tests/quant.rs:41-58"""
     t = [3 + (i * 37) % 500 for i in range(96)]
