@@ -1,12 +1,13 @@
-"""Greedy speculative generation for one sequence over the device path.
+"""Greedy speculative generation over the device path.
 
-A host-side mirror of the reference engine's single-sequence greedy loop
+A host-side mirror of the reference engine's greedy loop
 (Engine::schedule/execute/propose, src/engine.rs:395-717): chunked prompt
 prefill under the token budget, then speculative steps of k draft proposals
 verified in one target pass, with the reference's rollback of the
-`computed` / `draft_computed` counters (src/engine.rs:613-615). The device
-does all model work (ferrolm_amd.gpu); this loop only does the reference's
-bookkeeping.
+`computed` / `draft_computed` counters (src/engine.rs:613-615). `Runner`
+drives one request; `Batch` drives several that decode together, every step
+one device speculative step over all of them. The device does all model work
+(ferrolm_amd.gpu); these loops only do the reference's bookkeeping.
 """
 from __future__ import annotations
 
@@ -43,6 +44,92 @@ class BlockPool:
             table.append(self.next)
             self.next += 1
         return True
+
+
+class ShuffledPool(BlockPool):
+    """Block ids in a seeded random order, so that block tables are not
+    contiguous (the block pool of the batched configurations)."""
+
+    def __init__(self, blocks: int, seed: int):
+        super().__init__(blocks)
+        self.order = [int(b) for b in np.random.default_rng(seed).permutation(blocks)]
+
+    def grow(self, table: list, tokens: int, bs: int = 16) -> bool:
+        while len(table) * bs < tokens:
+            if self.next >= self.blocks:
+                return False
+            table.append(self.order[self.next])
+            self.next += 1
+        return True
+
+
+class Batch:
+    """Several greedy requests decoded together (ignore_eos). The prompts are
+    prefilled in one forward over all their chunks (Logits::Last each); then
+    every step runs the reference's spec plan for every sequence at once
+    (Engine::execute over decoding sequences, src/engine.rs:499-654): one
+    device speculative step, then each sequence's rollback. Blocks come from a
+    shuffled pool shared by all sequences."""
+
+    def __init__(self, ctx: gpu.Context, target: gpu.Model, draft: gpu.Model, prompts, k: int, kv_blocks: int,
+                 seed: int = 0, tkv=None, dkv=None):
+        self.ctx, self.target, self.draft, self.k = ctx, target, draft, k
+        self.max_len = target.cfg.max_position
+        self.tkv = tkv or gpu.KvCache(ctx, target.cfg, kv_blocks)
+        self.dkv = dkv or gpu.KvCache(ctx, draft.cfg, kv_blocks)
+        self.tpool, self.dpool = ShuffledPool(kv_blocks, seed), ShuffledPool(kv_blocks, seed + 1)
+        self.tokens = [[int(t) for t in p] for p in prompts]
+        n = len(self.tokens)
+        self.tb, self.db = [[] for _ in range(n)], [[] for _ in range(n)]
+        self.computed, self.dcomp = [0] * n, [0] * n
+        self.stats = GenStats()
+
+    def prefill(self) -> list:
+        """The first token of every sequence."""
+        chunks = []
+        for i, t in enumerate(self.tokens):
+            if not self.tpool.grow(self.tb[i], len(t)):
+                raise RuntimeError("out of cache blocks")
+            chunks.append((t, 0, self.tb[i], gpu.LOGITS_LAST))
+        o = gpu.forward(self.ctx, self.target, self.tkv, chunks, logits=False)
+        first = []
+        for i, t in enumerate(self.tokens):
+            self.computed[i] = len(t)
+            t.append(int(o.argmax[i]))
+            first.append(t[-1])
+        return first
+
+    def step(self) -> list:
+        """One speculative step for every sequence; the emitted ids of each."""
+        k = self.k
+        seqs = []
+        for i, t in enumerate(self.tokens):
+            if len(t) - self.computed[i] != 1 or len(t) + k >= self.max_len:
+                raise RuntimeError("every sequence must be decoding, with room for k more tokens")
+            if not self.tpool.grow(self.tb[i], self.computed[i] + k + 1) or \
+                    not self.dpool.grow(self.db[i], len(t) + k - 1):
+                raise RuntimeError("out of cache blocks")
+            seqs.append(gpu.SpecSeq(tail=np.array(t[self.dcomp[i]:], np.uint32), draft_pos=self.dcomp[i],
+                                    pos=self.computed[i], blocks=np.array(self.tb[i], np.uint32),
+                                    draft_blocks=np.array(self.db[i], np.uint32)))
+        toks, acc = gpu.spec_step(self.ctx, self.target, self.tkv, self.draft, self.dkv, seqs, k)
+        t_us = gpu.last_step_times(self.ctx)
+        st = self.stats
+        st.draft_us.append(float(t_us[0]))
+        st.verify_us.append(float(t_us[1]))
+        st.spec_steps += 1
+        out = []
+        for i, t in enumerate(self.tokens):
+            a = int(acc[i])
+            st.proposed += k
+            st.accepted += a
+            base = len(t)
+            self.computed[i] = base + a
+            self.dcomp[i] = min(base + k - 1, base + a)
+            em = [int(x) for x in toks[i]]
+            t.extend(em)
+            out.append(em)
+        return out
 
 
 class Runner:

@@ -15,7 +15,7 @@ import pytest
 
 import oracle
 from ferrolm_amd import gpu
-from ferrolm_amd.spec import generate
+from ferrolm_amd.spec import Batch, generate
 from ferrolm_amd.weights import BF16, INT4, INT8, Matrix, bf16_to_f32, f32_to_bf16, load_model
 
 from conftest import FIXTURES, GOLDEN
@@ -157,6 +157,71 @@ def test_speculative_graph_replay_across_capacity(ctx):
     want, _, _ = oracle.generate(om, None, prompt, 48, 0, kv_blocks=80)
     got = generate(ctx, tm, tm.truncated(1), prompt, 48, 3, kv_blocks=80)
     assert np.array_equal(got, want)
+
+
+def _batched_matches_oracle(ctx, hm, prompts, k, steps, kv_blocks, seed):
+    """Prefill every prompt in one device forward, then run batched device spec
+    steps; each sequence must emit what the oracle's spec step for that sequence
+    alone emits from the same state, with the same rollback counters."""
+    om = oracle.Model(hm)
+    tm = gpu.Model(ctx, hm)
+    dm, od = tm.truncated(1), om.truncated(1)
+    b = Batch(ctx, tm, dm, prompts, k, kv_blocks=kv_blocks, seed=seed)
+    first = b.prefill()
+    okv, odkv = om.kv(kv_blocks), od.kv(kv_blocks)
+    for i, p in enumerate(prompts):
+        ol = om.forward(okv, [(p, 0, b.tb[i], 1)])
+        assert int(np.argmax(ol[0])) == first[i], i
+    otoks = [list(p) + [first[i]] for i, p in enumerate(prompts)]
+    oc, odc = [len(p) for p in prompts], [0] * len(prompts)
+    accepted = 0
+    for step in range(steps):
+        got = b.step()
+        for i in range(len(prompts)):
+            em, acc, c, dc = oracle.spec_step(om, okv, od, odkv, otoks[i], oc[i], odc[i], b.tb[i], b.db[i], k)
+            assert [int(x) for x in em] == got[i], (step, i)
+            assert (c, dc) == (b.computed[i], b.dcomp[i]), (step, i)
+            otoks[i] += [int(x) for x in em]
+            oc[i], odc[i] = c, dc
+            accepted += acc
+    return accepted
+
+
+def _quantized(hm, kind):
+    """Model::quantize of every projection (src/model.rs:192-219), no importance."""
+    if kind == BF16:
+        return hm
+    for l in hm.layers:
+        for name in ["wqkv", "wo", "w_gate_up", "w_down"]:
+            mat = getattr(l, name)
+            setattr(l, name, oracle.quantize(kind, bf16_to_f32(mat.bf16).reshape(mat.rows, mat.cols)))
+    return hm
+
+
+@pytest.mark.parametrize("kind", [BF16, INT8, INT4])
+def test_batched_speculative_steps_over_shuffled_tables(ctx, kind):
+    """Batched verify (five sequences of different lengths, k=4) over block tables
+    drawn from a shuffled pool, at fixture size, with a bf16, int8 or int4 target
+    (src/engine.rs:499-717 for every sequence of a step; src/kv.rs:139-151 tables)."""
+    hm = _quantized(load_model(GOLDEN / "llama-gqa"), kind)
+    rng = np.random.default_rng(11)
+    prompts = [[int(x) for x in rng.integers(3, 500, n)] for n in (23, 61, 150, 97, 200)]
+    accepted = _batched_matches_oracle(ctx, hm, prompts, k=4, steps=12, kv_blocks=128, seed=5)
+    assert accepted > 0  # the one-layer draft agrees sometimes: varied tails and accept counts
+
+
+def test_batched_speculative_steps_gqa_head_dim_128(ctx):
+    """The larger-GQA attention shape (head_dim 128: 32-position spans; four query
+    heads per kv head; rope theta 500000) in batched spec steps over contexts of
+    300 to 700 positions."""
+    from ferrolm_amd.synth import random_model
+    from ferrolm_amd.weights import Config
+    cfg = Config(vocab=512, hidden=256, intermediate=512, layers=2, heads=8, kv_heads=2, head_dim=128,
+                 rms_eps=1e-5, rope_theta=500000.0, max_position=2048)
+    hm = random_model(cfg, seed=9, std=0.05)
+    rng = np.random.default_rng(12)
+    prompts = [[int(x) for x in rng.integers(3, 500, n)] for n in (300, 451, 700)]
+    _batched_matches_oracle(ctx, hm, prompts, k=4, steps=6, kv_blocks=160, seed=6)
 
 
 def test_quantized_forward_matches_oracle(ctx):
