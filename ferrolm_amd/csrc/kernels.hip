@@ -66,53 +66,86 @@ __device__ __forceinline__ float dev_exp(float x) {
 // sum rounded values in a symmetric order (the library is built without
 // floating-point contraction, so a shuffle sum is never fused with a product).
 // ---------------------------------------------------------------------------
+// bf16 piece `piece` of x: four successive bf16 roundings of the remainder
+// (all four are formed and one is selected, without branches).
+__device__ __forceinline__ uint32_t bf16_piece(float x, int piece) {
+    uint32_t h = f32_to_bf16_bits(x), sel = h;
+#pragma unroll
+    for (int p = 1; p < 4; p++) {
+        x = x - bf16_bits_to_f32(h);
+        h = f32_to_bf16_bits(x);
+        sel = p == piece ? h : sel;
+    }
+    return sel;
+}
+
+// Exponent e of the int8 block scale 2^e shared by the four lanes of a row
+// (l, l^16, l^32, l^48 hold its 32 inputs; mx is this lane's max |input|):
+// the block maximum / 2^e lies in [64, 128) and never rounds past 127.
+__device__ __forceinline__ int int8_block_exp(float mx) {
+    mx = fmaxf(mx, __shfl_xor(mx, 16));
+    mx = fmaxf(mx, __shfl_xor(mx, 32));
+    int e = 0;
+    if (mx > 0.0f) {
+        int fe;
+        frexpf(mx, &fe);
+        e = fe - 7;
+        if (ldexpf(mx, -e) > 127.0f) e++;
+    }
+    return e;
+}
+
+// int8 piece `piece` of x at block exponent e: x / 2^e = a0 + a1/128 + ...
+__device__ __forceinline__ int int8_piece(float x, int e, int piece) {
+    float r = ldexpf(x, -e);  // exact
+    float a = rintf(r), sel = a;
+#pragma unroll
+    for (int p = 1; p < 4; p++) {
+        r = (r - a) * 128.0f;  // both exact
+        a = rintf(r);
+        sel = p == piece ? a : sel;
+    }
+    return (int)sel;
+}
+
 template <int CK>
 __device__ __forceinline__ void write_pieces(const float (&v)[8], int kb, int pass, int passes, int row, int piece,
                                              int lane, void* out, float* xs) {
+    const size_t slot = ((size_t)kb * passes + pass) * 64 + lane;
     if (CK == BF16) {
-        // all four pieces are formed and this lane's is selected (no branches)
         u16x8 o;
 #pragma unroll
-        for (int s = 0; s < 8; s++) {
-            float r = v[s];
-            uint32_t h = f32_to_bf16_bits(r), sel = h;
-#pragma unroll
-            for (int p = 1; p < 4; p++) {
-                r = r - bf16_bits_to_f32(h);
-                h = f32_to_bf16_bits(r);
-                sel = p == piece ? h : sel;
-            }
-            o[s] = (uint16_t)sel;
-        }
-        ((u16x8*)out)[((size_t)kb * passes + pass) * 64 + lane] = o;
+        for (int s = 0; s < 8; s++) o[s] = (uint16_t)bf16_piece(v[s], piece);
+        ((u16x8*)out)[slot] = o;
     } else {
         float mx = 0.0f;
 #pragma unroll
         for (int s = 0; s < 8; s++) mx = fmaxf(mx, fabsf(v[s]));
-        mx = fmaxf(mx, __shfl_xor(mx, 16));
-        mx = fmaxf(mx, __shfl_xor(mx, 32));
-        int e = 0;
-        if (mx > 0.0f) {
-            int fe;
-            frexpf(mx, &fe);
-            e = fe - 7;  // mx / 2^e in [64, 128)
-            if (ldexpf(mx, -e) > 127.0f) e++;
-        }
+        const int e = int8_block_exp(mx);
         i8x8 o;
 #pragma unroll
-        for (int s = 0; s < 8; s++) {
-            float r = ldexpf(v[s], -e);  // exact
-            float a = rintf(r), sel = a;
-#pragma unroll
-            for (int p = 1; p < 4; p++) {
-                r = (r - a) * 128.0f;  // both exact
-                a = rintf(r);
-                sel = p == piece ? a : sel;
-            }
-            o[s] = (int8_t)(int)sel;
-        }
-        ((i8x8*)out)[((size_t)kb * passes + pass) * 64 + lane] = o;
+        for (int s = 0; s < 8; s++) o[s] = (int8_t)int8_piece(v[s], e, piece);
+        ((i8x8*)out)[slot] = o;
         if (lane < 16 && (lane & 3) == 0) xs[(size_t)kb * passes * 4 + row] = ldexpf(1.0f, e);
+    }
+}
+
+// Inputs 2*pair and 2*pair+1 of a lane's eight (x0, x1), written as their
+// part of the lane's slot (4 bytes of bf16 pieces, 2 bytes of int8); mx is the
+// lane's max |input| over all eight, so the int8 block scale still covers the
+// row's 32 inputs. Four calls (pair 0..3, possibly from four waves) write
+// exactly what one write_pieces call writes.
+template <int CK>
+__device__ __forceinline__ void write_pieces_pair(float x0, float x1, float mx, int pair, int kb, int pass,
+                                                  int passes, int row, int piece, int lane, void* out, float* xs) {
+    const size_t slot = ((size_t)kb * passes + pass) * 64 + lane;
+    if (CK == BF16) {
+        ((uint32_t*)out)[slot * 4 + pair] = bf16_piece(x0, piece) | (bf16_piece(x1, piece) << 16);
+    } else {
+        const int e = int8_block_exp(mx);
+        ((uint16_t*)out)[slot * 4 + pair] =
+            (uint16_t)((uint8_t)int8_piece(x0, e, piece) | ((uint32_t)(uint8_t)int8_piece(x1, e, piece) << 8));
+        if (pair == 0 && lane < 16 && (lane & 3) == 0) xs[(size_t)kb * passes * 4 + row] = ldexpf(1.0f, e);
     }
 }
 
@@ -122,6 +155,15 @@ __device__ __forceinline__ void write_pieces_kind(int kind, const float (&v)[8],
         write_pieces<BF16>(v, kb, pass, passes, row, piece, lane, out, xs);
     else
         write_pieces<INT8>(v, kb, pass, passes, row, piece, lane, out, xs);
+}
+
+__device__ __forceinline__ void write_pieces_pair_kind(int kind, float x0, float x1, float mx, int pair, int kb,
+                                                       int pass, int passes, int row, int piece, int lane, void* out,
+                                                       float* xs) {
+    if (kind == BF16)
+        write_pieces_pair<BF16>(x0, x1, mx, pair, kb, pass, passes, row, piece, lane, out, xs);
+    else
+        write_pieces_pair<INT8>(x0, x1, mx, pair, kb, pass, passes, row, piece, lane, out, xs);
 }
 
 // Pieces of g * x[rows_src[row]] (g, rows_src optional). One wave per
@@ -237,6 +279,7 @@ __global__ __launch_bounds__(512) void k_gemv(const GemvArgs a) {
     __shared__ float rtmp[16 * 17];
     __shared__ __align__(16) float et[16 * YS];  // epilogue inputs: x tile (EPI_RESID) or bias
     __shared__ __align__(16) float gs[32];       // g_next of this group's 32 columns (EPI_RESID)
+    __shared__ __align__(16) float vt[16 * YS];  // finished values for the next consumer's pieces
 
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, W = blockDim.x >> 6;
     const int tile0 = blockIdx.x * NT;
@@ -406,12 +449,16 @@ __global__ __launch_bounds__(512) void k_gemv(const GemvArgs a) {
 #pragma unroll
     for (int it = 0; it < EPI_IT; it++) asm volatile("" : "+v"(pre[it]));
     asm volatile("" : "+v"(gv));
-    if (NEED_R && rfast) {
+    if (NEED_R && rfast && (int)threadIdx.x < rslots) {
+        // the 16 partials of a row sit in 16 consecutive lanes (whole waves take part)
         float v = 0.0f;
 #pragma unroll
         for (int i = 0; i < RL; i++) v += rv[i];
-        for (int idx = threadIdx.x; idx < 256; idx += blockDim.x)
-            rtmp[(idx >> 4) * 17 + (idx & 15)] = idx == (int)threadIdx.x ? v : 0.0f;
+        v += __shfl_xor(v, 8);
+        v += __shfl_xor(v, 4);
+        v += __shfl_xor(v, 2);
+        v += __shfl_xor(v, 1);
+        if ((threadIdx.x & 15) == 0) rs[threadIdx.x >> 4] = 1.0f / sqrtf(v / (float)a.hidden + a.eps);
     }
     if (EPI == EPI_RESID || ((EPI == EPI_QKV || EPI == EPI_STORE) && a.bias)) {
 #pragma unroll
@@ -431,7 +478,7 @@ __global__ __launch_bounds__(512) void k_gemv(const GemvArgs a) {
                 red[((wave * NT + t) * 4 + p) * 64 + lane] =
                     Q ? accq[t][p] : ((accb[t][p][0] + accb[t][p][1]) + accb[t][p][2]) + accb[t][p][3];
     __syncthreads();
-    if (NEED_R && threadIdx.x < 16) {
+    if (NEED_R && !rfast && threadIdx.x < 16) {
         float s = 0.0f;
         for (int j = 0; j < 16; j++) s += rtmp[threadIdx.x * 17 + j];
         rs[threadIdx.x] = 1.0f / sqrtf(s / (float)a.hidden + a.eps);
@@ -483,53 +530,49 @@ __global__ __launch_bounds__(512) void k_gemv(const GemvArgs a) {
         }
         return;
     }
-    // EPI_RESID / EPI_SILU: one wave per pass finishes the group's 32 output
-    // columns, one k-block of the next consumer. Lane l works on row
-    // 4p + (l%16)/4, columns 8(l/16)..+7, and writes piece l%4 of them.
-    for (int p = wave; p < np; p += W) {
-        const int c = lane & 15, r = p * 4 + (c >> 2), piece = c & 3, q = lane >> 4;
-        const int row = pass0 * 4 + r;
+    // EPI_RESID / EPI_SILU finish the group's 32 output columns: one k-block of
+    // the next consumer. (A) every thread finishes some of the rows x 32 values
+    // into LDS; (B) one wave forms each row's sum of squares (EPI_RESID);
+    // (C) up to four waves per pass write the pieces, two of a lane's eight
+    // inputs each, so the conversions run on several SIMDs at once.
+    for (int idx = threadIdx.x; idx < rows * 32; idx += blockDim.x) {
+        const int r = idx >> 5, cc = idx & 31, row = pass0 * 4 + r;
         const bool live = row < a.m;
-        const float4 y0 = *(const float4*)&yt[r * YS + q * 8], y1 = *(const float4*)&yt[r * YS + q * 8 + 4];
-        const float yv[8] = {y0.x, y0.y, y0.z, y0.w, y1.x, y1.y, y1.z, y1.w};
-        float v[8];
         if (EPI == EPI_RESID) {
-            // x += y, then the sum of squares of the row's 32 new values
-            const float4 e0 = *(const float4*)&et[r * YS + q * 8], e1 = *(const float4*)&et[r * YS + q * 8 + 4];
-            const float ev[8] = {e0.x, e0.y, e0.z, e0.w, e1.x, e1.y, e1.z, e1.w};
-            float ssq = 0.0f;
-#pragma unroll
-            for (int s = 0; s < 8; s++) {
-                v[s] = live ? ev[s] + yv[s] : 0.0f;
-                ssq = fmaf(v[s], v[s], ssq);
-            }
-            if (live && piece == 0) {
-                float* xr = a.x + (size_t)row * a.ldx + blockIdx.x * 32 + q * 8;
-#pragma unroll
-                for (int s = 0; s < 8; s++) xr[s] = v[s];
-            }
-            ssq += __shfl_xor(ssq, 16);
-            ssq += __shfl_xor(ssq, 32);
-            if (live && q == 0 && piece == 0) a.ss_out[(size_t)blockIdx.x * a.ss_m + row] = ssq;
-            if (a.g_next) {
-                const float4 g0 = *(const float4*)&gs[q * 8], g1 = *(const float4*)&gs[q * 8 + 4];
-                const float gv8[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
-#pragma unroll
-                for (int s = 0; s < 8; s++) v[s] *= gv8[s];
-            }
+            const float xn = live ? et[r * YS + cc] + yt[r * YS + cc] : 0.0f;
+            if (live) a.x[(size_t)row * a.ldx + blockIdx.x * 32 + cc] = xn;
+            yt[r * YS + cc] = xn;
+            vt[r * YS + cc] = a.g_next ? gs[cc] * xn : xn;
         } else {
-            // columns 0..31 gate, 32..63 up of 32 intermediate channels
-            const float4 u0 = *(const float4*)&yt[r * YS + 32 + q * 8], u1 = *(const float4*)&yt[r * YS + 36 + q * 8];
-            const float uv[8] = {u0.x, u0.y, u0.z, u0.w, u1.x, u1.y, u1.z, u1.w};
-            const float rr = rs[r];
-#pragma unroll
-            for (int s = 0; s < 8; s++) {
-                const float gt = yv[s] * rr, up = uv[s] * rr;
-                v[s] = live ? gt / (1.0f + dev_exp(-gt)) * up : 0.0f;
-            }
+            const float gt = yt[r * YS + cc] * rs[r], up = yt[r * YS + 32 + cc] * rs[r];
+            vt[r * YS + cc] = live ? gt / (1.0f + dev_exp(-gt)) * up : 0.0f;
         }
-        if (a.pa) write_pieces_kind(a.pa_kind, v, blockIdx.x, pass0 + p, a.pa_passes, row, piece, lane, a.pa, a.pxs);
     }
+    __syncthreads();
+    if (EPI == EPI_RESID && wave == W - 1)
+        for (int p = 0; p < np; p++) {
+            // row 4p + lane/16: lane j of 16 takes columns 2j, 2j+1
+            const int r = p * 4 + (lane >> 4), j = lane & 15, row = pass0 * 4 + r;
+            const float x0 = yt[r * YS + 2 * j], x1 = yt[r * YS + 2 * j + 1];
+            float ssq = fmaf(x1, x1, x0 * x0);
+            ssq += __shfl_xor(ssq, 8);
+            ssq += __shfl_xor(ssq, 4);
+            ssq += __shfl_xor(ssq, 2);
+            ssq += __shfl_xor(ssq, 1);
+            if (j == 0 && row < a.m) a.ss_out[(size_t)blockIdx.x * a.ss_m + row] = ssq;
+        }
+    if (a.pa)
+        for (int t = wave; t < np * 4; t += W) {
+            const int p = t >> 2, pair = t & 3;
+            const int c = lane & 15, r = p * 4 + (c >> 2), q = lane >> 4;
+            const float* vr = &vt[r * YS + q * 8];
+            const float4 v0 = *(const float4*)vr, v1 = *(const float4*)(vr + 4);
+            const float mx = fmaxf(fmaxf(fmaxf(fabsf(v0.x), fabsf(v0.y)), fmaxf(fabsf(v0.z), fabsf(v0.w))),
+                                   fmaxf(fmaxf(fabsf(v1.x), fabsf(v1.y)), fmaxf(fabsf(v1.z), fabsf(v1.w))));
+            const float2 xp = *(const float2*)(vr + 2 * pair);
+            write_pieces_pair_kind(a.pa_kind, xp.x, xp.y, mx, pair, blockIdx.x, pass0 + p, a.pa_passes,
+                                   pass0 * 4 + r, c & 3, lane, a.pa, a.pxs);
+        }
     // the consumer's zero padding past the last k-block, one wave per (k-block, pass)
     if (a.pa && blockIdx.x == gridDim.x - 1) {
         const float z[8] = {0, 0, 0, 0, 0, 0, 0, 0};
@@ -627,6 +670,42 @@ __global__ __launch_bounds__(256) void k_attn(AttnArgs a) {
     // rows of a chunk hold consecutive positions: row r sees positions <= its own
     const int pos_of_row0 = cpos0 + row0 - crow0;
     for (int q = tid; q < Q; q += 256) lim[q] = pos_of_row0 + q / G;
+    // Every load of the span is issued before anything waits on one: the keys
+    // and values (from the cache, or from the q/k/v rows for this chunk's new
+    // positions, with their cos/sin) into registers, then q. One round trip.
+    constexpr int KI = P * (HALF / 4), KIT = (KI + 255) / 256;
+    constexpr int VI = P * (HD / 4), VIT = (VI + 255) / 256;
+    float4 ku[KIT], kw[KIT], kcs[KIT], ksn[KIT], vv[VIT];
+#pragma unroll
+    for (int it = 0; it < KIT; it++) {
+        const int i = tid + it * 256;
+        const float4 z = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        ku[it] = kw[it] = kcs[it] = ksn[it] = z;
+        if (i < KI) {
+            const int o = i / (HALF / 4), d = (i % (HALF / 4)) * 4, p = p0 + o;
+            if (p < p1) {
+                const float* kp = p < cpos0 ? a.kc + ((blk(o >> 4) * a.nkv + h) * 16 + (p & 15)) * HD
+                                            : a.qkv + (size_t)(crow0 + p - cpos0) * a.ld + qd + h * HD;
+                ku[it] = *(const float4*)(kp + d);
+                kw[it] = *(const float4*)(kp + d + HALF);
+                if (p >= cpos0) {
+                    kcs[it] = *(const float4*)(a.cos_t + (size_t)p * HALF + d);
+                    ksn[it] = *(const float4*)(a.sin_t + (size_t)p * HALF + d);
+                }
+            }
+        }
+    }
+#pragma unroll
+    for (int it = 0; it < VIT; it++) {
+        const int i = tid + it * 256;
+        vv[it] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        if (i < VI) {
+            const int o = i / (HD / 4), d = (i % (HD / 4)) * 4, p = p0 + o;
+            if (p < p1)
+                vv[it] = p < cpos0 ? *(const float4*)(a.vc + ((blk(o >> 4) * a.nkv + h) * 16 + (p & 15)) * HD + d)
+                                   : *(const float4*)(a.qkv + (size_t)(crow0 + p - cpos0) * a.ld + qd + kvd + h * HD + d);
+        }
+    }
     // q, rotated: 4 (d, d + HALF) pairs per item
     for (int i = tid; i < Q * (HALF / 4); i += 256) {
         const int q = i / (HALF / 4), d = (i % (HALF / 4)) * 4, r = q / G, j = q % G, row = row0 + r;
@@ -643,54 +722,28 @@ __global__ __launch_bounds__(256) void k_attn(AttnArgs a) {
             qs[q][d + HALF + e] = __fadd_rn(__fmul_rn(a2[e], cc[e]), __fmul_rn(a1[e], ss[e]));
         }
     }
-    __syncthreads();
-    // keys (rotated when new) and values of the span, 16-byte loads
-    constexpr int KI = P * (HALF / 4);
+    // keys (rotated when new) and values to LDS
 #pragma unroll
-    for (int it = 0; it < (KI + 255) / 256; it++) {
+    for (int it = 0; it < KIT; it++) {
         const int i = tid + it * 256;
         if (i < KI) {
             const int o = i / (HALF / 4), d = (i % (HALF / 4)) * 4, p = p0 + o;
-            float k1[4] = {0, 0, 0, 0}, k2[4] = {0, 0, 0, 0};
-            if (p < p1) {
-                if (p < cpos0) {
-                    const float* kp = a.kc + ((blk(o >> 4) * a.nkv + h) * 16 + (p & 15)) * HD;
-                    const float4 u = *(const float4*)(kp + d), w = *(const float4*)(kp + d + HALF);
-                    k1[0] = u.x; k1[1] = u.y; k1[2] = u.z; k1[3] = u.w;
-                    k2[0] = w.x; k2[1] = w.y; k2[2] = w.z; k2[3] = w.w;
-                } else {
-                    const float* src = a.qkv + (size_t)(crow0 + p - cpos0) * a.ld + qd + h * HD;
-                    const float4 u = *(const float4*)(src + d), w = *(const float4*)(src + d + HALF);
-                    const float4 c = *(const float4*)(a.cos_t + (size_t)p * HALF + d);
-                    const float4 sn = *(const float4*)(a.sin_t + (size_t)p * HALF + d);
-                    const float a1[4] = {u.x, u.y, u.z, u.w}, a2[4] = {w.x, w.y, w.z, w.w};
-                    const float cc[4] = {c.x, c.y, c.z, c.w}, ss[4] = {sn.x, sn.y, sn.z, sn.w};
-#pragma unroll
-                    for (int e = 0; e < 4; e++) {
-                        k1[e] = __fadd_rn(__fmul_rn(a1[e], cc[e]), __fmul_rn(-a2[e], ss[e]));
-                        k2[e] = __fadd_rn(__fmul_rn(a2[e], cc[e]), __fmul_rn(a1[e], ss[e]));
-                    }
-                }
-            }
+            const float a1[4] = {ku[it].x, ku[it].y, ku[it].z, ku[it].w};
+            const float a2[4] = {kw[it].x, kw[it].y, kw[it].z, kw[it].w};
+            const float cc[4] = {kcs[it].x, kcs[it].y, kcs[it].z, kcs[it].w};
+            const float ss[4] = {ksn[it].x, ksn[it].y, ksn[it].z, ksn[it].w};
+            const bool rot = p < p1 && p >= cpos0;
 #pragma unroll
             for (int e = 0; e < 4; e++) {
-                ks[o][d + e] = k1[e];
-                ks[o][d + HALF + e] = k2[e];
+                ks[o][d + e] = rot ? __fadd_rn(__fmul_rn(a1[e], cc[e]), __fmul_rn(-a2[e], ss[e])) : a1[e];
+                ks[o][d + HALF + e] = rot ? __fadd_rn(__fmul_rn(a2[e], cc[e]), __fmul_rn(a1[e], ss[e])) : a2[e];
             }
         }
     }
-    constexpr int VI = P * (HD / 4);
 #pragma unroll
-    for (int it = 0; it < (VI + 255) / 256; it++) {
+    for (int it = 0; it < VIT; it++) {
         const int i = tid + it * 256;
-        if (i < VI) {
-            const int o = i / (HD / 4), d = (i % (HD / 4)) * 4, p = p0 + o;
-            float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-            if (p < p1)
-                v = p < cpos0 ? *(const float4*)(a.vc + ((blk(o >> 4) * a.nkv + h) * 16 + (p & 15)) * HD + d)
-                              : *(const float4*)(a.qkv + (size_t)(crow0 + p - cpos0) * a.ld + qd + kvd + h * HD + d);
-            *(float4*)&vs[o][d] = v;
-        }
+        if (i < VI) *(float4*)&vs[i / (HD / 4)][(i % (HD / 4)) * 4] = vv[it];
     }
     __syncthreads();
     // this group's new rows in the span go to the cache
