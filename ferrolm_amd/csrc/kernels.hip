@@ -267,11 +267,13 @@ void launch_embed(hipStream_t st, const uint32_t* tokens, int stride, const uint
 // ---------------------------------------------------------------------------
 constexpr int YS = 64;  // row stride of the output tile in LDS
 
-template <int KIND, int NT, int EPI, int PG>
-__global__ __launch_bounds__(512) void k_gemv(const GemvArgs a) {
+template <int KIND, int NT, int EPI, int PG, int WMAX = 8>
+__global__ __launch_bounds__(64 * WMAX) void k_gemv(const GemvArgs a) {
     constexpr bool Q = KIND != BF16;
-    // chunks loaded ahead per wave: about 16 B x 4 per lane and tile of weights in flight
-    constexpr int U = PG == 1 ? (KIND == INT4 ? 4 : 2) : 1;
+    // chunks loaded ahead per wave: about 16 B x 4 per lane and tile of weights in
+    // flight; with 16 waves (4 per SIMD, 128 VGPRs) half as many, the other waves
+    // of the SIMD covering each one's wait
+    constexpr int U = PG == 1 ? (KIND == INT4 ? 4 : 2) / (WMAX == 16 ? 2 : 1) : 1;
     constexpr bool NEED_R = EPI == EPI_QKV || EPI == EPI_SILU || EPI == EPI_ARGMAX;
     __shared__ float red[32 * 4 * 64];
     __shared__ __align__(16) float yt[16 * YS];
@@ -600,6 +602,13 @@ static void gemv_pg(hipStream_t st, const DMat& w, const GemvArgs& a, hipEvent_t
     const int KC = w.kb / 4;
     const int maxw = 8;  // waves per group: launch bounds of k_gemv
     if (a.p_total == 1) {
+        if constexpr (KIND == INT4 && NT == 2) {
+            if (KC >= 16) {
+                // 16 waves (4 per SIMD) cover each other's waits on the big int4 matrices
+                launch_timed(k_gemv<KIND, NT, EPI, 1, 16>, dim3(groups, 1, 1), dim3(64 * 16), st, a, e0, e1);
+                return;
+            }
+        }
         const int W = std::max(1, std::min(maxw, KC));
         launch_timed(k_gemv<KIND, NT, EPI, 1>, dim3(groups, 1, 1), dim3(64 * W), st, a, e0, e1);
     } else {

@@ -224,6 +224,22 @@ def test_batched_speculative_steps_gqa_head_dim_128(ctx):
     _batched_matches_oracle(ctx, hm, prompts, k=4, steps=6, kv_blocks=160, seed=6)
 
 
+@pytest.mark.parametrize("n_seqs", [1, 2])
+def test_speculative_steps_self_merging_output_projection(ctx, n_seqs):
+    """Head dim 64 with one pass of rows (up to 4): the output projection merges the
+    attention spans itself instead of a separate merge launch. One sequence uses it
+    in the draft rounds and the verify; two sequences use it in the draft rounds and
+    the separate merge in the 6-row verify. Each step is checked against the oracle."""
+    from ferrolm_amd.synth import random_model
+    from ferrolm_amd.weights import Config
+    cfg = Config(vocab=512, hidden=192, intermediate=384, layers=2, heads=6, kv_heads=2, head_dim=64,
+                 rms_eps=1e-5, max_position=2048)
+    hm = random_model(cfg, seed=13, std=0.05)
+    rng = np.random.default_rng(14)
+    prompts = [[int(x) for x in rng.integers(3, 500, n)] for n in (333, 150)[:n_seqs]]
+    _batched_matches_oracle(ctx, hm, prompts, k=2, steps=10, kv_blocks=80, seed=8)
+
+
 def test_quantized_forward_matches_oracle(ctx):
     hm = load_model(GOLDEN / "llama-gqa")
     for kind in [INT8, INT4]:
