@@ -59,6 +59,7 @@ def main() -> int:
     ap.add_argument("--cpu-seconds", type=float, default=20.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-profile", action="store_true")
+    ap.add_argument("--batch", type=int, default=0, help="sequences for configs 3/4 (default: the config's own)")
     ap.add_argument("--copy-calib", type=int, default=0, metavar="MIB",
                     help="only run a plain device copy of MIB MiB and exit (calibrates rocprofv3 FETCH_SIZE/WRITE_SIZE)")
     a = ap.parse_args()
@@ -87,6 +88,8 @@ def main() -> int:
     target = gpu.Model(ctx, wl.target)
     draft = gpu.Model(ctx, wl.draft) if wl.draft is not None else target.truncated(wl.draft_layers)
     log(f"uploaded: target {target.weight_bytes() / 1e9:.3f} GB, draft {draft.weight_bytes() / 1e9:.3f} GB")
+    if a.batch > 1 or wl.batch > 1:
+        return run_batched(a, wl, ctx, target, draft)
     cfg = wl.target.cfg
     prompt = synth.prompt_ids(wl.prompt_len, cfg.vocab, a.seed)
     k = wl.k
@@ -206,6 +209,83 @@ def main() -> int:
                    "prompt": wl.prompt_len, "context_at_timed_start": ctx_start},
         "verify_step_us": round(verify_us, 2), "draft_us": round(draft_us, 2), "acceptance": round(acceptance, 4),
         "roofline": roofline, "cpu_baseline": cpu, "parity": parity,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+def run_batched(a, wl, ctx, target, draft) -> int:
+    """Batched verify (configs 3 and 4): B sequences with context lengths drawn
+    uniformly (cfg3 128-2048, cfg4 512-4096), block tables from a shuffled pool,
+    every step one device speculative step over all of them. Reports emitted
+    tok/s over all sequences, the verify step's device time, and the MFMA rate of
+    the verify GEMMs (algorithmic 2*rows*n*k over their summed launch time). No
+    CPU baseline here: the oracle would need a host copy of the whole cache; the
+    per-sequence parity of batched steps is a GPU test."""
+    from ferrolm_amd import gpu, spec, synth
+    from ferrolm_amd.weights import KIND_NAMES
+    B = a.batch if a.batch > 1 else wl.batch
+    k = wl.k
+    cfg = wl.target.cfg
+    lo, hi = (512, 4096) if a.config == 4 else (128, 2048)
+    rng = np.random.default_rng(a.seed)
+    lens = [int(x) for x in rng.integers(lo, hi + 1, B)]
+    prompts = [[int(t) for t in synth.prompt_ids(n, cfg.vocab, a.seed + 1 + i)] for i, n in enumerate(lens)]
+    total = a.warmup + 2 * a.steps
+    blocks = sum((n + total * (k + 1) + 32) // 16 + 2 for n in lens)
+    b = spec.Batch(ctx, target, draft, prompts, k, kv_blocks=blocks, seed=a.seed)
+    t1 = time.time()
+    b.prefill(max_tokens=2048)
+    log(f"prefill of {B} prompts ({sum(lens)} tokens, {min(lens)}..{max(lens)}): {time.time() - t1:.2f}s")
+    for _ in range(a.warmup):
+        b.step()
+    st0 = len(b.stats.verify_us)
+    ctx.sync()
+    tt = time.perf_counter()
+    n_tok = 0
+    for _ in range(a.steps):
+        n_tok += sum(len(e) for e in b.step())
+    ctx.sync()
+    elapsed = time.perf_counter() - tt
+    value = n_tok / elapsed
+    verify_us = float(np.mean(b.stats.verify_us[st0:]))
+    draft_us = float(np.mean(b.stats.draft_us[st0:]))
+    acceptance = b.stats.accepted / max(1, b.stats.proposed)
+    log(f"timed {a.steps} steps x {B} sequences: {elapsed * 1e3:.1f} ms, {n_tok} tokens, {value:.1f} tok/s, "
+        f"verify {verify_us:.1f} us, draft {draft_us:.1f} us")
+    roofline = None
+    if not a.no_profile:
+        gpu.profile(ctx, True)
+        gpu.profile_read(ctx, reset=True)
+        for _ in range(a.steps):
+            b.step()
+        ctx.sync()
+        recs = gpu.profile_read(ctx, reset=True)
+        gpu.profile(ctx, False)
+        for rec in recs:
+            log(f"gemv {rec['kind']} passes<={rec['passes']}: {rec['launches']} launches, "
+                f"{rec['us'] / rec['launches']:.2f} us avg, {rec['bytes'] / rec['us'] / 1e3:.0f} GB/s, "
+                f"{rec['flops'] / rec['us'] / 1e6:.1f} TFLOP/s")
+        tkind = KIND_NAMES[wl.target_kind]
+        dom = max([x for x in recs if x["kind"] == tkind and x["passes"] > 1] or recs, key=lambda x: x["us"])
+        ach = dom["flops"] / dom["us"] / 1e6
+        peak = {"int8": 5000.0, "int4": 5000.0, "bf16": 2500.0}[dom["kind"]]
+        roofline = {"bound": "mfma", "achieved": round(ach, 2), "peak": peak, "unit": "TFLOP/s",
+                    "frac": round(ach / peak, 5), "traffic": None,
+                    "kernel": f"k_gemv {dom['kind']} (target verify GEMMs, {B * (k + 1)} rows)",
+                    "flops_per_launch": round(dom["flops"] / dom["launches"]),
+                    "us_per_launch": round(dom["us"] / dom["launches"], 3), "launches": dom["launches"]}
+    metric = (f"accepted tok/s + verify-step µs, {cfg.hidden}-hidden {KIND_NAMES[wl.target_kind]} target + draft, "
+              f"k={k}, bs={B}")
+    line = {
+        "metric": metric, "value": round(value, 2), "unit": "tok/s", "n_gpus": 1, "steps": a.steps,
+        "warmup": a.warmup, "ms_per_step": round(elapsed / a.steps * 1e3, 4), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": KIND_NAMES[wl.target_kind], "data": "synthetic",
+        "config": {"workload": f"{wl.name}: {KIND_NAMES[wl.target_kind]} target ({cfg.layers} layers, hidden "
+                               f"{cfg.hidden}) + bf16 draft, k={k}, {B} sequences, contexts {lo}-{hi}, "
+                               f"shuffled 16-token blocks", "batch": B, "k": k},
+        "verify_step_us": round(verify_us, 2), "draft_us": round(draft_us, 2), "acceptance": round(acceptance, 4),
+        "roofline": roofline, "cpu_baseline": None, "parity": None,
     }
     print(json.dumps(line), flush=True)
     return 0

@@ -89,13 +89,13 @@ struct fg_ctx {
     size_t pev_used = 0;
     struct Pending {
         int cls;
-        double bytes;
+        double bytes, flops;
         size_t ev;
     };
     std::vector<Pending> pending;
     struct Rec {
         int64_t n = 0;
-        double us = 0, bytes = 0;
+        double us = 0, bytes = 0, flops = 0;
     };
     Rec rec[12];
     // HIP graphs of the speculative step (draft rounds, verify pass), one
@@ -158,7 +158,7 @@ static void gemv(fg_ctx* c, int epi, const DMat& w, const GemvArgs& a) {
         return;
     }
     launch_gemv(c->stream, epi, w, a, e0, e1);
-    c->pending.push_back({w.kind * 4 + pg, gemv_bytes(w, a.m), i0});
+    c->pending.push_back({w.kind * 4 + pg, gemv_bytes(w, a.m), 2.0 * a.m * w.rows * w.cols, i0});
 }
 
 struct DLayer {
@@ -1069,8 +1069,9 @@ int fg_profile(fg_ctx* ctx, int32_t on) {
 }
 
 int fg_profile_read(fg_ctx* ctx, int32_t cap, int32_t* cls, int64_t* launches, double* us, double* bytes,
-                    int32_t reset) {
-    if (!ctx || cap < 0 || (cap > 0 && (!cls || !launches || !us || !bytes))) return fail(FG_E_ARG, "bad argument");
+                    double* flops, int32_t reset) {
+    if (!ctx || cap < 0 || (cap > 0 && (!cls || !launches || !us || !bytes || !flops)))
+        return fail(FG_E_ARG, "bad argument");
     HIPCHK(hipStreamSynchronize(ctx->stream));
     for (const auto& p : ctx->pending) {
         float ms = 0;
@@ -1079,6 +1080,7 @@ int fg_profile_read(fg_ctx* ctx, int32_t cap, int32_t* cls, int64_t* launches, d
         r.n++;
         r.us += ms * 1000.0;
         r.bytes += p.bytes;
+        r.flops += p.flops;
     }
     ctx->pending.clear();
     ctx->pev_used = 0;
@@ -1090,6 +1092,7 @@ int fg_profile_read(fg_ctx* ctx, int32_t cap, int32_t* cls, int64_t* launches, d
             launches[n] = ctx->rec[i].n;
             us[n] = ctx->rec[i].us;
             bytes[n] = ctx->rec[i].bytes;
+            flops[n] = ctx->rec[i].flops;
         }
         n++;
     }

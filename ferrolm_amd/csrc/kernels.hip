@@ -265,7 +265,6 @@ void launch_embed(hipStream_t st, const uint32_t* tokens, int stride, const uint
 // D layout of a 16x16 MFMA: lane l holds rows 4*(l/16)+r (r = 0..3, the
 // four pieces of activation row l/16 of the pass) of column l%16 (output n).
 // ---------------------------------------------------------------------------
-constexpr int YS = 64;  // row stride of the output tile in LDS
 
 template <int KIND, int NT, int EPI, int PG, int WMAX = 8>
 __global__ __launch_bounds__(64 * WMAX) void k_gemv(const GemvArgs a) {
@@ -273,9 +272,10 @@ __global__ __launch_bounds__(64 * WMAX) void k_gemv(const GemvArgs a) {
     // chunks loaded ahead per wave: about 16 B x 4 per lane and tile of weights in
     // flight; with 16 waves (4 per SIMD, 128 VGPRs) half as many, the other waves
     // of the SIMD covering each one's wait
-    constexpr int U = PG == 1 ? (KIND == INT4 ? 4 : 2) / (WMAX == 16 ? 2 : 1) : 1;
+    constexpr int U = PG == 1 ? (KIND == INT4 ? 4 : NT == 8 ? 1 : 2) / (WMAX == 16 ? 2 : 1) : 1;
     constexpr bool NEED_R = EPI == EPI_QKV || EPI == EPI_SILU || EPI == EPI_ARGMAX;
-    __shared__ float red[32 * 4 * 64];
+    constexpr int YS = NT * 16 > 64 ? NT * 16 : 64;  // row stride of the output tile in LDS
+    __shared__ float red[WMAX * NT * PG * 64];
     __shared__ __align__(16) float yt[16 * YS];
     __shared__ float rs[16];
     __shared__ float rtmp[16 * 17];
@@ -477,7 +477,7 @@ __global__ __launch_bounds__(64 * WMAX) void k_gemv(const GemvArgs a) {
 #pragma unroll
         for (int p = 0; p < PG; p++)
             if (p < np)
-                red[((wave * NT + t) * 4 + p) * 64 + lane] =
+                red[((wave * NT + t) * PG + p) * 64 + lane] =
                     Q ? accq[t][p] : ((accb[t][p][0] + accb[t][p][1]) + accb[t][p][2]) + accb[t][p][3];
     __syncthreads();
     if (NEED_R && !rfast && threadIdx.x < 16) {
@@ -488,7 +488,7 @@ __global__ __launch_bounds__(64 * WMAX) void k_gemv(const GemvArgs a) {
     for (int idx = threadIdx.x; idx < NT * np * 64; idx += blockDim.x) {
         const int t = idx / (np * 64), rem = idx % (np * 64), p = rem >> 6, l = rem & 63;
         float v = 0.0f;
-        for (int w = 0; w < W; w++) v += red[((w * NT + t) * 4 + p) * 64 + l];
+        for (int w = 0; w < W; w++) v += red[((w * NT + t) * PG + p) * 64 + l];
         yt[(p * 4 + (l >> 4)) * YS + t * 16 + (l & 15)] = v;
     }
     __syncthreads();
@@ -510,24 +510,28 @@ __global__ __launch_bounds__(64 * WMAX) void k_gemv(const GemvArgs a) {
         return;
     }
     if (EPI == EPI_ARGMAX) {
-        for (int idx = threadIdx.x; idx < rows * 32; idx += blockDim.x) {
-            const int r = idx >> 5, cc = idx & 31, row = pass0 * 4 + r, col = tile0 * 16 + cc;
+        for (int idx = threadIdx.x; idx < rows * COLS; idx += blockDim.x) {
+            const int r = idx / COLS, cc = idx % COLS, row = pass0 * 4 + r, col = tile0 * 16 + cc;
             const float v = yt[r * YS + cc] * rs[r];
             if (row < a.m && a.logits) a.logits[(size_t)row * a.N + col] = v;
             yt[r * YS + cc] = v != v ? -INFINITY : v;
         }
         __syncthreads();
-        if (threadIdx.x < rows) {
-            const int row = pass0 * 4 + threadIdx.x;
+        // (max, first index) of each row in each 32-column tile of the group
+        constexpr int SUB = COLS / 32;
+        if ((int)threadIdx.x < rows * SUB) {
+            const int r = threadIdx.x / SUB, j = threadIdx.x % SUB, row = pass0 * 4 + r;
             if (row < a.m) {
-                float bv = yt[threadIdx.x * YS];
+                const float* yr = &yt[r * YS + j * 32];
+                float bv = yr[0];
                 int bi = 0;
                 for (int cc = 1; cc < 32; cc++)
-                    if (yt[threadIdx.x * YS + cc] > bv) {
-                        bv = yt[threadIdx.x * YS + cc];
+                    if (yr[cc] > bv) {
+                        bv = yr[cc];
                         bi = cc;
                     }
-                a.best[(size_t)blockIdx.x * a.m + row] = make_float2(bv, __int_as_float(tile0 * 16 + bi));
+                a.best[((size_t)blockIdx.x * SUB + j) * a.m + row] =
+                    make_float2(bv, __int_as_float(tile0 * 16 + j * 32 + bi));
             }
         }
         return;
@@ -611,7 +615,7 @@ static void gemv_pg(hipStream_t st, const DMat& w, const GemvArgs& a, hipEvent_t
         }
         const int W = std::max(1, std::min(maxw, KC));
         launch_timed(k_gemv<KIND, NT, EPI, 1>, dim3(groups, 1, 1), dim3(64 * W), st, a, e0, e1);
-    } else {
+    } else if constexpr (NT <= 4) {
         const int pg = (a.p_total + 3) / 4;
         int W = (4096 + groups * pg - 1) / (groups * pg);
         W = std::max(1, std::min(std::min(W, maxw), KC));
@@ -626,7 +630,16 @@ static void gemv_kind(hipStream_t st, int epi, const DMat& w, const GemvArgs& a,
         case EPI_QKV: gemv_pg<KIND, 2, EPI_QKV>(st, w, a, e0, e1); break;
         case EPI_RESID: gemv_pg<KIND, 2, EPI_RESID>(st, w, a, e0, e1); break;
         case EPI_SILU: gemv_pg<KIND, 4, EPI_SILU>(st, w, a, e0, e1); break;
-        case EPI_ARGMAX: gemv_pg<KIND, 2, EPI_ARGMAX>(st, w, a, e0, e1); break;
+        case EPI_ARGMAX:
+            // bf16 lm_head: 128 columns per group when decoding (fewer, fuller workgroups)
+            if constexpr (KIND == BF16) {
+                if (a.p_total == 1 && w.n_tiles % 8 == 0) {
+                    gemv_pg<KIND, 8, EPI_ARGMAX>(st, w, a, e0, e1);
+                    break;
+                }
+            }
+            gemv_pg<KIND, 2, EPI_ARGMAX>(st, w, a, e0, e1);
+            break;
     }
 }
 
@@ -888,18 +901,29 @@ void launch_attention(hipStream_t st, const AttnArgs& a, int m, int consumer_kin
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ bool better(float v, int i, float bv, int bi) { return v > bv || (v == bv && i < bi); }
 
-__global__ __launch_bounds__(64) void k_argmax_final(const float2* __restrict__ best, int tiles, int rows,
-                                                     uint32_t* __restrict__ am, uint32_t* __restrict__ aux,
-                                                     int aux_stride, int aux_off) {
+__global__ __launch_bounds__(256) void k_argmax_final(const float2* __restrict__ best, int tiles, int rows,
+                                                      uint32_t* __restrict__ am, uint32_t* __restrict__ aux,
+                                                      int aux_stride, int aux_off) {
+    constexpr int UN = 8;  // partials per thread per pass, loaded before any is compared
+    __shared__ float sv[4];
+    __shared__ int si[4];
     const int r = blockIdx.x;
     float bv = -INFINITY;
     int bi = 0x7FFFFFFF;
-    for (int t = threadIdx.x; t < tiles; t += 64) {
-        const float2 e = best[(size_t)t * rows + r];
-        const int i = __float_as_int(e.y);
-        if (better(e.x, i, bv, bi)) {
-            bv = e.x;
-            bi = i;
+    for (int t0 = threadIdx.x; t0 < tiles; t0 += 256 * UN) {
+        float2 e[UN];
+#pragma unroll
+        for (int u = 0; u < UN; u++) {
+            const int t = t0 + u * 256;
+            e[u] = t < tiles ? best[(size_t)t * rows + r] : make_float2(-INFINITY, __int_as_float(0x7FFFFFFF));
+        }
+#pragma unroll
+        for (int u = 0; u < UN; u++) {
+            const int i = __float_as_int(e[u].y);
+            if (better(e[u].x, i, bv, bi)) {
+                bv = e[u].x;
+                bi = i;
+            }
         }
     }
     for (int o = 32; o > 0; o >>= 1) {
@@ -910,7 +934,17 @@ __global__ __launch_bounds__(64) void k_argmax_final(const float2* __restrict__ 
             bi = oi;
         }
     }
+    if ((threadIdx.x & 63) == 0) {
+        sv[threadIdx.x >> 6] = bv;
+        si[threadIdx.x >> 6] = bi;
+    }
+    __syncthreads();
     if (threadIdx.x == 0) {
+        for (int w = 1; w < 4; w++)
+            if (better(sv[w], si[w], bv, bi)) {
+                bv = sv[w];
+                bi = si[w];
+            }
         const uint32_t t = bi == 0x7FFFFFFF ? 0u : (uint32_t)bi;
         if (am) am[r] = t;
         if (aux) aux[(size_t)r * aux_stride + aux_off] = t;
@@ -920,7 +954,7 @@ __global__ __launch_bounds__(64) void k_argmax_final(const float2* __restrict__ 
 void launch_argmax_final(hipStream_t st, const float2* best, int tiles, int rows, uint32_t* argmax_out,
                          uint32_t* aux, int aux_stride, int aux_off) {
     if (rows <= 0) return;
-    hipLaunchKernelGGL(k_argmax_final, dim3(rows), dim3(64), 0, st, best, tiles, rows, argmax_out, aux, aux_stride,
+    hipLaunchKernelGGL(k_argmax_final, dim3(rows), dim3(256), 0, st, best, tiles, rows, argmax_out, aux, aux_stride,
                        aux_off);
 }
 

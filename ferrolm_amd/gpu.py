@@ -77,7 +77,7 @@ EXPORTS = {
     "fg_last_step_times": (C.c_int, [C.c_void_p, f32p]),
     "fg_profile": (C.c_int, [C.c_void_p, C.c_int32]),
     "fg_profile_read": (C.c_int, [C.c_void_p, C.c_int32, i32p, C.POINTER(C.c_int64), C.POINTER(C.c_double),
-                                  C.POINTER(C.c_double), C.c_int32]),
+                                  C.POINTER(C.c_double), C.POINTER(C.c_double), C.c_int32]),
     "fg_mat_upload": (C.c_int, [C.c_void_p, C.POINTER(FgMatrix), C.POINTER(C.c_void_p)]),
     "fg_mat_destroy": (None, [C.c_void_p]),
     "fg_matmul": (C.c_int, [C.c_void_p, C.c_void_p, f32p, C.c_int32, f32p, f32p]),
@@ -297,19 +297,20 @@ def profile(ctx: Context, on: bool) -> None:
 
 
 def profile_read(ctx: Context, reset: bool = True) -> list:
-    """Per kernel class: dict(kind, passes, launches, us, bytes)."""
+    """Per kernel class: dict(kind, passes, launches, us, bytes, flops)."""
     cap = 12
     cls = np.zeros(cap, np.int32)
     n = np.zeros(cap, np.int64)
     us = np.zeros(cap, np.float64)
     by = np.zeros(cap, np.float64)
+    fl = np.zeros(cap, np.float64)
+    dp = C.POINTER(C.c_double)
     r = lib().fg_profile_read(ctx.h, cap, ptr(cls, i32p), n.ctypes.data_as(C.POINTER(C.c_int64)),
-                              us.ctypes.data_as(C.POINTER(C.c_double)), by.ctypes.data_as(C.POINTER(C.c_double)),
-                              int(reset))
+                              us.ctypes.data_as(dp), by.ctypes.data_as(dp), fl.ctypes.data_as(dp), int(reset))
     if r < 0:
         check(r)
     return [dict(kind=KIND_LABEL[int(cls[i]) // 4], passes=(1, 2, 4)[int(cls[i]) % 4], launches=int(n[i]),
-                 us=float(us[i]), bytes=float(by[i])) for i in range(min(r, cap))]
+                 us=float(us[i]), bytes=float(by[i]), flops=float(fl[i])) for i in range(min(r, cap))]
 
 
 class Mat:

@@ -84,19 +84,36 @@ class Batch:
         self.computed, self.dcomp = [0] * n, [0] * n
         self.stats = GenStats()
 
-    def prefill(self) -> list:
-        """The first token of every sequence."""
-        chunks = []
+    def prefill(self, max_tokens: int = 0) -> list:
+        """The first token of every sequence. With max_tokens, the prompts go
+        through forwards of at most that many tokens (a long prompt in chunks, as
+        the reference's token budget does, src/engine.rs:455); otherwise all of
+        them in one forward."""
         for i, t in enumerate(self.tokens):
             if not self.tpool.grow(self.tb[i], len(t)):
                 raise RuntimeError("out of cache blocks")
-            chunks.append((t, 0, self.tb[i], gpu.LOGITS_LAST))
-        o = gpu.forward(self.ctx, self.target, self.tkv, chunks, logits=False)
-        first = []
+        first = [0] * len(self.tokens)
+        budget = max_tokens or sum(len(t) for t in self.tokens)
+        work = [(i, 0) for i in range(len(self.tokens))]  # (sequence, next position)
+        while work:
+            chunks, rows, room = [], [], budget
+            while work and room > 0:
+                i, pos = work.pop(0)
+                t = self.tokens[i]
+                n = min(len(t) - pos, room)
+                last = pos + n == len(t)
+                chunks.append((t[pos:pos + n], pos, self.tb[i], gpu.LOGITS_LAST if last else gpu.LOGITS_NONE))
+                if last:
+                    rows.append(i)
+                else:
+                    work.insert(0, (i, pos + n))
+                room -= n
+            o = gpu.forward(self.ctx, self.target, self.tkv, chunks, logits=False)
+            for r, i in enumerate(rows):
+                first[i] = int(o.argmax[r])
         for i, t in enumerate(self.tokens):
             self.computed[i] = len(t)
-            t.append(int(o.argmax[i]))
-            first.append(t[-1])
+            t.append(first[i])
         return first
 
     def step(self) -> list:

@@ -187,11 +187,12 @@ int fg_last_step_times(const fg_ctx* ctx, float* us3);
  * record per kernel class and returns up to `cap` records:
  * cls[i] = format*4 + (rows-per-pass group: 1, 2 or 4 passes -> 0, 1, 2),
  * launches[i], us[i] (summed device time), bytes[i] (summed algorithmic
- * bytes: codes + scales + activations in + outputs, per launch).
+ * bytes: codes + scales + activations in + outputs, per launch), flops[i]
+ * (summed algorithmic flops, 2 x rows x n x k per launch).
  * Returns the record count (or a negative error). reset != 0 clears. */
 int fg_profile(fg_ctx* ctx, int32_t on);
 int fg_profile_read(fg_ctx* ctx, int32_t cap, int32_t* cls, int64_t* launches,
-                    double* us, double* bytes, int32_t reset);
+                    double* us, double* bytes, double* flops, int32_t reset);
 
 /* ---- single matrix (kernels::matmul, src/kernels.rs:249-275) ----------- */
 int fg_mat_upload(fg_ctx* ctx, const fg_matrix* w, fg_mat** out);
