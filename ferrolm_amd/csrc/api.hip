@@ -235,15 +235,15 @@ static inline int qcode(const uint8_t* q, int kind, int K, int r, int k) {
     return (c < 16 ? (b & 15) : (b >> 4)) - 8;
 }
 
-// Device row r of the gate/up matrix (interleaved in blocks of 32, see
+// Device row r of the gate/up matrix (interleaved in blocks of il rows, see
 // internal.h) and the source row it holds.
-static inline int src_row(int r, int inter) {
+static inline int src_row(int r, int inter, int il) {
     if (inter <= 0) return r;
-    const int blk = r / 64, within = r % 64;
-    return within < 32 ? blk * 32 + within : inter + blk * 32 + within - 32;
+    const int blk = r / (2 * il), within = r % (2 * il);
+    return within < il ? blk * il + within : inter + blk * il + within - il;
 }
 
-static int repack(const fg_matrix& src, DMat& d, std::vector<uint8_t>& w, std::vector<float>& s, int inter) {
+static int repack(const fg_matrix& src, DMat& d, std::vector<uint8_t>& w, std::vector<float>& s, int inter, int il) {
     if (src.rows <= 0 || src.cols <= 0 || src.rows % 32 || (src.format != FG_BF16 && src.cols % 32))
         return fail(FG_E_SHAPE, "matrix rows must be a multiple of 32 (and cols of 32 when quantized)");
     if (src.format == FG_BF16 && !src.bf16) return fail(FG_E_ARG, "bf16 matrix without data");
@@ -263,7 +263,7 @@ static int repack(const fg_matrix& src, DMat& d, std::vector<uint8_t>& w, std::v
         parallel_for(d.n_tiles, [&](int t) {
             for (int kb = 0; kb < KB; kb++)
                 for (int l = 0; l < 64; l++) {
-                    const int n = src_row(t * 16 + l % 16, inter), k0 = kb * 32 + 8 * (l / 16);
+                    const int n = src_row(t * 16 + l % 16, inter, il), k0 = kb * 32 + 8 * (l / 16);
                     uint16_t* o = out + (((size_t)t * KB + kb) * 64 + l) * 8;
                     for (int sl = 0; sl < 8; sl++) o[sl] = k0 + sl < K ? src.bf16[(size_t)n * K + k0 + sl] : 0;
                 }
@@ -278,7 +278,7 @@ static int repack(const fg_matrix& src, DMat& d, std::vector<uint8_t>& w, std::v
     parallel_for(d.n_tiles, [&](int t) {
         for (int kb = 0; kb < G; kb++)
             for (int r = 0; r < 16; r++) {
-                const int n = src_row(t * 16 + r, inter), p = n / 32, c = n % 32;
+                const int n = src_row(t * 16 + r, inter, il), p = n / 32, c = n % 32;
                 float v = src.s[((size_t)p * G + kb) * 32 + c];
                 if (q4) v *= 0.0625f;
                 s[(((size_t)t * KC + kb / 4) * 16 + r) * 4 + kb % 4] = v;
@@ -290,7 +290,7 @@ static int repack(const fg_matrix& src, DMat& d, std::vector<uint8_t>& w, std::v
         parallel_for(d.n_tiles, [&](int t) {
             for (int kb = 0; kb < G; kb++)
                 for (int l = 0; l < 64; l++) {
-                    const int n = src_row(t * 16 + l % 16, inter), k0 = kb * 32 + 8 * (l / 16);
+                    const int n = src_row(t * 16 + l % 16, inter, il), k0 = kb * 32 + 8 * (l / 16);
                     uint32_t word = 0;
                     for (int sl = 0; sl < 8; sl++) {
                         const int code = qcode(src.q, INT4, K, n, k0 + sl);
@@ -306,7 +306,7 @@ static int repack(const fg_matrix& src, DMat& d, std::vector<uint8_t>& w, std::v
         parallel_for(d.n_tiles, [&](int t) {
             for (int kb = 0; kb < G; kb++)
                 for (int l = 0; l < 64; l++) {
-                    const int n = src_row(t * 16 + l % 16, inter), k0 = kb * 32 + 8 * (l / 16);
+                    const int n = src_row(t * 16 + l % 16, inter, il), k0 = kb * 32 + 8 * (l / 16);
                     int8_t* o = out + (((size_t)t * (KB / 2) + kb / 2) * 64 + l) * 16 + (kb % 2) * 8;
                     for (int sl = 0; sl < 8; sl++) o[sl] = (int8_t)qcode(src.q, INT8, K, n, k0 + sl);
                 }
@@ -315,12 +315,13 @@ static int repack(const fg_matrix& src, DMat& d, std::vector<uint8_t>& w, std::v
     return 0;
 }
 
-static int upload_mat(const fg_matrix& src, DMat& d, std::vector<void*>* allocs, int inter = 0) {
+static int upload_mat(const fg_matrix& src, DMat& d, std::vector<void*>* allocs, int inter = 0, int il = 32) {
     std::vector<uint8_t> w;
     std::vector<float> s;
     if (inter > 0 && (inter % 32 || src.rows != 2 * inter))
         return fail(FG_E_SHAPE, "intermediate size must be a multiple of 32");
-    int rc = repack(src, d, w, s, inter);
+    d.il = inter > 0 ? il : 0;
+    int rc = repack(src, d, w, s, inter, il);
     if (rc) return rc;
     d.w_bytes = w.size();
     d.s_bytes = s.size() * 4;
@@ -492,6 +493,11 @@ struct Work {
 };
 
 static int kind_of(const DMat& m) { return m.kind; }
+
+// n-tiles per workgroup of a projection with fewer than 256 tiles: one, so that
+// it spreads over twice the CUs (a CU streams only about 22 GB/s), unless it
+// finishes int8 pieces, whose per-block scale needs a whole 32-column k-block.
+static int narrow_nt(const DMat& w, bool int8_pieces) { return w.n_tiles < 256 && !int8_pieces ? 1 : 2; }
 static int qkv_dim(const fg_config& c) { return (c.heads + 2 * c.kv_heads) * c.head_dim; }
 
 static size_t layout_work(const fg_model* m, const Plan& P, Work& w, void* base) {
@@ -505,7 +511,7 @@ static size_t layout_work(const fg_model* m, const Plan& P, Work& w, void* base)
     w.lm_passes = (S + 3) / 4;
     const int passes = std::max(w.passes, w.lm_passes);
     w.x = cv.take<float>((size_t)t * H);
-    w.ss = cv.take<float>((size_t)(H / 32) * t);
+    w.ss = cv.take<float>((size_t)(H / 16) * t);
     for (int i = 0; i < 2; i++) {
         w.pa[i] = cv.take<uint8_t>((size_t)kb_max * passes * 64 * 16);
         w.pxs[i] = cv.take<float>((size_t)kb_max * passes * 4);
@@ -582,6 +588,7 @@ static int run_forward(fg_ctx* ctx, const fg_model* m, fg_kv* kv, const Plan& P,
     aa.bs = kv->block_size;
     aa.scale = 1.0f / sqrtf((float)hd);
 
+    int ss_cols = 32;  // columns per sum-of-squares partial in w.ss (the embedding writes one per k-block)
     for (int li = 0; li < L; li++) {
         const DLayer& l = m->layers[li];
         // q/k/v of the normed rows: rinv from the sum-of-squares partials
@@ -590,10 +597,11 @@ static int run_forward(fg_ctx* ctx, const fg_model* m, fg_kv* kv, const Plan& P,
         g.ldo = qkv_dim(c);
         g.bias = l.bqkv;
         g.ss_in = w.ss;
-        g.ss_tiles = H / 32;
+        g.ss_tiles = H / ss_cols;
         g.ss_m = t;
         g.hidden = H;
         g.eps = c.rms_eps;
+        g.nt = narrow_nt(l.wqkv, false);
         gemv(ctx, EPI_QKV, l.wqkv, g);
         // attention (RoPE, cache write) and the merge into wo's pieces
         aa.kc = kv->k + li * kv->layer_floats();
@@ -613,12 +621,14 @@ static int run_forward(fg_ctx* ctx, const fg_model* m, fg_kv* kv, const Plan& P,
         g.pa_kind = kind_of(l.w_gate_up);
         g.pa_passes = passes;
         g.pa_kb = l.w_gate_up.kb;
+        g.nt = narrow_nt(l.wo, g.pa_kind != BF16);
+        ss_cols = 16 * g.nt;
         gemv(ctx, EPI_RESID, l.wo, g);
         cur ^= 1;
         // gate/up with SiLU; pieces of the activation for down
         g = gemv_args(l.w_gate_up, pieces(w, cur, l.w_gate_up.kb, passes), t);
         g.ss_in = w.ss;
-        g.ss_tiles = H / 32;
+        g.ss_tiles = H / ss_cols;
         g.ss_m = t;
         g.hidden = H;
         g.eps = c.rms_eps;
@@ -644,6 +654,8 @@ static int run_forward(fg_ctx* ctx, const fg_model* m, fg_kv* kv, const Plan& P,
             g.pa_passes = passes;
             g.pa_kb = nl.wqkv.kb;
         }
+        g.nt = narrow_nt(l.w_down, g.pa && g.pa_kind != BF16);
+        ss_cols = 16 * g.nt;
         gemv(ctx, EPI_RESID, l.w_down, g);
         cur ^= 1;
         if (hidden_host)
@@ -658,7 +670,7 @@ static int run_forward(fg_ctx* ctx, const fg_model* m, fg_kv* kv, const Plan& P,
     launch_pieces(st, kind_of(m->lm_head), w.x, H, P.S, H, m->norm, sel, pl);
     GemvArgs g = gemv_args(m->lm_head, pl, P.S);
     g.ss_in = w.ss;
-    g.ss_tiles = H / 32;
+    g.ss_tiles = H / ss_cols;
     g.ss_m = t;
     g.hidden = H;
     g.eps = c.rms_eps;
@@ -752,7 +764,10 @@ int fg_model_upload(fg_ctx* ctx, const fg_config* cfg, const fg_layer* layers, c
         if (c.qkv_bias && (rc = upload_vec(s.bqkv, qkv, &d.bqkv, m->allocs))) return bad(rc);
         if ((rc = upload_mat(s.wqkv, d.wqkv, &m->allocs))) return bad(rc);
         if ((rc = upload_mat(s.wo, d.wo, &m->allocs))) return bad(rc);
-        if ((rc = upload_mat(s.w_gate_up, d.w_gate_up, &m->allocs, c.intermediate))) return bad(rc);
+        // bf16 gate/up feeding a bf16 down: 16-row blocks, so a 32-row output group
+        // finishes 16 channels (bf16 pieces carry no per-block scale)
+        const int il = s.w_gate_up.format == FG_BF16 && s.w_down.format == FG_BF16 ? 16 : 32;
+        if ((rc = upload_mat(s.w_gate_up, d.w_gate_up, &m->allocs, c.intermediate, il))) return bad(rc);
         if ((rc = upload_mat(s.w_down, d.w_down, &m->allocs))) return bad(rc);
         ref += d.wqkv.ref_bytes + d.wo.ref_bytes + d.w_gate_up.ref_bytes + d.w_down.ref_bytes;
     }

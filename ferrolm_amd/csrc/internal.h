@@ -28,8 +28,10 @@ namespace fg {
 // consecutive memory.
 //
 // Row order: the stacked gate/up matrix is stored interleaved in blocks of
-// 32, [gate 32c..32c+31, up 32c..32c+31] for c = 0.., so one 64-row output
-// tile holds the gate and up values of 32 intermediate channels.
+// il rows (DMat::il), [gate il*c .. +il-1, up il*c .. +il-1] for c = 0.., so
+// one 2*il-row output group holds the gate and up values of il intermediate
+// channels. il is 32 when the down projection takes int8 pieces (their scale
+// spans a whole k-block) and 16 for bf16 pieces.
 // ---------------------------------------------------------------------------
 enum { BF16 = 0, INT8 = 1, INT4 = 2 };
 
@@ -37,6 +39,7 @@ struct DMat {
     int kind = 0;
     int rows = 0, cols = 0;   // N, K (unpadded)
     int n_tiles = 0, kb = 0;  // rows/16, padded K/32 (multiple of 4)
+    int il = 0;               // gate/up interleave block (0: not interleaved)
     void* w = nullptr;        // packed codes / bf16
     float* s = nullptr;       // packed scales (quantized kinds)
     size_t w_bytes = 0, s_bytes = 0;
@@ -75,6 +78,7 @@ struct GemvArgs {
     const uint8_t* XA = nullptr;  // input pieces
     const float* XS = nullptr;
     int m = 0, p_total = 0;
+    int nt = 2;  // n-tiles per workgroup for STORE/QKV/RESID (1 or 2; SILU takes 2*il/16)
     // STORE / QKV
     float* out = nullptr;
     int ldo = 0;
@@ -87,7 +91,7 @@ struct GemvArgs {
     // RESID / SILU
     float* x = nullptr;
     int ldx = 0;
-    float* ss_out = nullptr;
+    float* ss_out = nullptr;        // [group][ss_m] sums of squares of each group's 16*nt columns
     const float* g_next = nullptr;  // norm weight applied to the next consumer's input (nullptr: none)
     void* pa = nullptr;             // next consumer's pieces (nullptr: none)
     float* pxs = nullptr;

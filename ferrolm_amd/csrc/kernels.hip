@@ -275,6 +275,9 @@ __global__ __launch_bounds__(64 * WMAX) void k_gemv(const GemvArgs a) {
     constexpr int U = PG == 1 ? (KIND == INT4 ? 4 : NT == 8 ? 1 : 2) / (WMAX == 16 ? 2 : 1) : 1;
     constexpr bool NEED_R = EPI == EPI_QKV || EPI == EPI_SILU || EPI == EPI_ARGMAX;
     constexpr int YS = NT * 16 > 64 ? NT * 16 : 64;  // row stride of the output tile in LDS
+    // finished output columns per group (EPI_RESID, EPI_SILU): 16 or 32, a half
+    // or a whole k-block of the next consumer
+    constexpr int OC = EPI == EPI_SILU ? NT * 8 : NT * 16;
     __shared__ float red[WMAX * NT * PG * 64];
     __shared__ __align__(16) float yt[16 * YS];
     __shared__ float rs[16];
@@ -335,12 +338,12 @@ __global__ __launch_bounds__(64 * WMAX) void k_gemv(const GemvArgs a) {
         pre[it] = 0.0f;
         if (idx < rows * COLS) {
             const int r = idx / COLS, cc = idx % COLS, row = pass0 * 4 + r;
-            if (EPI == EPI_RESID && row < a.m) pre[it] = a.x[(size_t)row * a.ldx + blockIdx.x * 32 + cc];
+            if (EPI == EPI_RESID && row < a.m) pre[it] = a.x[(size_t)row * a.ldx + blockIdx.x * OC + cc];
             if ((EPI == EPI_QKV || EPI == EPI_STORE) && a.bias) pre[it] = a.bias[tile0 * 16 + cc];
         }
     }
     float gv = 1.0f;
-    if (EPI == EPI_RESID && a.g_next && threadIdx.x < 32) gv = a.g_next[blockIdx.x * 32 + threadIdx.x];
+    if (EPI == EPI_RESID && a.g_next && threadIdx.x < OC) gv = a.g_next[blockIdx.x * OC + threadIdx.x];
 
     float accq[NT][PG];
     f32x4 accb[NT][PG];
@@ -469,7 +472,7 @@ __global__ __launch_bounds__(64 * WMAX) void k_gemv(const GemvArgs a) {
             if (idx < rows * COLS) et[(idx / COLS) * YS + idx % COLS] = pre[it];
         }
     }
-    if (EPI == EPI_RESID && threadIdx.x < 32) gs[threadIdx.x] = gv;
+    if (EPI == EPI_RESID && threadIdx.x < OC) gs[threadIdx.x] = gv;
 
     // reduce across waves
 #pragma unroll
@@ -536,55 +539,71 @@ __global__ __launch_bounds__(64 * WMAX) void k_gemv(const GemvArgs a) {
         }
         return;
     }
-    // EPI_RESID / EPI_SILU finish the group's 32 output columns: one k-block of
-    // the next consumer. (A) every thread finishes some of the rows x 32 values
-    // into LDS; (B) one wave forms each row's sum of squares (EPI_RESID);
+    // EPI_RESID / EPI_SILU finish the group's OC output columns: one k-block of
+    // the next consumer (OC 32), or half of one (OC 16, bf16 pieces only: they
+    // carry no per-block scale). (A) every thread finishes some of the rows x OC
+    // values into LDS; (B) one wave forms each row's sum of squares (EPI_RESID);
     // (C) up to four waves per pass write the pieces, two of a lane's eight
     // inputs each, so the conversions run on several SIMDs at once.
-    for (int idx = threadIdx.x; idx < rows * 32; idx += blockDim.x) {
-        const int r = idx >> 5, cc = idx & 31, row = pass0 * 4 + r;
+    static_assert(EPI != EPI_RESID && EPI != EPI_SILU || OC == 16 || OC == 32, "16 or 32 finished columns");
+    for (int idx = threadIdx.x; idx < rows * OC; idx += blockDim.x) {
+        const int r = idx / OC, cc = idx % OC, row = pass0 * 4 + r;
         const bool live = row < a.m;
         if (EPI == EPI_RESID) {
             const float xn = live ? et[r * YS + cc] + yt[r * YS + cc] : 0.0f;
-            if (live) a.x[(size_t)row * a.ldx + blockIdx.x * 32 + cc] = xn;
+            if (live) a.x[(size_t)row * a.ldx + blockIdx.x * OC + cc] = xn;
             yt[r * YS + cc] = xn;
             vt[r * YS + cc] = a.g_next ? gs[cc] * xn : xn;
         } else {
-            const float gt = yt[r * YS + cc] * rs[r], up = yt[r * YS + 32 + cc] * rs[r];
+            const float gt = yt[r * YS + cc] * rs[r], up = yt[r * YS + OC + cc] * rs[r];
             vt[r * YS + cc] = live ? gt / (1.0f + dev_exp(-gt)) * up : 0.0f;
         }
     }
     __syncthreads();
     if (EPI == EPI_RESID && wave == W - 1)
         for (int p = 0; p < np; p++) {
-            // row 4p + lane/16: lane j of 16 takes columns 2j, 2j+1
+            // row 4p + lane/16: lane j of 16 takes columns j*OC/16 .. +OC/16-1
             const int r = p * 4 + (lane >> 4), j = lane & 15, row = pass0 * 4 + r;
-            const float x0 = yt[r * YS + 2 * j], x1 = yt[r * YS + 2 * j + 1];
-            float ssq = fmaf(x1, x1, x0 * x0);
+            float ssq;
+            if (OC == 32) {
+                const float x0 = yt[r * YS + 2 * j], x1 = yt[r * YS + 2 * j + 1];
+                ssq = fmaf(x1, x1, x0 * x0);
+            } else {
+                const float x0 = yt[r * YS + j];
+                ssq = x0 * x0;
+            }
             ssq += __shfl_xor(ssq, 8);
             ssq += __shfl_xor(ssq, 4);
             ssq += __shfl_xor(ssq, 2);
             ssq += __shfl_xor(ssq, 1);
             if (j == 0 && row < a.m) a.ss_out[(size_t)blockIdx.x * a.ss_m + row] = ssq;
         }
+    // the consumer's k-block and, for OC 16, which half of it (lanes 32h .. 32h+31)
+    const int pkb = blockIdx.x * OC / 32, half = OC == 16 ? (int)(blockIdx.x & 1) : 0;
     if (a.pa)
         for (int t = wave; t < np * 4; t += W) {
             const int p = t >> 2, pair = t & 3;
             const int c = lane & 15, r = p * 4 + (c >> 2), q = lane >> 4;
-            const float* vr = &vt[r * YS + q * 8];
+            if (OC == 16 && (q >> 1) != half) continue;
+            const float* vr = &vt[r * YS + (OC == 16 ? q & 1 : q) * 8];
             const float4 v0 = *(const float4*)vr, v1 = *(const float4*)(vr + 4);
-            const float mx = fmaxf(fmaxf(fmaxf(fabsf(v0.x), fabsf(v0.y)), fmaxf(fabsf(v0.z), fabsf(v0.w))),
-                                   fmaxf(fmaxf(fabsf(v1.x), fabsf(v1.y)), fmaxf(fabsf(v1.z), fabsf(v1.w))));
             const float2 xp = *(const float2*)(vr + 2 * pair);
-            write_pieces_pair_kind(a.pa_kind, xp.x, xp.y, mx, pair, blockIdx.x, pass0 + p, a.pa_passes,
-                                   pass0 * 4 + r, c & 3, lane, a.pa, a.pxs);
+            if (OC == 16) {
+                write_pieces_pair<BF16>(xp.x, xp.y, 0.0f, pair, pkb, pass0 + p, a.pa_passes, pass0 * 4 + r, c & 3,
+                                        lane, a.pa, a.pxs);
+            } else {
+                const float mx = fmaxf(fmaxf(fmaxf(fabsf(v0.x), fabsf(v0.y)), fmaxf(fabsf(v0.z), fabsf(v0.w))),
+                                       fmaxf(fmaxf(fabsf(v1.x), fabsf(v1.y)), fmaxf(fabsf(v1.z), fabsf(v1.w))));
+                write_pieces_pair_kind(a.pa_kind, xp.x, xp.y, mx, pair, pkb, pass0 + p, a.pa_passes, pass0 * 4 + r,
+                                       c & 3, lane, a.pa, a.pxs);
+            }
         }
     // the consumer's zero padding past the last k-block, one wave per (k-block, pass)
     if (a.pa && blockIdx.x == gridDim.x - 1) {
         const float z[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-        const int c = lane & 15;
-        for (int idx = wave; idx < (a.pa_kb - (int)gridDim.x) * np; idx += W) {
-            const int kb2 = gridDim.x + idx / np, p = idx % np;
+        const int c = lane & 15, covered = (int)gridDim.x * OC / 32;
+        for (int idx = wave; idx < (a.pa_kb - covered) * np; idx += W) {
+            const int kb2 = covered + idx / np, p = idx % np;
             write_pieces_kind(a.pa_kind, z, kb2, pass0 + p, a.pa_passes, pass0 * 4 + p * 4 + (c >> 2), c & 3, lane,
                               a.pa, a.pxs);
         }
@@ -627,9 +646,24 @@ template <int KIND>
 static void gemv_kind(hipStream_t st, int epi, const DMat& w, const GemvArgs& a, hipEvent_t e0, hipEvent_t e1) {
     switch (epi) {
         case EPI_STORE: gemv_pg<KIND, 2, EPI_STORE>(st, w, a, e0, e1); break;
-        case EPI_QKV: gemv_pg<KIND, 2, EPI_QKV>(st, w, a, e0, e1); break;
-        case EPI_RESID: gemv_pg<KIND, 2, EPI_RESID>(st, w, a, e0, e1); break;
-        case EPI_SILU: gemv_pg<KIND, 4, EPI_SILU>(st, w, a, e0, e1); break;
+        case EPI_QKV:
+            if (a.nt == 1)
+                gemv_pg<KIND, 1, EPI_QKV>(st, w, a, e0, e1);
+            else
+                gemv_pg<KIND, 2, EPI_QKV>(st, w, a, e0, e1);
+            break;
+        case EPI_RESID:
+            if (a.nt == 1)
+                gemv_pg<KIND, 1, EPI_RESID>(st, w, a, e0, e1);
+            else
+                gemv_pg<KIND, 2, EPI_RESID>(st, w, a, e0, e1);
+            break;
+        case EPI_SILU:
+            if (w.il == 16)
+                gemv_pg<KIND, 2, EPI_SILU>(st, w, a, e0, e1);
+            else
+                gemv_pg<KIND, 4, EPI_SILU>(st, w, a, e0, e1);
+            break;
         case EPI_ARGMAX:
             // bf16 lm_head: 128 columns per group when decoding (fewer, fuller workgroups)
             if constexpr (KIND == BF16) {
