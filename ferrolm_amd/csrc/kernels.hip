@@ -728,39 +728,34 @@ __global__ __launch_bounds__(256) void k_attn(AttnArgs a) {
     for (int q = tid; q < Q; q += 256) lim[q] = pos_of_row0 + q / G;
     // Every load of the span is issued before anything waits on one: the keys
     // and values (from the cache, or from the q/k/v rows for this chunk's new
-    // positions, with their cos/sin) into registers, then q. One round trip.
+    // positions) with the cos/sin of their positions into registers, then q.
+    // One round trip. The loads take no branches (a value loaded under a
+    // condition gets copied at the join, which waits on it): positions past
+    // the span read its last position, and the LDS stores below select.
     constexpr int KI = P * (HALF / 4), KIT = (KI + 255) / 256;
     constexpr int VI = P * (HD / 4), VIT = (VI + 255) / 256;
     float4 ku[KIT], kw[KIT], kcs[KIT], ksn[KIT], vv[VIT];
+    auto src_of = [&](int p, int col) -> const float* {  // position p's key (col 0) or value (col kvd)
+        const bool cached = p < cpos0;
+        const size_t crow = cached ? 0 : (size_t)(crow0 + p - cpos0);
+        return cached ? (col ? a.vc : a.kc) + ((blk((p - p0) >> 4) * a.nkv + h) * 16 + (p & 15)) * HD
+                      : a.qkv + crow * a.ld + qd + col + h * HD;
+    };
 #pragma unroll
     for (int it = 0; it < KIT; it++) {
-        const int i = tid + it * 256;
-        const float4 z = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-        ku[it] = kw[it] = kcs[it] = ksn[it] = z;
-        if (i < KI) {
-            const int o = i / (HALF / 4), d = (i % (HALF / 4)) * 4, p = p0 + o;
-            if (p < p1) {
-                const float* kp = p < cpos0 ? a.kc + ((blk(o >> 4) * a.nkv + h) * 16 + (p & 15)) * HD
-                                            : a.qkv + (size_t)(crow0 + p - cpos0) * a.ld + qd + h * HD;
-                ku[it] = *(const float4*)(kp + d);
-                kw[it] = *(const float4*)(kp + d + HALF);
-                if (p >= cpos0) {
-                    kcs[it] = *(const float4*)(a.cos_t + (size_t)p * HALF + d);
-                    ksn[it] = *(const float4*)(a.sin_t + (size_t)p * HALF + d);
-                }
-            }
-        }
+        const int i = min(tid + it * 256, KI - 1);
+        const int d = (i % (HALF / 4)) * 4, p = min(p0 + i / (HALF / 4), p1 - 1);
+        const float* kp = src_of(p, 0);
+        ku[it] = *(const float4*)(kp + d);
+        kw[it] = *(const float4*)(kp + d + HALF);
+        kcs[it] = *(const float4*)(a.cos_t + (size_t)p * HALF + d);
+        ksn[it] = *(const float4*)(a.sin_t + (size_t)p * HALF + d);
     }
 #pragma unroll
     for (int it = 0; it < VIT; it++) {
-        const int i = tid + it * 256;
-        vv[it] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-        if (i < VI) {
-            const int o = i / (HD / 4), d = (i % (HD / 4)) * 4, p = p0 + o;
-            if (p < p1)
-                vv[it] = p < cpos0 ? *(const float4*)(a.vc + ((blk(o >> 4) * a.nkv + h) * 16 + (p & 15)) * HD + d)
-                                   : *(const float4*)(a.qkv + (size_t)(crow0 + p - cpos0) * a.ld + qd + kvd + h * HD + d);
-        }
+        const int i = min(tid + it * 256, VI - 1);
+        const int d = (i % (HD / 4)) * 4, p = min(p0 + i / (HD / 4), p1 - 1);
+        vv[it] = *(const float4*)(src_of(p, kvd) + d);
     }
     // q, rotated: 4 (d, d + HALF) pairs per item
     for (int i = tid; i < Q * (HALF / 4); i += 256) {
@@ -788,18 +783,25 @@ __global__ __launch_bounds__(256) void k_attn(AttnArgs a) {
             const float a2[4] = {kw[it].x, kw[it].y, kw[it].z, kw[it].w};
             const float cc[4] = {kcs[it].x, kcs[it].y, kcs[it].z, kcs[it].w};
             const float ss[4] = {ksn[it].x, ksn[it].y, ksn[it].z, ksn[it].w};
-            const bool rot = p < p1 && p >= cpos0;
+            const bool live = p < p1, rot = live && p >= cpos0;
 #pragma unroll
             for (int e = 0; e < 4; e++) {
-                ks[o][d + e] = rot ? __fadd_rn(__fmul_rn(a1[e], cc[e]), __fmul_rn(-a2[e], ss[e])) : a1[e];
-                ks[o][d + HALF + e] = rot ? __fadd_rn(__fmul_rn(a2[e], cc[e]), __fmul_rn(a1[e], ss[e])) : a2[e];
+                const float r1 = rot ? __fadd_rn(__fmul_rn(a1[e], cc[e]), __fmul_rn(-a2[e], ss[e])) : a1[e];
+                const float r2 = rot ? __fadd_rn(__fmul_rn(a2[e], cc[e]), __fmul_rn(a1[e], ss[e])) : a2[e];
+                ks[o][d + e] = live ? r1 : 0.0f;
+                ks[o][d + HALF + e] = live ? r2 : 0.0f;
             }
         }
     }
 #pragma unroll
     for (int it = 0; it < VIT; it++) {
         const int i = tid + it * 256;
-        if (i < VI) *(float4*)&vs[i / (HD / 4)][(i % (HD / 4)) * 4] = vv[it];
+        if (i < VI) {
+            const bool live = p0 + i / (HD / 4) < p1;
+            *(float4*)&vs[i / (HD / 4)][(i % (HD / 4)) * 4] =
+                make_float4(live ? vv[it].x : 0.0f, live ? vv[it].y : 0.0f, live ? vv[it].z : 0.0f,
+                            live ? vv[it].w : 0.0f);
+        }
     }
     __syncthreads();
     // this group's new rows in the span go to the cache
@@ -870,22 +872,35 @@ __global__ __launch_bounds__(64) void k_merge_pieces(AttnArgs a, int m, void* __
         const int qi = mr.x + j, wi0 = mr.y, ns = mr.z;
         const size_t stride = (size_t)a.nkv * QM * (HD + 2);
         const float* base = a.part + ((size_t)wi0 * a.nkv * QM + (size_t)h * QM + qi) * (HD + 2);
-        // online merge of this lane's spans (every fourth), one read of each
+        // online merge of this lane's spans (every fourth), SB per round trip:
+        // every load of a batch is issued (from clamped, always valid
+        // addresses) before the first is used; spans past ns are masked out
         float M = -INFINITY, L = 0.0f, O[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-#pragma unroll 4
-        for (int s = piece; s < ns; s += 4) {
-            const float* p = base + s * stride;
-            const float2 st = *(const float2*)p;
-            const float2 o01 = *(const float2*)(p + 2 + d0), o23 = *(const float2*)(p + 4 + d0);
-            const float2 o45 = *(const float2*)(p + 6 + d0), o67 = *(const float2*)(p + 8 + d0);
-            const float ov[8] = {o01.x, o01.y, o23.x, o23.y, o45.x, o45.y, o67.x, o67.y};
-            const float nM = fmaxf(M, st.x);
-            const float fo = M == -INFINITY ? 0.0f : dev_exp(M - nM);
-            const float w = st.x == -INFINITY ? 0.0f : dev_exp(st.x - nM);
-            L = fmaf(st.y, w, L * fo);
+        constexpr int SB = 8;
+        for (int s0 = piece; s0 < ns; s0 += 4 * SB) {
+            float2 st[SB];
+            float ov[SB][8];
 #pragma unroll
-            for (int e = 0; e < 8; e++) O[e] = fmaf(ov[e], w, O[e] * fo);
-            M = nM;
+            for (int b = 0; b < SB; b++) {
+                const float* p = base + min(s0 + 4 * b, ns - 1) * stride;
+                st[b] = *(const float2*)p;
+                const float2 o01 = *(const float2*)(p + 2 + d0), o23 = *(const float2*)(p + 4 + d0);
+                const float2 o45 = *(const float2*)(p + 6 + d0), o67 = *(const float2*)(p + 8 + d0);
+                ov[b][0] = o01.x, ov[b][1] = o01.y, ov[b][2] = o23.x, ov[b][3] = o23.y;
+                ov[b][4] = o45.x, ov[b][5] = o45.y, ov[b][6] = o67.x, ov[b][7] = o67.y;
+            }
+#pragma unroll
+            for (int b = 0; b < SB; b++) {
+                const bool ok = s0 + 4 * b < ns;
+                const float nM = fmaxf(M, st[b].x);
+                const float fo = M == -INFINITY ? 0.0f : dev_exp(M - nM);
+                const float w = st[b].x == -INFINITY ? 0.0f : dev_exp(st[b].x - nM);
+                const float nL = fmaf(st[b].y, w, L * fo);
+#pragma unroll
+                for (int e = 0; e < 8; e++) O[e] = ok ? fmaf(ov[b][e], w, O[e] * fo) : O[e];
+                L = ok ? nL : L;
+                M = ok ? nM : M;
+            }
         }
         // the four lanes of the pair, in a fixed order
         float MA = fmaxf(M, __shfl_xor(M, 1));
