@@ -494,10 +494,14 @@ struct Work {
 
 static int kind_of(const DMat& m) { return m.kind; }
 
-// n-tiles per workgroup of a projection with fewer than 256 tiles: one, so that
-// it spreads over twice the CUs (a CU streams only about 22 GB/s), unless it
-// finishes int8 pieces, whose per-block scale needs a whole 32-column k-block.
-static int narrow_nt(const DMat& w, bool int8_pieces) { return w.n_tiles < 256 && !int8_pieces ? 1 : 2; }
+// n-tiles per workgroup of a bf16 projection with fewer than 256 tiles: one, so
+// that it spreads over twice the CUs (a CU streams only about 22 GB/s), unless
+// it finishes int8 pieces, whose per-block scale needs a whole 32-column
+// k-block. Quantized projections keep two (their 16-wave two-tile variant
+// streams faster per CU).
+static int narrow_nt(const DMat& w, bool int8_pieces) {
+    return w.kind == BF16 && w.n_tiles < 256 && !int8_pieces ? 1 : 2;
+}
 static int qkv_dim(const fg_config& c) { return (c.heads + 2 * c.kv_heads) * c.head_dim; }
 
 static size_t layout_work(const fg_model* m, const Plan& P, Work& w, void* base) {

@@ -24,6 +24,7 @@
 #include <math.h>
 
 #include <algorithm>
+#include <type_traits>
 
 namespace fg {
 
@@ -357,50 +358,54 @@ __global__ __launch_bounds__(64 * WMAX) void k_gemv(const GemvArgs a) {
     const i32x4 izero = {0, 0, 0, 0};
     const float inv128 = 0.0078125f;
 
-    for (int c = c0; c < c1; c += U) {
-        long aq[U][4][PG];
-        bf16x8 ab[U][4][PG];
-        float sx[U][4][PG];
-        u32x4 wq[U][NT][2];
-        bf16x8 wb[U][NT][4];
-        float4 sv[U][NT];
+    // The main loop: batches of UU chunks whose loads are all issued before
+    // the first MFMA. Every load is unconditional (full batches, then single
+    // chunks; passes past np re-read the last one and are masked out), so no
+    // register carries a possibly pending load across iterations and nothing
+    // waits before the first weights are requested.
+    auto chunks = [&](int c, auto uu) {
+        constexpr int UU = decltype(uu)::value;
+        long aq[UU][4][PG];
+        bf16x8 ab[UU][4][PG];
+        float sx[UU][4][PG];
+        u32x4 wq[UU][NT][2];
+        bf16x8 wb[UU][NT][4];
+        float4 sv[UU][NT];
 #pragma unroll
-        for (int u = 0; u < U; u++) {
-            const int cc = c + u;
-            if (cc < c1) {
-                const int kb = cc * 4;
+        for (int u = 0; u < UU; u++) {
+            const int cc = c + u, kb = cc * 4;
 #pragma unroll
-                for (int j = 0; j < 4; j++)
+            for (int j = 0; j < 4; j++)
 #pragma unroll
-                    for (int p = 0; p < PG; p++)
-                        if (p < np) {
-                            const size_t idx = ((size_t)(kb + j) * a.p_total + pass0 + p) * 64 + lane;
-                            if (Q) {
-                                aq[u][j][p] = ((const long*)a.XA)[idx];
-                                sx[u][j][p] = a.XS[(size_t)(kb + j) * a.p_total * 4 + (pass0 + p) * 4 + (lane >> 4)];
-                            } else {
-                                ab[u][j][p] = ((const bf16x8*)a.XA)[idx];
-                            }
-                        }
-#pragma unroll
-                for (int t = 0; t < NT; t++) {
-                    const size_t tile = tile0 + t;
-                    if (KIND == INT4) {
-                        wq[u][t][0] = ((const u32x4*)a.W)[(tile * KC + cc) * 64 + lane];
-                    } else if (KIND == INT8) {
-                        wq[u][t][0] = ((const u32x4*)a.W)[(tile * (KB >> 1) + 2 * cc) * 64 + lane];
-                        wq[u][t][1] = ((const u32x4*)a.W)[(tile * (KB >> 1) + 2 * cc + 1) * 64 + lane];
+                for (int p = 0; p < PG; p++) {
+                    const int pp = pass0 + (PG == 1 ? 0 : min(p, np - 1));
+                    const size_t idx = ((size_t)(kb + j) * a.p_total + pp) * 64 + lane;
+                    if (Q) {
+                        aq[u][j][p] = ((const long*)a.XA)[idx];
+                        sx[u][j][p] = a.XS[(size_t)(kb + j) * a.p_total * 4 + pp * 4 + (lane >> 4)];
                     } else {
-#pragma unroll
-                        for (int j = 0; j < 4; j++) wb[u][t][j] = ((const bf16x8*)a.W)[(tile * KB + kb + j) * 64 + lane];
+                        ab[u][j][p] = ((const bf16x8*)a.XA)[idx];
                     }
-                    if (Q) sv[u][t] = ((const float4*)a.S)[(tile * KC + cc) * 16 + (lane & 15)];
                 }
+#pragma unroll
+            for (int t = 0; t < NT; t++) {
+                const size_t tile = tile0 + t;
+                if (KIND == INT4) {
+                    wq[u][t][0] = ((const u32x4*)a.W)[(tile * KC + cc) * 64 + lane];
+                } else if (KIND == INT8) {
+                    wq[u][t][0] = ((const u32x4*)a.W)[(tile * (KB >> 1) + 2 * cc) * 64 + lane];
+                    wq[u][t][1] = ((const u32x4*)a.W)[(tile * (KB >> 1) + 2 * cc + 1) * 64 + lane];
+                } else {
+#pragma unroll
+                    for (int j = 0; j < 4; j++) wb[u][t][j] = ((const bf16x8*)a.W)[(tile * KB + kb + j) * 64 + lane];
+                }
+                if (Q) sv[u][t] = ((const float4*)a.S)[(tile * KC + cc) * 16 + (lane & 15)];
             }
         }
+        // keep the scheduler from sinking loads of the batch below its first MFMA
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int u = 0; u < U; u++) {
-            if (c + u >= c1) break;
+        for (int u = 0; u < UU; u++) {
 #pragma unroll
             for (int t = 0; t < NT; t++) {
                 if (Q) {
@@ -441,7 +446,11 @@ __global__ __launch_bounds__(64 * WMAX) void k_gemv(const GemvArgs a) {
                 }
             }
         }
-    }
+    };
+    int c = c0;
+    for (; c + U <= c1; c += U) chunks(c, std::integral_constant<int, U>{});
+    if constexpr (U > 1)
+        for (; c < c1; c++) chunks(c, std::integral_constant<int, 1>{});
 
     // Park the prologue's values in LDS. Their loads completed with the main
     // loop's; reading them back from LDS later keeps the epilogue from waiting
