@@ -696,6 +696,33 @@ void launch_gemv(hipStream_t st, int epi, const DMat& w, const GemvArgs& a, hipE
         gemv_kind<BF16>(st, epi, w, a, start, stop);
 }
 
+// Max / sum over aligned groups of N lanes (N = 16, 32 or 64), every lane of
+// a group getting the same bits: DPP quad swaps and mirrors within rows of 16,
+// then the gfx950 row swaps (each step combines the same two operands, in the
+// same order, in both lanes of a pair).
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
+}
+template <int N, bool MAX>
+__device__ __forceinline__ float group_reduce(float v) {
+    static_assert(N == 16 || N == 32 || N == 64, "16, 32 or 64 lanes");
+    auto op = [](float x, float y) { return MAX ? fmaxf(x, y) : x + y; };
+    v = op(v, dpp_f<0xB1>(v));   // quad_perm [1,0,3,2]
+    v = op(v, dpp_f<0x4E>(v));   // quad_perm [2,3,0,1]
+    v = op(v, dpp_f<0x141>(v));  // row_half_mirror
+    v = op(v, dpp_f<0x140>(v));  // row_mirror
+    if (N >= 32) {
+        const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+        v = op(__uint_as_float(r[0]), __uint_as_float(r[1]));
+    }
+    if (N >= 64) {
+        const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+        v = op(__uint_as_float(r[0]), __uint_as_float(r[1]));
+    }
+    return v;
+}
+
 // ---------------------------------------------------------------------------
 // Paged attention, split over the context (flash-decoding). A work item is
 // (row group, span of P positions) x kv head: the rows of a group are
@@ -711,13 +738,13 @@ void launch_gemv(hipStream_t st, int epi, const DMat& w, const GemvArgs& a, hipE
 template <int HD, int P, int QM>
 __global__ __launch_bounds__(256) void k_attn(AttnArgs a) {
     constexpr int HALF = HD / 2;
-    __shared__ float ks[P][HD + 1];
-    __shared__ float vs[P][HD];
-    __shared__ float qs[QM][HD];
-    __shared__ float pr[QM][P];
+    __shared__ __align__(16) float ks[P][HD + 4];  // rows 16-byte aligned; lanes' 16-byte reads hit distinct banks
+    __shared__ __align__(16) float vs[P][HD];
+    __shared__ __align__(16) float qs[QM][HD];
+    __shared__ __align__(16) float pr[QM][P];
     __shared__ int lim[QM];
 
-    static_assert(P <= 64 && P % 16 == 0, "a span covers at most four cache blocks");
+    static_assert(P <= 64 && P % 16 == 0 && 64 % P == 0, "a span covers at most four cache blocks");
     // grid (kv head, work item): every real item is dispatched before the
     // launch's unused capacity slots, which exit at once
     const int h = blockIdx.x, wi = blockIdx.y;
@@ -824,41 +851,52 @@ __global__ __launch_bounds__(256) void k_attn(AttnArgs a) {
             a.vc[at] = vs[o][d];
         }
     }
-    // scores
-    for (int i = tid; i < Q * P; i += 256) {
-        const int q = i / P, o = i % P, p = p0 + o;
+    // Scores and their softmax statistics in one pass: item i = q * P + o, so
+    // each wave holds whole queries (one per P lanes) and reduces them in
+    // registers.
+    for (int base = wave * 64; base < Q * P; base += 256) {
+        const int i = base + lane, q = i / P, o = i % P, p = p0 + o;
         float sc = -INFINITY;
-        if (p < p1 && p <= lim[q]) {
+        if (q < Q && p < p1 && p <= lim[q]) {
+            const float4* kr = (const float4*)&ks[o][0];
+            const float4* qr = (const float4*)&qs[q][0];
             float acc = 0.0f;
-#pragma unroll 16
-            for (int e = 0; e < HD; e++) acc = fmaf(qs[q][e], ks[o][e], acc);
+#pragma unroll
+            for (int e4 = 0; e4 < HD / 4; e4++) {
+                const float4 kv = kr[e4], qv = qr[e4];
+                acc = fmaf(qv.x, kv.x, acc);
+                acc = fmaf(qv.y, kv.y, acc);
+                acc = fmaf(qv.z, kv.z, acc);
+                acc = fmaf(qv.w, kv.w, acc);
+            }
             sc = acc * a.scale;
         }
-        pr[q][o] = sc;
-    }
-    __syncthreads();
-    // softmax statistics of each query over the span (one wave per query)
-    for (int q = wave; q < Q; q += 4) {
-        const float sc = lane < P ? pr[q][lane] : -INFINITY;
-        float mx = sc;
-        for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+        const float mx = group_reduce<P, true>(sc);
         const float e = (sc == -INFINITY) ? 0.0f : dev_exp(sc - mx);
-        float sum = e;
-        for (int o = 32; o > 0; o >>= 1) sum += __shfl_xor(sum, o);
-        if (lane < P) pr[q][lane] = e;
-        if (lane == 0) {
-            float* dst = a.part + (((size_t)wi * a.nkv + h) * QM + q) * (HD + 2);
-            dst[0] = mx;
-            dst[1] = sum;
+        const float sum = group_reduce<P, false>(e);
+        if (q < Q) {
+            pr[q][o] = e;
+            if (o == 0) {
+                float* dst = a.part + (((size_t)wi * a.nkv + h) * QM + q) * (HD + 2);
+                dst[0] = mx;
+                dst[1] = sum;
+            }
         }
     }
     __syncthreads();
     // weighted values
     for (int i = tid; i < Q * HD; i += 256) {
         const int q = i / HD, d = i % HD;
+        const float4* prr = (const float4*)&pr[q][0];
         float acc = 0.0f;
-#pragma unroll 16
-        for (int o = 0; o < P; o++) acc = fmaf(pr[q][o], vs[o][d], acc);
+#pragma unroll
+        for (int o4 = 0; o4 < P / 4; o4++) {
+            const float4 w = prr[o4];
+            acc = fmaf(w.x, vs[4 * o4][d], acc);
+            acc = fmaf(w.y, vs[4 * o4 + 1][d], acc);
+            acc = fmaf(w.z, vs[4 * o4 + 2][d], acc);
+            acc = fmaf(w.w, vs[4 * o4 + 3][d], acc);
+        }
         a.part[(((size_t)wi * a.nkv + h) * QM + q) * (HD + 2) + 2 + d] = acc;
     }
 }
