@@ -67,6 +67,43 @@ __device__ __forceinline__ float dev_exp(float x) {
 // sum rounded values in a symmetric order (the library is built without
 // floating-point contraction, so a shuffle sum is never fused with a product).
 // ---------------------------------------------------------------------------
+// Cross-lane reductions without the LDS crossbar (ds_bpermute). Within rows
+// of 16 lanes: DPP quad swaps (partners l^1, l^2) and the row mirrors; across
+// rows: the gfx950 row swaps, whose two results hold the even and the odd
+// 16-lane rows (or 32-lane halves), so both lanes of a pair combine the same
+// operands in the same order and end with the same bits. Every lane of the
+// group must be active.
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
+}
+__device__ __forceinline__ float lane_xor1(float v) { return dpp_f<0xB1>(v); }  // quad_perm [1,0,3,2]
+__device__ __forceinline__ float lane_xor2(float v) { return dpp_f<0x4E>(v); }  // quad_perm [2,3,0,1]
+template <bool MAX>
+__device__ __forceinline__ float red_op(float x, float y) { return MAX ? fmaxf(x, y) : x + y; }
+// over lanes l, l^16 (and l^32 when WIDE)
+template <bool MAX, bool WIDE>
+__device__ __forceinline__ float reduce_rows(float v) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = red_op<MAX>(__uint_as_float(r[0]), __uint_as_float(r[1]));
+    if (WIDE) {
+        const auto h = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+        v = red_op<MAX>(__uint_as_float(h[0]), __uint_as_float(h[1]));
+    }
+    return v;
+}
+// Max / sum over aligned groups of N lanes (16, 32 or 64).
+template <int N, bool MAX>
+__device__ __forceinline__ float group_reduce(float v) {
+    static_assert(N == 16 || N == 32 || N == 64, "16, 32 or 64 lanes");
+    v = red_op<MAX>(v, lane_xor1(v));
+    v = red_op<MAX>(v, lane_xor2(v));
+    v = red_op<MAX>(v, dpp_f<0x141>(v));  // row_half_mirror: the other quad of the 8
+    v = red_op<MAX>(v, dpp_f<0x140>(v));  // row_mirror: the other 8 of the row
+    if (N >= 32) v = reduce_rows<MAX, N == 64>(v);
+    return v;
+}
+
 // bf16 piece `piece` of x: four successive bf16 roundings of the remainder
 // (all four are formed and one is selected, without branches).
 __device__ __forceinline__ uint32_t bf16_piece(float x, int piece) {
@@ -84,8 +121,7 @@ __device__ __forceinline__ uint32_t bf16_piece(float x, int piece) {
 // (l, l^16, l^32, l^48 hold its 32 inputs; mx is this lane's max |input|):
 // the block maximum / 2^e lies in [64, 128) and never rounds past 127.
 __device__ __forceinline__ int int8_block_exp(float mx) {
-    mx = fmaxf(mx, __shfl_xor(mx, 16));
-    mx = fmaxf(mx, __shfl_xor(mx, 32));
+    mx = reduce_rows<true, true>(mx);
     int e = 0;
     if (mx > 0.0f) {
         int fe;
@@ -226,8 +262,7 @@ __global__ __launch_bounds__(64) void k_embed(const uint32_t* __restrict__ tok, 
     float sq = 0.0f;
 #pragma unroll
     for (int s = 0; s < 8; s++) sq = fmaf(v[s], v[s], sq);
-    sq += __shfl_xor(sq, 16);
-    sq += __shfl_xor(sq, 32);
+    sq = reduce_rows<false, true>(sq);
     if (rv && piece == 0) {
 #pragma unroll
         for (int s = 0; s < 8; s++)
@@ -468,10 +503,7 @@ __global__ __launch_bounds__(64 * WMAX) void k_gemv(const GemvArgs a) {
         float v = 0.0f;
 #pragma unroll
         for (int i = 0; i < RL; i++) v += rv[i];
-        v += __shfl_xor(v, 8);
-        v += __shfl_xor(v, 4);
-        v += __shfl_xor(v, 2);
-        v += __shfl_xor(v, 1);
+        v = group_reduce<16, false>(v);
         if ((threadIdx.x & 15) == 0) rs[threadIdx.x >> 4] = 1.0f / sqrtf(v / (float)a.hidden + a.eps);
     }
     if (EPI == EPI_RESID || ((EPI == EPI_QKV || EPI == EPI_STORE) && a.bias)) {
@@ -581,10 +613,7 @@ __global__ __launch_bounds__(64 * WMAX) void k_gemv(const GemvArgs a) {
                 const float x0 = yt[r * YS + j];
                 ssq = x0 * x0;
             }
-            ssq += __shfl_xor(ssq, 8);
-            ssq += __shfl_xor(ssq, 4);
-            ssq += __shfl_xor(ssq, 2);
-            ssq += __shfl_xor(ssq, 1);
+            ssq = group_reduce<16, false>(ssq);
             if (j == 0 && row < a.m) a.ss_out[(size_t)blockIdx.x * a.ss_m + row] = ssq;
         }
     // the consumer's k-block and, for OC 16, which half of it (lanes 32h .. 32h+31)
@@ -694,33 +723,6 @@ void launch_gemv(hipStream_t st, int epi, const DMat& w, const GemvArgs& a, hipE
         gemv_kind<INT8>(st, epi, w, a, start, stop);
     else
         gemv_kind<BF16>(st, epi, w, a, start, stop);
-}
-
-// Max / sum over aligned groups of N lanes (N = 16, 32 or 64), every lane of
-// a group getting the same bits: DPP quad swaps and mirrors within rows of 16,
-// then the gfx950 row swaps (each step combines the same two operands, in the
-// same order, in both lanes of a pair).
-template <int CTRL>
-__device__ __forceinline__ float dpp_f(float v) {
-    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
-}
-template <int N, bool MAX>
-__device__ __forceinline__ float group_reduce(float v) {
-    static_assert(N == 16 || N == 32 || N == 64, "16, 32 or 64 lanes");
-    auto op = [](float x, float y) { return MAX ? fmaxf(x, y) : x + y; };
-    v = op(v, dpp_f<0xB1>(v));   // quad_perm [1,0,3,2]
-    v = op(v, dpp_f<0x4E>(v));   // quad_perm [2,3,0,1]
-    v = op(v, dpp_f<0x141>(v));  // row_half_mirror
-    v = op(v, dpp_f<0x140>(v));  // row_mirror
-    if (N >= 32) {
-        const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-        v = op(__uint_as_float(r[0]), __uint_as_float(r[1]));
-    }
-    if (N >= 64) {
-        const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-        v = op(__uint_as_float(r[0]), __uint_as_float(r[1]));
-    }
-    return v;
 }
 
 // ---------------------------------------------------------------------------
@@ -950,17 +952,17 @@ __global__ __launch_bounds__(64) void k_merge_pieces(AttnArgs a, int m, void* __
             }
         }
         // the four lanes of the pair, in a fixed order
-        float MA = fmaxf(M, __shfl_xor(M, 1));
-        MA = fmaxf(MA, __shfl_xor(MA, 2));
+        float MA = fmaxf(M, lane_xor1(M));
+        MA = fmaxf(MA, lane_xor2(MA));
         const float f = M == -INFINITY ? 0.0f : dev_exp(M - MA);
         L *= f;
-        L += __shfl_xor(L, 1);
-        L += __shfl_xor(L, 2);
+        L += lane_xor1(L);
+        L += lane_xor2(L);
 #pragma unroll
         for (int e = 0; e < 8; e++) {
             O[e] *= f;
-            O[e] += __shfl_xor(O[e], 1);
-            O[e] += __shfl_xor(O[e], 2);
+            O[e] += lane_xor1(O[e]);
+            O[e] += lane_xor2(O[e]);
             v[e] = O[e] / L;
         }
     }
