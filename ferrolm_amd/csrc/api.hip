@@ -485,6 +485,8 @@ static void pack_plan(const Plan& P, int32_t* h) {
 // Workspace of one forward pass over a plan.
 struct Work {
     float *x, *ss, *qkv, *apart, *logits;
+    float* kpart;  // GEMM split-K partial tiles (steps of more than kGemvRows rows)
+    size_t kpart_cap;
     void* pa[2];   // activation pieces, ping-pong: each kernel reads one and writes the other
     float* pxs[2];
     float2* best;
@@ -493,6 +495,10 @@ struct Work {
 };
 
 static int kind_of(const DMat& m) { return m.kind; }
+
+// Steps with more rows than this run their projections as GEMMs (k_gemm on
+// MM pieces); up to this many rows, as GEMVs on BF16/INT8 pieces.
+static constexpr int kGemvRows = 16;
 
 // n-tiles per workgroup of a bf16 projection with fewer than 256 tiles: one, so
 // that it spreads over twice the CUs (a CU streams only about 22 GB/s), unless
@@ -525,6 +531,9 @@ static size_t layout_work(const fg_model* m, const Plan& P, Work& w, void* base)
     w.logits = cv.take<float>((size_t)S * c.vocab);
     w.best = cv.take<float2>((size_t)(c.vocab / 32) * S);
     w.am = cv.take<uint32_t>(S);
+    // the split rule keeps splits x rows x N within 64 x 256 x 64 floats
+    w.kpart_cap = t > kGemvRows ? (size_t)1 << 20 : 0;
+    w.kpart = w.kpart_cap ? cv.take<float>(w.kpart_cap) : nullptr;
     return cv.off + 256;
 }
 
@@ -537,8 +546,10 @@ static Pieces pieces(const Work& w, int i, int kb, int passes) {
     return p;
 }
 
-static GemvArgs gemv_args(const DMat& d, const Pieces& in, int m) {
+static GemvArgs gemv_args(const DMat& d, const Pieces& in, int m, const Work& w) {
     GemvArgs a;
+    a.kpart = w.kpart;
+    a.kpart_cap = w.kpart_cap;
     a.W = (const uint8_t*)d.w;
     a.S = d.s;
     a.kind = d.kind;
@@ -566,11 +577,14 @@ static int run_forward(fg_ctx* ctx, const fg_model* m, fg_kv* kv, const Plan& P,
     if (t == 0) return 0;
     const int passes = w.passes;
     int cur = 0;  // pieces buffer the next GEMV reads
+    // more than 16 rows: every projection runs as a GEMM on MM pieces
+    const bool mm = t > kGemvRows;
+    auto ck = [&](const DMat& d) { return mm ? (int)MM : kind_of(d); };
 
     if (L > 0) {
         Pieces p0 = pieces(w, cur, m->layers[0].wqkv.kb, passes);
         launch_embed(st, tok_dev, tok_stride, m->embed, t, H, m->layers[0].attn_norm, w.x, w.ss,
-                     kind_of(m->layers[0].wqkv), p0);
+                     ck(m->layers[0].wqkv), p0);
     } else {
         Pieces p0 = pieces(w, cur, m->lm_head.kb, passes);
         launch_embed(st, tok_dev, tok_stride, m->embed, t, H, nullptr, w.x, w.ss, BF16, p0);
@@ -596,25 +610,26 @@ static int run_forward(fg_ctx* ctx, const fg_model* m, fg_kv* kv, const Plan& P,
     for (int li = 0; li < L; li++) {
         const DLayer& l = m->layers[li];
         // q/k/v of the normed rows: rinv from the sum-of-squares partials
-        GemvArgs g = gemv_args(l.wqkv, pieces(w, cur, l.wqkv.kb, passes), t);
+        GemvArgs g = gemv_args(l.wqkv, pieces(w, cur, l.wqkv.kb, passes), t, w);
         g.out = w.qkv;
         g.ldo = qkv_dim(c);
         g.bias = l.bqkv;
         g.ss_in = w.ss;
-        g.ss_tiles = H / ss_cols;
+        g.ss_tiles = (H + ss_cols - 1) / ss_cols;
         g.ss_m = t;
         g.hidden = H;
         g.eps = c.rms_eps;
         g.nt = narrow_nt(l.wqkv, false);
+        g.mm = mm;
         gemv(ctx, EPI_QKV, l.wqkv, g);
         // attention (RoPE, cache write) and the merge into wo's pieces
         aa.kc = kv->k + li * kv->layer_floats();
         aa.vc = kv->v + li * kv->layer_floats();
         Pieces po = pieces(w, cur ^ 1, l.wo.kb, passes);
-        launch_attention(st, aa, t, kind_of(l.wo), po);
+        launch_attention(st, aa, t, ck(l.wo), po);
         cur ^= 1;
         // o projection + residual; pieces of mlp_norm * x for gate/up
-        g = gemv_args(l.wo, pieces(w, cur, l.wo.kb, passes), t);
+        g = gemv_args(l.wo, pieces(w, cur, l.wo.kb, passes), t, w);
         g.x = w.x;
         g.ldx = H;
         g.ss_out = w.ss;
@@ -622,29 +637,32 @@ static int run_forward(fg_ctx* ctx, const fg_model* m, fg_kv* kv, const Plan& P,
         g.g_next = l.mlp_norm;
         g.pa = w.pa[cur ^ 1];
         g.pxs = w.pxs[cur ^ 1];
-        g.pa_kind = kind_of(l.w_gate_up);
+        g.pa_kind = ck(l.w_gate_up);
         g.pa_passes = passes;
         g.pa_kb = l.w_gate_up.kb;
-        g.nt = narrow_nt(l.wo, g.pa_kind != BF16);
-        ss_cols = 16 * g.nt;
+        g.nt = narrow_nt(l.wo, g.pa_kind == INT8 || g.pa_kind == INT4);
+        g.mm = mm;
+        ss_cols = mm ? 64 : 16 * g.nt;
         gemv(ctx, EPI_RESID, l.wo, g);
         cur ^= 1;
         // gate/up with SiLU; pieces of the activation for down
-        g = gemv_args(l.w_gate_up, pieces(w, cur, l.w_gate_up.kb, passes), t);
+        g = gemv_args(l.w_gate_up, pieces(w, cur, l.w_gate_up.kb, passes), t, w);
         g.ss_in = w.ss;
-        g.ss_tiles = H / ss_cols;
+        g.ss_tiles = (H + ss_cols - 1) / ss_cols;
         g.ss_m = t;
         g.hidden = H;
         g.eps = c.rms_eps;
         g.pa = w.pa[cur ^ 1];
         g.pxs = w.pxs[cur ^ 1];
-        g.pa_kind = kind_of(l.w_down);
+        g.pa_kind = ck(l.w_down);
         g.pa_passes = passes;
         g.pa_kb = l.w_down.kb;
+        g.il = l.w_gate_up.il;
+        g.mm = mm;
         gemv(ctx, EPI_SILU, l.w_gate_up, g);
         cur ^= 1;
         // down projection + residual; pieces of the next layer's attn_norm * x
-        g = gemv_args(l.w_down, pieces(w, cur, l.w_down.kb, passes), t);
+        g = gemv_args(l.w_down, pieces(w, cur, l.w_down.kb, passes), t, w);
         g.x = w.x;
         g.ldx = H;
         g.ss_out = w.ss;
@@ -654,12 +672,13 @@ static int run_forward(fg_ctx* ctx, const fg_model* m, fg_kv* kv, const Plan& P,
             g.g_next = nl.attn_norm;
             g.pa = w.pa[cur ^ 1];
             g.pxs = w.pxs[cur ^ 1];
-            g.pa_kind = kind_of(nl.wqkv);
+            g.pa_kind = ck(nl.wqkv);
             g.pa_passes = passes;
             g.pa_kb = nl.wqkv.kb;
         }
-        g.nt = narrow_nt(l.w_down, g.pa && g.pa_kind != BF16);
-        ss_cols = 16 * g.nt;
+        g.nt = narrow_nt(l.w_down, g.pa && (g.pa_kind == INT8 || g.pa_kind == INT4));
+        g.mm = mm;
+        ss_cols = mm ? 64 : 16 * g.nt;
         gemv(ctx, EPI_RESID, l.w_down, g);
         cur ^= 1;
         if (hidden_host)
@@ -671,10 +690,12 @@ static int run_forward(fg_ctx* ctx, const fg_model* m, fg_kv* kv, const Plan& P,
     // final norm of the selected rows (weight now, 1/rms in the epilogue), lm_head, argmax
     const int32_t* sel = meta + P.o_sel;
     Pieces pl = pieces(w, cur, m->lm_head.kb, w.lm_passes);
-    launch_pieces(st, kind_of(m->lm_head), w.x, H, P.S, H, m->norm, sel, pl);
-    GemvArgs g = gemv_args(m->lm_head, pl, P.S);
+    const bool lm_mm = P.S > kGemvRows;
+    launch_pieces(st, lm_mm ? (int)MM : kind_of(m->lm_head), w.x, H, P.S, H, m->norm, sel, pl);
+    GemvArgs g = gemv_args(m->lm_head, pl, P.S, w);
+    g.mm = lm_mm;
     g.ss_in = w.ss;
-    g.ss_tiles = H / ss_cols;
+    g.ss_tiles = (H + ss_cols - 1) / ss_cols;
     g.ss_m = t;
     g.hidden = H;
     g.eps = c.rms_eps;
@@ -1141,8 +1162,9 @@ void fg_mat_destroy(fg_mat* m) {
     delete m;
 }
 
-// Workspace for a lone product: pieces, staged x and y.
-static size_t layout_mat(const DMat& d, int m, Pieces& p, float** xbuf, float** ybuf, float** bbuf, void* base) {
+// Workspace for a lone product: pieces, staged x and y, GEMM split-K partials.
+static size_t layout_mat(const DMat& d, int m, Pieces& p, float** xbuf, float** ybuf, float** bbuf, Work& w,
+                         void* base) {
     Carver cv(base);
     p.kb = d.kb;
     p.passes = (m + 3) / 4;
@@ -1151,12 +1173,19 @@ static size_t layout_mat(const DMat& d, int m, Pieces& p, float** xbuf, float** 
     *xbuf = cv.take<float>((size_t)m * d.cols);
     *ybuf = cv.take<float>((size_t)m * d.rows);
     *bbuf = cv.take<float>((size_t)d.rows);
+    w.kpart_cap = m > kGemvRows ? (size_t)1 << 20 : 0;
+    w.kpart = w.kpart_cap ? cv.take<float>(w.kpart_cap) : nullptr;
     return cv.off + 256;
 }
 
-static void matmul_launch(fg_ctx* ctx, const DMat& d, Pieces& p, const float* x, int m, const float* bias, float* y) {
-    launch_pieces(ctx->stream, d.kind, x, d.cols, m, d.cols, nullptr, nullptr, p);
-    GemvArgs g = gemv_args(d, p, m);
+// y = x W^T (+ bias): a GEMV on BF16/INT8 pieces up to kGemvRows rows, a GEMM
+// on MM pieces beyond, as in the forward pass.
+static void matmul_launch(fg_ctx* ctx, const DMat& d, Pieces& p, const Work& w, const float* x, int m,
+                          const float* bias, float* y) {
+    const bool mm = m > kGemvRows;
+    launch_pieces(ctx->stream, mm ? (int)MM : d.kind, x, d.cols, m, d.cols, nullptr, nullptr, p);
+    GemvArgs g = gemv_args(d, p, m, w);
+    g.mm = mm;
     g.out = y;
     g.ldo = d.rows;
     g.bias = bias;
@@ -1168,14 +1197,15 @@ int fg_matmul(fg_ctx* ctx, const fg_mat* w, const float* x, int32_t m, const flo
     HIPCHK(hipSetDevice(ctx->device));
     const DMat& d = w->m;
     Pieces p;
+    Work wk{};
     float *xb, *yb, *bb;
     int rc;
-    if ((rc = ensure(&ctx->ws, &ctx->ws_cap, layout_mat(d, m, p, &xb, &yb, &bb, nullptr), ctx->stream, false)))
+    if ((rc = ensure(&ctx->ws, &ctx->ws_cap, layout_mat(d, m, p, &xb, &yb, &bb, wk, nullptr), ctx->stream, false)))
         return rc;
-    layout_mat(d, m, p, &xb, &yb, &bb, ctx->ws);
+    layout_mat(d, m, p, &xb, &yb, &bb, wk, ctx->ws);
     if (bias) HIPCHK(hipMemcpyAsync(bb, bias, (size_t)d.rows * 4, hipMemcpyHostToDevice, ctx->stream));
     HIPCHK(hipMemcpyAsync(xb, x, (size_t)m * d.cols * 4, hipMemcpyHostToDevice, ctx->stream));
-    matmul_launch(ctx, d, p, xb, m, bias ? bb : nullptr, yb);
+    matmul_launch(ctx, d, p, wk, xb, m, bias ? bb : nullptr, yb);
     HIPCHK(hipGetLastError());
     HIPCHK(hipMemcpyAsync(y, yb, (size_t)m * d.rows * 4, hipMemcpyDeviceToHost, ctx->stream));
     HIPCHK(hipStreamSynchronize(ctx->stream));
@@ -1186,12 +1216,13 @@ int fg_matmul_device(fg_ctx* ctx, const fg_mat* w, const float* x_dev, int32_t m
     if (!ctx || !w || !x_dev || !y_dev || m <= 0) return fail(FG_E_ARG, "bad argument");
     const DMat& d = w->m;
     Pieces p;
+    Work wk{};
     float *xb, *yb, *bb;
     int rc;
-    if ((rc = ensure(&ctx->ws, &ctx->ws_cap, layout_mat(d, m, p, &xb, &yb, &bb, nullptr), ctx->stream, false)))
+    if ((rc = ensure(&ctx->ws, &ctx->ws_cap, layout_mat(d, m, p, &xb, &yb, &bb, wk, nullptr), ctx->stream, false)))
         return rc;
-    layout_mat(d, m, p, &xb, &yb, &bb, ctx->ws);
-    matmul_launch(ctx, d, p, x_dev, m, nullptr, y_dev);
+    layout_mat(d, m, p, &xb, &yb, &bb, wk, ctx->ws);
+    matmul_launch(ctx, d, p, wk, x_dev, m, nullptr, y_dev);
     HIPCHK(hipGetLastError());
     return 0;
 }

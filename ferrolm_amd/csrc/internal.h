@@ -34,6 +34,9 @@ namespace fg {
 // spans a whole k-block) and 16 for bf16 pieces.
 // ---------------------------------------------------------------------------
 enum { BF16 = 0, INT8 = 1, INT4 = 2 };
+// Activation operand formats ("pieces", below): BF16 and INT8 for the GEMV
+// consumers, MM for the GEMM consumers (more than 16 rows).
+enum { MM = 3 };
 
 struct DMat {
     int kind = 0;
@@ -56,6 +59,12 @@ struct DMat {
 //     [kb][pass*4 + row-in-pass] f32.
 //   BF16 consumers: x = p0 + p1 + p2 + p3 with each piece a bf16, exact to
 //     f32. Layout [kb][pass][lane][8 x bf16].
+//   MM (GEMM) consumers: x = hi + lo, two bf16 pieces (16 significant bits),
+//     in the MFMA A-operand layout of 16 distinct rows: [kb][rt][h][lane]
+//     [8 x bf16] for row tile rt = row / 16 (ceil(passes / 4) of them), h = 0
+//     hi / 1 lo; lane l holds row 16 rt + l % 16, inputs 8 (l / 16) .. +7.
+//     Rows past the last pass are never written (a GEMM output row depends on
+//     its own input row only, and rows >= m are discarded).
 struct Pieces {
     void* a = nullptr;
     float* xs = nullptr;
@@ -79,6 +88,12 @@ struct GemvArgs {
     const float* XS = nullptr;
     int m = 0, p_total = 0;
     int nt = 2;  // n-tiles per workgroup for STORE/QKV/RESID (1 or 2; SILU takes 2*il/16)
+    int il = 0;  // gate/up interleave block of the weights (EPI_SILU)
+    bool mm = false;  // inputs in the MM format: the GEMM path (64 x 64 tiles)
+    // GEMM split K: partial tiles [split][m][N] (kpart_cap floats available, nullptr: no split)
+    float* kpart = nullptr;
+    size_t kpart_cap = 0;
+    int ks = 1;
     // STORE / QKV
     float* out = nullptr;
     int ldo = 0;

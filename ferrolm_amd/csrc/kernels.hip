@@ -92,14 +92,14 @@ __device__ __forceinline__ float reduce_rows(float v) {
     }
     return v;
 }
-// Max / sum over aligned groups of N lanes (16, 32 or 64).
+// Max / sum over aligned groups of N lanes (4, 8, 16, 32 or 64).
 template <int N, bool MAX>
 __device__ __forceinline__ float group_reduce(float v) {
-    static_assert(N == 16 || N == 32 || N == 64, "16, 32 or 64 lanes");
+    static_assert(N == 4 || N == 8 || N == 16 || N == 32 || N == 64, "4, 8, 16, 32 or 64 lanes");
     v = red_op<MAX>(v, lane_xor1(v));
     v = red_op<MAX>(v, lane_xor2(v));
-    v = red_op<MAX>(v, dpp_f<0x141>(v));  // row_half_mirror: the other quad of the 8
-    v = red_op<MAX>(v, dpp_f<0x140>(v));  // row_mirror: the other 8 of the row
+    if (N >= 8) v = red_op<MAX>(v, dpp_f<0x141>(v));  // row_half_mirror: the other quad of the 8
+    if (N >= 16) v = red_op<MAX>(v, dpp_f<0x140>(v));  // row_mirror: the other 8 of the row
     if (N >= 32) v = reduce_rows<MAX, N == 64>(v);
     return v;
 }
@@ -148,6 +148,18 @@ __device__ __forceinline__ int int8_piece(float x, int e, int piece) {
 template <int CK>
 __device__ __forceinline__ void write_pieces(const float (&v)[8], int kb, int pass, int passes, int row, int piece,
                                              int lane, void* out, float* xs) {
+    if (CK == MM) {
+        // pieces 0 and 1 of the row's 8 inputs, at its A-operand slot
+        if (piece < 2) {
+            const size_t at = ((((size_t)kb * ((passes + 3) >> 2) + (row >> 4)) * 2 + piece) * 64) +
+                              (lane >> 4) * 16 + (row & 15);
+            u16x8 o;
+#pragma unroll
+            for (int s = 0; s < 8; s++) o[s] = (uint16_t)bf16_piece(v[s], piece);
+            ((u16x8*)out)[at] = o;
+        }
+        return;
+    }
     const size_t slot = ((size_t)kb * passes + pass) * 64 + lane;
     if (CK == BF16) {
         u16x8 o;
@@ -175,6 +187,14 @@ __device__ __forceinline__ void write_pieces(const float (&v)[8], int kb, int pa
 template <int CK>
 __device__ __forceinline__ void write_pieces_pair(float x0, float x1, float mx, int pair, int kb, int pass,
                                                   int passes, int row, int piece, int lane, void* out, float* xs) {
+    if (CK == MM) {
+        if (piece < 2) {
+            const size_t at = ((((size_t)kb * ((passes + 3) >> 2) + (row >> 4)) * 2 + piece) * 64) +
+                              (lane >> 4) * 16 + (row & 15);
+            ((uint32_t*)out)[at * 4 + pair] = bf16_piece(x0, piece) | (bf16_piece(x1, piece) << 16);
+        }
+        return;
+    }
     const size_t slot = ((size_t)kb * passes + pass) * 64 + lane;
     if (CK == BF16) {
         ((uint32_t*)out)[slot * 4 + pair] = bf16_piece(x0, piece) | (bf16_piece(x1, piece) << 16);
@@ -190,6 +210,8 @@ __device__ __forceinline__ void write_pieces_kind(int kind, const float (&v)[8],
                                                   int row, int piece, int lane, void* out, float* xs) {
     if (kind == BF16)
         write_pieces<BF16>(v, kb, pass, passes, row, piece, lane, out, xs);
+    else if (kind == MM)
+        write_pieces<MM>(v, kb, pass, passes, row, piece, lane, out, xs);
     else
         write_pieces<INT8>(v, kb, pass, passes, row, piece, lane, out, xs);
 }
@@ -199,6 +221,8 @@ __device__ __forceinline__ void write_pieces_pair_kind(int kind, float x0, float
                                                        float* xs) {
     if (kind == BF16)
         write_pieces_pair<BF16>(x0, x1, mx, pair, kb, pass, passes, row, piece, lane, out, xs);
+    else if (kind == MM)
+        write_pieces_pair<MM>(x0, x1, mx, pair, kb, pass, passes, row, piece, lane, out, xs);
     else
         write_pieces_pair<INT8>(x0, x1, mx, pair, kb, pass, passes, row, piece, lane, out, xs);
 }
@@ -234,6 +258,9 @@ void launch_pieces(hipStream_t st, int consumer_kind, const float* x, int ldx, i
     dim3 grid(out.kb, out.passes);
     if (consumer_kind == BF16)
         hipLaunchKernelGGL(k_pieces<BF16>, grid, dim3(64), 0, st, x, ldx, m, K, g, rows_src, out.a, out.xs,
+                           out.passes);
+    else if (consumer_kind == MM)
+        hipLaunchKernelGGL(k_pieces<MM>, grid, dim3(64), 0, st, x, ldx, m, K, g, rows_src, out.a, out.xs,
                            out.passes);
     else
         hipLaunchKernelGGL(k_pieces<INT8>, grid, dim3(64), 0, st, x, ldx, m, K, g, rows_src, out.a, out.xs,
@@ -281,6 +308,9 @@ void launch_embed(hipStream_t st, const uint32_t* tokens, int stride, const uint
     dim3 grid(out.kb, out.passes);
     if (consumer_kind == BF16)
         hipLaunchKernelGGL(k_embed<BF16>, grid, dim3(64), 0, st, tokens, stride, embed, m, H, g, x, ss, out.a,
+                           out.xs, out.passes);
+    else if (consumer_kind == MM)
+        hipLaunchKernelGGL(k_embed<MM>, grid, dim3(64), 0, st, tokens, stride, embed, m, H, g, x, ss, out.a,
                            out.xs, out.passes);
     else
         hipLaunchKernelGGL(k_embed<INT8>, grid, dim3(64), 0, st, tokens, stride, embed, m, H, g, x, ss, out.a,
@@ -626,9 +656,13 @@ __global__ __launch_bounds__(64 * WMAX) void k_gemv(const GemvArgs a) {
             const float* vr = &vt[r * YS + (OC == 16 ? q & 1 : q) * 8];
             const float4 v0 = *(const float4*)vr, v1 = *(const float4*)(vr + 4);
             const float2 xp = *(const float2*)(vr + 2 * pair);
-            if (OC == 16) {
-                write_pieces_pair<BF16>(xp.x, xp.y, 0.0f, pair, pkb, pass0 + p, a.pa_passes, pass0 * 4 + r, c & 3,
-                                        lane, a.pa, a.pxs);
+            if (OC == 16) {  // bf16 or MM pieces: no block scale
+                if (a.pa_kind == MM)
+                    write_pieces_pair<MM>(xp.x, xp.y, 0.0f, pair, pkb, pass0 + p, a.pa_passes, pass0 * 4 + r,
+                                          c & 3, lane, a.pa, a.pxs);
+                else
+                    write_pieces_pair<BF16>(xp.x, xp.y, 0.0f, pair, pkb, pass0 + p, a.pa_passes, pass0 * 4 + r,
+                                            c & 3, lane, a.pa, a.pxs);
             } else {
                 const float mx = fmaxf(fmaxf(fmaxf(fabsf(v0.x), fabsf(v0.y)), fmaxf(fabsf(v0.z), fabsf(v0.w))),
                                        fmaxf(fmaxf(fabsf(v1.x), fabsf(v1.y)), fmaxf(fabsf(v1.z), fabsf(v1.w))));
@@ -655,6 +689,393 @@ static void launch_timed(K kernel, dim3 grid, dim3 block, hipStream_t st, const 
         hipExtLaunchKernelGGL(kernel, grid, block, 0, st, e0, e1, 0, a);
     else
         hipLaunchKernelGGL(kernel, grid, block, 0, st, a);
+}
+
+// ---------------------------------------------------------------------------
+// GEMM for more than 16 activation rows (batched verify, prefill chunks):
+// bf16 MFMA (v_mfma_f32_16x16x32_bf16) on activations in the MM format (x =
+// hi + lo, two bf16 pieces: 16 significant bits) and on weights converted to
+// bf16 exactly (int8 codes, int4 codes x 16, bf16 as stored); the group
+// scale is applied once per k-block after the hi and lo products, as the
+// reference applies it to each group's dot product (src/quant.rs:331-374).
+// A workgroup owns a 64-row x 64-column output tile; its eight waves are two
+// halves of K x four 32 x 32 sub-tiles (2 row tiles x 2 n-tiles each), whose
+// operands each wave loads straight into registers (the other waves' copies
+// hit in L1); a chunk's loads are all issued before its first MFMA. The two
+// K halves meet in LDS, then the same epilogues as the GEMV run on the tile.
+// ---------------------------------------------------------------------------
+
+// bytes b, b+1 of w (two's-complement int8) as two bf16, exactly
+__device__ __forceinline__ uint32_t bf16x2_i8(uint32_t w, int b) {
+    const float f0 = (float)(int8_t)(w >> (8 * b)), f1 = (float)(int8_t)(w >> (8 * b + 8));
+    return (__float_as_uint(f0) >> 16) | (__float_as_uint(f1) & 0xFFFF0000u);
+}
+
+// The GEMM epilogues on the finished 64 x 64 tile yt (rows [row0, row0 + rows),
+// columns from col0): 1/rms from the producers' sums of squares, then the
+// GEMV's epilogues (internal.h) with the next operand in the MM format.
+template <int EPI, int NTHR>
+__device__ void gemm_epilogue(const GemvArgs& a, float* yt, float* part, float* rs, int row0, int rows, int col0) {
+    constexpr bool NEED_R = EPI == EPI_QKV || EPI == EPI_SILU || EPI == EPI_ARGMAX;
+    constexpr int YS = 68;
+    const int tid = threadIdx.x;
+    __syncthreads();
+    // 1/rms of each row from the producers' sums of squares: four lanes per row
+    if (NEED_R && tid < 256) {
+        const int rr = tid >> 2, q4 = tid & 3, row = row0 + rr;
+        float v = 0.0f;
+        if (rr < rows) {
+            const int src = a.rows_src ? a.rows_src[row] : row;
+            for (int t = q4; t < a.ss_tiles; t += 4) v += a.ss_in[(size_t)t * a.ss_m + src];
+        }
+        v = group_reduce<4, false>(v);
+        if (q4 == 0) rs[rr] = 1.0f / sqrtf(v / (float)a.hidden + a.eps);
+    }
+    __syncthreads();
+
+    if (EPI == EPI_STORE || EPI == EPI_QKV) {
+        for (int idx = tid; idx < 64 * 64; idx += NTHR) {
+            const int rr = idx >> 6, cc = idx & 63, row = row0 + rr, col = col0 + cc;
+            if (rr < rows && col < a.N) {
+                float v = yt[rr * YS + cc];
+                if (EPI == EPI_QKV) v *= rs[rr];
+                if (a.bias) v += a.bias[col];
+                a.out[(size_t)row * a.ldo + col] = v;
+            }
+        }
+        return;
+    }
+    if (EPI == EPI_ARGMAX) {
+        for (int idx = tid; idx < 64 * 64; idx += NTHR) {
+            const int rr = idx >> 6, cc = idx & 63, row = row0 + rr, col = col0 + cc;
+            const float v = yt[rr * YS + cc] * rs[rr];
+            if (rr < rows && col < a.N && a.logits) a.logits[(size_t)row * a.N + col] = v;
+            yt[rr * YS + cc] = v != v ? -INFINITY : v;
+        }
+        __syncthreads();
+        // (max, first index) of each row in each 32-column tile
+        if (tid < 128) {
+            const int rr = tid >> 1, j = tid & 1, row = row0 + rr;
+            if (rr < rows && col0 + j * 32 < a.N) {
+                const float* yr = &yt[rr * YS + j * 32];
+                float bv = yr[0];
+                int bi = 0;
+                for (int cc = 1; cc < 32; cc++)
+                    if (yr[cc] > bv) {
+                        bv = yr[cc];
+                        bi = cc;
+                    }
+                a.best[((size_t)blockIdx.x * 2 + j) * a.m + row] = make_float2(bv, __int_as_float(col0 + j * 32 + bi));
+            }
+        }
+        return;
+    }
+    // EPI_RESID / EPI_SILU: the finished values of the group's output columns
+    // (64 for RESID, the 32 channels of SILU) go to LDS, then out as the next
+    // GEMM's MM pieces (two bf16 pieces per value) in 16-byte slots.
+    constexpr int OC = EPI == EPI_RESID ? 64 : 32;
+    float* vt = part;  // free again after the tree
+    for (int idx = tid; idx < 64 * OC; idx += NTHR) {
+        const int rr = idx / OC, cc = idx % OC, row = row0 + rr;
+        const bool live = rr < rows && (EPI == EPI_SILU || col0 + cc < a.N);
+        if (EPI == EPI_RESID) {
+            const size_t at = (size_t)row * a.ldx + col0 + cc;
+            const float xn = live ? a.x[at] + yt[rr * YS + cc] : 0.0f;
+            if (live) a.x[at] = xn;
+            yt[rr * YS + cc] = xn;
+            vt[rr * YS + cc] = live && a.g_next ? a.g_next[col0 + cc] * xn : xn;
+        } else {
+            // channel cc: block b of the [gate il, up il] interleave, position j in it
+            const int b = cc / a.il, j = cc % a.il;
+            const float gt = yt[rr * YS + b * 2 * a.il + j] * rs[rr], up = yt[rr * YS + b * 2 * a.il + a.il + j] * rs[rr];
+            vt[rr * YS + cc] = live ? gt / (1.0f + dev_exp(-gt)) * up : 0.0f;
+        }
+    }
+    __syncthreads();
+    if (EPI == EPI_RESID && tid < 256) {
+        // each row's sum of squares over the group's columns: four lanes per row
+        const int rr = tid >> 2, q4 = tid & 3, row = row0 + rr;
+        float ssq = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 16; e++) {
+            const float x = yt[rr * YS + q4 * 16 + e];
+            ssq = fmaf(x, x, ssq);
+        }
+        ssq = group_reduce<4, false>(ssq);
+        if (q4 == 0 && rr < rows) a.ss_out[(size_t)blockIdx.x * a.ss_m + row] = ssq;
+    }
+    if (a.pa) {
+        // slot (k-block, row tile, piece h, lane q8 * 16 + row % 16) holds 8 values
+        const int prt = (a.pa_passes + 3) >> 2, kb0 = col0 / 32;
+        constexpr int Q8 = OC / 8;
+        for (int idx = tid; idx < 64 * Q8 * 2; idx += NTHR) {
+            const int h = idx & 1, q8 = (idx >> 1) % Q8, rr = (idx >> 1) / Q8, row = row0 + rr;
+            if (rr >= rows) continue;
+            const int kb = (EPI == EPI_RESID ? kb0 : (int)blockIdx.x) + q8 / 4;
+            const float* vr = &vt[rr * YS + q8 * 8];
+            u16x8 o;
+#pragma unroll
+            for (int e = 0; e < 8; e++) o[e] = (uint16_t)bf16_piece(vr[e], h);
+            ((u16x8*)a.pa)[(((size_t)kb * prt + (row >> 4)) * 2 + h) * 64 + (q8 & 3) * 16 + (row & 15)] = o;
+        }
+        // the consumer's zero padding past the last k-block
+        if (blockIdx.x == gridDim.x - 1) {
+            const int covered = EPI == EPI_RESID ? (a.N + 31) / 32 : (int)gridDim.x;
+            const u16x8 z = {0, 0, 0, 0, 0, 0, 0, 0};
+            for (int idx = tid; idx < (a.pa_kb - covered) * 64 * 8; idx += NTHR) {
+                const int kb = covered + idx / 512, rem = idx % 512, h = rem & 1, q8 = (rem >> 1) & 3,
+                          rr = rem >> 3, row = row0 + rr;
+                if (rr < rows)
+                    ((u16x8*)a.pa)[(((size_t)kb * prt + (row >> 4)) * 2 + h) * 64 + q8 * 16 + (row & 15)] = z;
+            }
+        }
+    }
+}
+
+template <int KIND, int EPI, int RTW>
+__global__ __launch_bounds__(512) void k_gemm(const GemvArgs a) {
+    constexpr int NW = 8, NTHR = 64 * NW;
+    constexpr bool Q = KIND != BF16;
+    constexpr bool NEED_R = EPI == EPI_QKV || EPI == EPI_SILU || EPI == EPI_ARGMAX;
+    constexpr int YS = 68;  // LDS row stride of the 64 x 64 tile
+    // the cross-wave tree: four partial tiles (the lanes' layout), then the tile
+    __shared__ __align__(16) float part[4 * 64 * 64];
+    __shared__ __align__(16) float yt[64 * YS];
+    __shared__ float rs[64];
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: scalar registers, no divergence
+    const int RT = (a.p_total + 3) >> 2;                         // row tiles of the activation buffer
+    const int rtb = blockIdx.y * RTW, tb = blockIdx.x * 4;
+    const int row0 = rtb * 16, col0 = tb * 16;
+    const int rows = min(16 * RTW, a.m - row0);  // rows of this tile that exist (others are discarded)
+    const int ntl = a.N >> 4, KB = a.KB, KC = KB >> 2;
+    // row tiles / n-tiles past the end re-read the last one (their results are discarded)
+    int rt_[RTW], t_[4];
+#pragma unroll
+    for (int i = 0; i < RTW; i++) rt_[i] = min(rtb + i, RT - 1);
+#pragma unroll
+    for (int t = 0; t < 4; t++) t_[t] = min(tb + t, ntl - 1);
+    // k-block pairs: this workgroup's share of K (blockIdx.z of gridDim.z), an
+    // eighth of it per wave
+    const int NP = KB >> 1, ks = gridDim.z;
+    const int g0 = blockIdx.z * NP / ks, g1 = (blockIdx.z + 1) * NP / ks;
+    const int p0 = g0 + wave * (g1 - g0) / NW, p1 = g0 + (wave + 1) * (g1 - g0) / NW;
+
+    f32x4 acc[RTW][4];
+#pragma unroll
+    for (int i = 0; i < RTW; i++)
+#pragma unroll
+        for (int t = 0; t < 4; t++) acc[i][t] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
+    const f32x4 fzero = {0.0f, 0.0f, 0.0f, 0.0f};
+
+    for (int pr = p0; pr < p1; pr++) {
+        const int kb0 = 2 * pr, c = kb0 >> 2, half = (kb0 >> 1) & 1;
+        // every operand of the pair in flight before the first MFMA
+        bf16x8 A[2][RTW][2];  // [k-block][row tile][hi/lo]
+        uint2 w4[4];          // int4: the pair's two 4-byte words
+        u32x4 w8[4];          // int8: the pair's 16 bytes
+        bf16x8 wb[4][2];
+        float2 sv[4];
+#pragma unroll
+        for (int j = 0; j < 2; j++)
+#pragma unroll
+            for (int i = 0; i < RTW; i++)
+#pragma unroll
+                for (int h = 0; h < 2; h++)
+                    A[j][i][h] = ((const bf16x8*)a.XA)[((((size_t)(kb0 + j) * RT + rt_[i]) * 2 + h) * 64) + lane];
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+            const size_t tile = t_[t];
+            if (KIND == INT4)
+                w4[t] = ((const uint2*)a.W)[((tile * KC + c) * 64 + lane) * 2 + half];
+            else if (KIND == INT8)
+                w8[t] = ((const u32x4*)a.W)[(tile * (KB >> 1) + pr) * 64 + lane];
+            else
+#pragma unroll
+                for (int j = 0; j < 2; j++) wb[t][j] = ((const bf16x8*)a.W)[(tile * KB + kb0 + j) * 64 + lane];
+            if (Q) sv[t] = ((const float2*)a.S)[((tile * KC + c) * 16 + (lane & 15)) * 2 + half];
+        }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int j = 0; j < 2; j++)
+#pragma unroll
+            for (int t = 0; t < 4; t++) {
+                bf16x8 B;
+                if (KIND == INT4) {
+                    const uint32_t w = j ? w4[t].y : w4[t].x;
+                    const uint32_t lo = (w << 4) & 0xF0F0F0F0u, hi = w & 0xF0F0F0F0u;
+                    const u32x4 bw = {bf16x2_i8(lo, 0), bf16x2_i8(lo, 2), bf16x2_i8(hi, 0), bf16x2_i8(hi, 2)};
+                    B = __builtin_bit_cast(bf16x8, bw);
+                } else if (KIND == INT8) {
+                    const uint32_t w0 = w8[t][2 * j], w1 = w8[t][2 * j + 1];
+                    const u32x4 bw = {bf16x2_i8(w0, 0), bf16x2_i8(w0, 2), bf16x2_i8(w1, 0), bf16x2_i8(w1, 2)};
+                    B = __builtin_bit_cast(bf16x8, bw);
+                } else {
+                    B = wb[t][j];
+                }
+                const float sj = Q ? (j == 0 ? sv[t].x : sv[t].y) : 1.0f;
+#pragma unroll
+                for (int i = 0; i < RTW; i++) {
+                    if (Q) {
+                        f32x4 d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A[j][i][0], B, fzero, 0, 0, 0);
+                        d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A[j][i][1], B, d, 0, 0, 0);
+#pragma unroll
+                        for (int r = 0; r < 4; r++) acc[i][t][r] = fmaf(d[r], sj, acc[i][t][r]);
+                    } else {
+                        acc[i][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A[j][i][0], B, acc[i][t], 0, 0, 0);
+                        acc[i][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A[j][i][1], B, acc[i][t], 0, 0, 0);
+                    }
+                }
+            }
+    }
+    // Eight partial tiles to one, in a fixed order: waves 4-7 hand theirs to 0-3,
+    // then 2-3 to 0-1, then 1 to 0 (each hand-off in the lanes' own layout).
+    auto put = [&](int slot) {
+#pragma unroll
+        for (int i = 0; i < RTW; i++)
+#pragma unroll
+            for (int t = 0; t < 4; t++)
+                *(f32x4*)&part[((slot * 16 + i * 4 + t) * 64 + lane) * 4] = acc[i][t];
+    };
+    auto take = [&](int slot) {
+#pragma unroll
+        for (int i = 0; i < RTW; i++)
+#pragma unroll
+            for (int t = 0; t < 4; t++) acc[i][t] += *(const f32x4*)&part[((slot * 16 + i * 4 + t) * 64 + lane) * 4];
+    };
+    if (wave >= 4) put(wave - 4);
+    __syncthreads();
+    if (wave < 4) take(wave);
+    __syncthreads();
+    if (wave == 2 || wave == 3) put(wave - 2);
+    __syncthreads();
+    if (wave < 2) take(wave);
+    __syncthreads();
+    if (wave == 1) put(0);
+    __syncthreads();
+    if (wave == 0) {
+        take(0);
+        if (ks > 1) {
+            // split K: this workgroup's partial tile goes to kpart[z][row][col]; k_gemm_finish sums
+            // the splits in order and runs the epilogue
+#pragma unroll
+            for (int i = 0; i < RTW; i++)
+#pragma unroll
+                for (int t = 0; t < 4; t++)
+#pragma unroll
+                    for (int r = 0; r < 4; r++) {
+                        const int rr = i * 16 + 4 * (lane >> 4) + r, cc = t * 16 + (lane & 15);
+                        if (rr < rows && col0 + cc < a.N)
+                            a.kpart[((size_t)blockIdx.z * a.m + row0 + rr) * a.N + col0 + cc] = acc[i][t][r];
+                    }
+            return;
+        }
+        // D of a 16 x 16 tile has row 4 (l / 16) + r, column l % 16 in lane l
+#pragma unroll
+        for (int i = 0; i < RTW; i++)
+#pragma unroll
+            for (int t = 0; t < 4; t++)
+#pragma unroll
+                for (int r = 0; r < 4; r++) yt[(i * 16 + 4 * (lane >> 4) + r) * YS + t * 16 + (lane & 15)] = acc[i][t][r];
+    }
+    if (ks > 1) return;
+    gemm_epilogue<EPI, NTHR>(a, yt, part, rs, row0, rows, col0);
+}
+
+// The split-K sum (splits in order, so the result does not depend on which
+// workgroup finished first) and the epilogue of one 16 RTW x 64 tile.
+template <int EPI, int RTW>
+__global__ __launch_bounds__(256) void k_gemm_finish(const GemvArgs a) {
+    constexpr int YS = 68;
+    __shared__ __align__(16) float vt[64 * YS];
+    __shared__ __align__(16) float yt[64 * YS];
+    __shared__ float rs[64];
+    const int row0 = blockIdx.y * RTW * 16, col0 = blockIdx.x * 64;
+    const int rows = min(16 * RTW, a.m - row0);
+    // four 4-column slots per thread, every split's load issued before the sums
+    // (clamped addresses; splits past ks and slots past the tile are masked)
+    constexpr int KSMAX = 8;
+    float4 v[4][KSMAX];
+#pragma unroll
+    for (int it = 0; it < 4; it++) {
+        const int slot = threadIdx.x + it * 256, rr = min(slot >> 4, rows - 1), c = min(col0 + (slot & 15) * 4, a.N - 4);
+#pragma unroll
+        for (int z = 0; z < KSMAX; z++)
+            v[it][z] = *(const float4*)&a.kpart[((size_t)min(z, a.ks - 1) * a.m + row0 + rr) * a.N + c];
+    }
+#pragma unroll
+    for (int it = 0; it < 4; it++) {
+        const int slot = threadIdx.x + it * 256, rr = slot >> 4, cc = (slot & 15) * 4;
+        const bool live = rr < rows && col0 + cc < a.N;
+        float4 t = v[it][0];
+#pragma unroll
+        for (int z = 1; z < KSMAX; z++)
+            if (z < a.ks) {
+                t.x += v[it][z].x;
+                t.y += v[it][z].y;
+                t.z += v[it][z].z;
+                t.w += v[it][z].w;
+            }
+        *(float4*)&yt[rr * YS + cc] = live ? t : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    }
+    gemm_epilogue<EPI, 256>(a, yt, vt, rs, row0, rows, col0);
+}
+
+template <int KIND, int RTW>
+static void gemm_rtw(hipStream_t st, int epi, const DMat& w, const GemvArgs& a0, int groups, hipEvent_t e0,
+                     hipEvent_t e1) {
+    // Split K across workgroups when the tiles alone leave most CUs idle: up
+    // to 256 workgroups, at least one k-block pair per wave and split, and the
+    // partial tiles within the workspace's kpart buffer.
+    GemvArgs a = a0;
+    const int cg = (w.n_tiles + 3) / 4, np = w.kb / 2;
+    int ks = 1;
+    if (a.kpart)
+        while (ks < 8 && cg * groups * ks * 2 <= 256 && np / (ks * 2) >= 8 &&
+               (size_t)ks * 2 * a.m * a.N <= a.kpart_cap)
+            ks *= 2;
+    a.ks = ks;
+    const dim3 grid(cg, groups, ks);
+    auto finish = [&](auto kern) {
+        if (ks > 1) hipLaunchKernelGGL(kern, dim3(cg, groups), dim3(256), 0, st, a);
+    };
+    // with a split, the timed span ends at the main kernel (the finish is short)
+    switch (epi) {
+        case EPI_STORE:
+            launch_timed(k_gemm<KIND, EPI_STORE, RTW>, grid, dim3(512), st, a, e0, e1);
+            finish(k_gemm_finish<EPI_STORE, RTW>);
+            break;
+        case EPI_QKV:
+            launch_timed(k_gemm<KIND, EPI_QKV, RTW>, grid, dim3(512), st, a, e0, e1);
+            finish(k_gemm_finish<EPI_QKV, RTW>);
+            break;
+        case EPI_RESID:
+            launch_timed(k_gemm<KIND, EPI_RESID, RTW>, grid, dim3(512), st, a, e0, e1);
+            finish(k_gemm_finish<EPI_RESID, RTW>);
+            break;
+        case EPI_SILU:
+            launch_timed(k_gemm<KIND, EPI_SILU, RTW>, grid, dim3(512), st, a, e0, e1);
+            finish(k_gemm_finish<EPI_SILU, RTW>);
+            break;
+        case EPI_ARGMAX:
+            launch_timed(k_gemm<KIND, EPI_ARGMAX, RTW>, grid, dim3(512), st, a, e0, e1);
+            finish(k_gemm_finish<EPI_ARGMAX, RTW>);
+            break;
+    }
+}
+
+// Row tiles per workgroup: as few groups of at most four as cover the rows,
+// each as small as that allows (rows past m cost loads and MFMAs).
+template <int KIND>
+static void gemm_kind(hipStream_t st, int epi, const DMat& w, const GemvArgs& a, hipEvent_t e0, hipEvent_t e1) {
+    const int rt = (a.p_total + 3) / 4, groups = (rt + 3) / 4, rtw = (rt + groups - 1) / groups;
+    if (rtw <= 2)
+        gemm_rtw<KIND, 2>(st, epi, w, a, (rt + 1) / 2, e0, e1);
+    else if (rtw == 3)
+        gemm_rtw<KIND, 3>(st, epi, w, a, (rt + 2) / 3, e0, e1);
+    else
+        gemm_rtw<KIND, 4>(st, epi, w, a, groups, e0, e1);
 }
 
 template <int KIND, int NT, int EPI>
@@ -717,6 +1138,15 @@ static void gemv_kind(hipStream_t st, int epi, const DMat& w, const GemvArgs& a,
 
 void launch_gemv(hipStream_t st, int epi, const DMat& w, const GemvArgs& a, hipEvent_t start, hipEvent_t stop) {
     if (a.m <= 0) return;
+    if (a.mm) {
+        if (w.kind == INT4)
+            gemm_kind<INT4>(st, epi, w, a, start, stop);
+        else if (w.kind == INT8)
+            gemm_kind<INT8>(st, epi, w, a, start, stop);
+        else
+            gemm_kind<BF16>(st, epi, w, a, start, stop);
+        return;
+    }
     if (w.kind == INT4)
         gemv_kind<INT4>(st, epi, w, a, start, stop);
     else if (w.kind == INT8)
@@ -974,6 +1404,9 @@ static void attention_hd(hipStream_t st, const AttnArgs& a, int m, int ck, Piece
     hipLaunchKernelGGL((k_attn<HD, P, QM>), dim3(a.nkv, a.n_wi), dim3(256), 0, st, a);
     if (ck == BF16)
         hipLaunchKernelGGL((k_merge_pieces<HD, QM, BF16>), dim3(out.kb, out.passes), dim3(64), 0, st, a, m, out.a,
+                           out.xs, out.passes);
+    else if (ck == MM)
+        hipLaunchKernelGGL((k_merge_pieces<HD, QM, MM>), dim3(out.kb, out.passes), dim3(64), 0, st, a, m, out.a,
                            out.xs, out.passes);
     else
         hipLaunchKernelGGL((k_merge_pieces<HD, QM, INT8>), dim3(out.kb, out.passes), dim3(64), 0, st, a, m, out.a,
