@@ -150,7 +150,7 @@ static void gemv(fg_ctx* c, int epi, const DMat& w, const GemvArgs& a) {
         launch_gemv(c->stream, epi, w, a);
         return;
     }
-    const int pg = a.p_total == 1 ? 0 : a.p_total == 2 ? 1 : 2;
+    const int pg = a.mm ? 3 : a.p_total == 1 ? 0 : a.p_total == 2 ? 1 : 2;
     const size_t i0 = c->pev_used;
     hipEvent_t e0 = prof_event(c), e1 = prof_event(c);
     if (!e0 || !e1) {

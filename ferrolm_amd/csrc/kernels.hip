@@ -685,7 +685,7 @@ __global__ __launch_bounds__(64 * WMAX) void k_gemv(const GemvArgs a) {
 template <class K>
 static void launch_timed(K kernel, dim3 grid, dim3 block, hipStream_t st, const GemvArgs& a, hipEvent_t e0,
                          hipEvent_t e1) {
-    if (e0 && e1)
+    if (e0 || e1)
         hipExtLaunchKernelGGL(kernel, grid, block, 0, st, e0, e1, 0, a);
     else
         hipLaunchKernelGGL(kernel, grid, block, 0, st, a);
@@ -984,7 +984,8 @@ __global__ __launch_bounds__(512) void k_gemm(const GemvArgs a) {
 }
 
 // The split-K sum (splits in order, so the result does not depend on which
-// workgroup finished first) and the epilogue of one 16 RTW x 64 tile.
+// workgroup finished first) and the epilogue of one 16 RTW x 64 tile (launched
+// on 16-row slabs, RTW 1, for more workgroups).
 template <int EPI, int RTW>
 __global__ __launch_bounds__(256) void k_gemm_finish(const GemvArgs a) {
     constexpr int YS = 68;
@@ -993,19 +994,20 @@ __global__ __launch_bounds__(256) void k_gemm_finish(const GemvArgs a) {
     __shared__ float rs[64];
     const int row0 = blockIdx.y * RTW * 16, col0 = blockIdx.x * 64;
     const int rows = min(16 * RTW, a.m - row0);
-    // four 4-column slots per thread, every split's load issued before the sums
-    // (clamped addresses; splits past ks and slots past the tile are masked)
+    // RTW 4-column slots per thread (16 RTW rows x 16 slots), every split's load
+    // issued before the sums (clamped addresses; splits past ks and slots past
+    // the tile are masked)
     constexpr int KSMAX = 8;
-    float4 v[4][KSMAX];
+    float4 v[RTW][KSMAX];
 #pragma unroll
-    for (int it = 0; it < 4; it++) {
+    for (int it = 0; it < RTW; it++) {
         const int slot = threadIdx.x + it * 256, rr = min(slot >> 4, rows - 1), c = min(col0 + (slot & 15) * 4, a.N - 4);
 #pragma unroll
         for (int z = 0; z < KSMAX; z++)
             v[it][z] = *(const float4*)&a.kpart[((size_t)min(z, a.ks - 1) * a.m + row0 + rr) * a.N + c];
     }
 #pragma unroll
-    for (int it = 0; it < 4; it++) {
+    for (int it = 0; it < RTW; it++) {
         const int slot = threadIdx.x + it * 256, rr = slot >> 4, cc = (slot & 15) * 4;
         const bool live = rr < rows && col0 + cc < a.N;
         float4 t = v[it][0];
@@ -1037,31 +1039,21 @@ static void gemm_rtw(hipStream_t st, int epi, const DMat& w, const GemvArgs& a0,
             ks *= 2;
     a.ks = ks;
     const dim3 grid(cg, groups, ks);
-    auto finish = [&](auto kern) {
-        if (ks > 1) hipLaunchKernelGGL(kern, dim3(cg, groups), dim3(256), 0, st, a);
+    // timed from the start of the main kernel to the end of the split's finish
+    auto run = [&](auto kern, auto fin) {
+        if (ks == 1) {
+            launch_timed(kern, grid, dim3(512), st, a, e0, e1);
+        } else {
+            launch_timed(kern, grid, dim3(512), st, a, e0, nullptr);
+            launch_timed(fin, dim3(cg, (a.m + 15) / 16), dim3(256), st, a, nullptr, e1);
+        }
     };
-    // with a split, the timed span ends at the main kernel (the finish is short)
     switch (epi) {
-        case EPI_STORE:
-            launch_timed(k_gemm<KIND, EPI_STORE, RTW>, grid, dim3(512), st, a, e0, e1);
-            finish(k_gemm_finish<EPI_STORE, RTW>);
-            break;
-        case EPI_QKV:
-            launch_timed(k_gemm<KIND, EPI_QKV, RTW>, grid, dim3(512), st, a, e0, e1);
-            finish(k_gemm_finish<EPI_QKV, RTW>);
-            break;
-        case EPI_RESID:
-            launch_timed(k_gemm<KIND, EPI_RESID, RTW>, grid, dim3(512), st, a, e0, e1);
-            finish(k_gemm_finish<EPI_RESID, RTW>);
-            break;
-        case EPI_SILU:
-            launch_timed(k_gemm<KIND, EPI_SILU, RTW>, grid, dim3(512), st, a, e0, e1);
-            finish(k_gemm_finish<EPI_SILU, RTW>);
-            break;
-        case EPI_ARGMAX:
-            launch_timed(k_gemm<KIND, EPI_ARGMAX, RTW>, grid, dim3(512), st, a, e0, e1);
-            finish(k_gemm_finish<EPI_ARGMAX, RTW>);
-            break;
+        case EPI_STORE: run(k_gemm<KIND, EPI_STORE, RTW>, k_gemm_finish<EPI_STORE, 1>); break;
+        case EPI_QKV: run(k_gemm<KIND, EPI_QKV, RTW>, k_gemm_finish<EPI_QKV, 1>); break;
+        case EPI_RESID: run(k_gemm<KIND, EPI_RESID, RTW>, k_gemm_finish<EPI_RESID, 1>); break;
+        case EPI_SILU: run(k_gemm<KIND, EPI_SILU, RTW>, k_gemm_finish<EPI_SILU, 1>); break;
+        case EPI_ARGMAX: run(k_gemm<KIND, EPI_ARGMAX, RTW>, k_gemm_finish<EPI_ARGMAX, 1>); break;
     }
 }
 

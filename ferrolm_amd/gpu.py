@@ -297,7 +297,8 @@ def profile(ctx: Context, on: bool) -> None:
 
 
 def profile_read(ctx: Context, reset: bool = True) -> list:
-    """Per kernel class: dict(kind, passes, launches, us, bytes, flops)."""
+    """Per kernel class: dict(kind, passes, gemm, launches, us, bytes, flops); gemm is True for
+    the GEMM path (more than 16 rows), whose passes is reported as 0."""
     cap = 12
     cls = np.zeros(cap, np.int32)
     n = np.zeros(cap, np.int64)
@@ -309,7 +310,8 @@ def profile_read(ctx: Context, reset: bool = True) -> list:
                               us.ctypes.data_as(dp), by.ctypes.data_as(dp), fl.ctypes.data_as(dp), int(reset))
     if r < 0:
         check(r)
-    return [dict(kind=KIND_LABEL[int(cls[i]) // 4], passes=(1, 2, 4)[int(cls[i]) % 4], launches=int(n[i]),
+    return [dict(kind=KIND_LABEL[int(cls[i]) // 4], passes=(1, 2, 4, 0)[int(cls[i]) % 4],
+                 gemm=int(cls[i]) % 4 == 3, launches=int(n[i]),
                  us=float(us[i]), bytes=float(by[i]), flops=float(fl[i])) for i in range(min(r, cap))]
 
 

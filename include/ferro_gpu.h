@@ -185,7 +185,8 @@ int fg_last_step_times(const fg_ctx* ctx, float* us3);
  * every GEMV launch on the context's stream is bracketed by HIP events;
  * fg_profile_read() synchronises, folds the finished launches into one
  * record per kernel class and returns up to `cap` records:
- * cls[i] = format*4 + (rows-per-pass group: 1, 2 or 4 passes -> 0, 1, 2),
+ * cls[i] = format*4 + (GEMV by passes of 4 rows: 1, 2 or more -> 0, 1, 2;
+ * the GEMM of more than 16 rows, including its split-K finish -> 3),
  * launches[i], us[i] (summed device time), bytes[i] (summed algorithmic
  * bytes: codes + scales + activations in + outputs, per launch), flops[i]
  * (summed algorithmic flops, 2 x rows x n x k per launch).
