@@ -497,8 +497,13 @@ struct Work {
 static int kind_of(const DMat& m) { return m.kind; }
 
 // Steps with more rows than this run their projections as GEMMs (k_gemm on
-// MM pieces); up to this many rows, as GEMVs on BF16/INT8 pieces.
+// MM pieces); up to this many rows, as GEMVs on BF16/INT8 pieces. A model
+// narrower than kGemmMinHidden keeps the GEMV at any row count: its small
+// projections finish sooner on the GEMV (measured: the 135M shape's at 8 to
+// 64 rows), while the lm_head, a large product either way, switches at
+// kGemvRows for every model.
 static constexpr int kGemvRows = 16;
+static constexpr int kGemmMinHidden = 1024;
 
 // n-tiles per workgroup of a bf16 projection with fewer than 256 tiles: one, so
 // that it spreads over twice the CUs (a CU streams only about 22 GB/s), unless
@@ -532,7 +537,7 @@ static size_t layout_work(const fg_model* m, const Plan& P, Work& w, void* base)
     w.best = cv.take<float2>((size_t)(c.vocab / 32) * S);
     w.am = cv.take<uint32_t>(S);
     // the split rule keeps splits x rows x N within 64 x 256 x 64 floats
-    w.kpart_cap = t > kGemvRows ? (size_t)1 << 20 : 0;
+    w.kpart_cap = (t > kGemvRows && H >= kGemmMinHidden) || S > kGemvRows ? (size_t)1 << 20 : 0;
     w.kpart = w.kpart_cap ? cv.take<float>(w.kpart_cap) : nullptr;
     return cv.off + 256;
 }
@@ -577,8 +582,8 @@ static int run_forward(fg_ctx* ctx, const fg_model* m, fg_kv* kv, const Plan& P,
     if (t == 0) return 0;
     const int passes = w.passes;
     int cur = 0;  // pieces buffer the next GEMV reads
-    // more than 16 rows: every projection runs as a GEMM on MM pieces
-    const bool mm = t > kGemvRows;
+    // more than 16 rows (of a wide enough model): every projection runs as a GEMM on MM pieces
+    const bool mm = t > kGemvRows && H >= kGemmMinHidden;
     auto ck = [&](const DMat& d) { return mm ? (int)MM : kind_of(d); };
 
     if (L > 0) {

@@ -225,11 +225,10 @@ def test_batched_speculative_steps_gqa_head_dim_128(ctx):
 
 
 @pytest.mark.parametrize("n_seqs", [1, 2])
-def test_speculative_steps_self_merging_output_projection(ctx, n_seqs):
-    """Head dim 64 with one pass of rows (up to 4): the output projection merges the
-    attention spans itself instead of a separate merge launch. One sequence uses it
-    in the draft rounds and the verify; two sequences use it in the draft rounds and
-    the separate merge in the 6-row verify. Each step is checked against the oracle."""
+def test_speculative_steps_head_dim_64_one_and_two_passes(ctx, n_seqs):
+    """Head dim 64 (64-position spans, three query heads per kv head): one sequence
+    keeps every step within one pass of rows (up to 4); two sequences make a 6-row
+    verify. Each step is checked against the oracle."""
     from ferrolm_amd.synth import random_model
     from ferrolm_amd.weights import Config
     cfg = Config(vocab=512, hidden=192, intermediate=384, layers=2, heads=6, kv_heads=2, head_dim=64,
@@ -258,3 +257,30 @@ def test_quantized_forward_matches_oracle(ctx):
         om = oracle.Model(hm)
         ol = om.forward(om.kv(8), [(prompt, 0, table, 2)])
         assert np.abs(out.logits - ol).max() < 1e-4 * np.abs(ol).max(), kind
+
+
+@pytest.mark.parametrize("kind", [BF16, INT8, INT4])
+def test_gemm_path_forward_and_batched_steps(ctx, kind):
+    """Steps of more than 16 rows on a model 1024 wide run every projection as the
+    bf16-MFMA GEMM (activations as hi + lo bf16 pieces, split K for the narrow
+    products): a 40-token prefill with all logits and the hidden states against the
+    oracle, then batched speculative steps whose 20-row verifies are GEMMs, each
+    sequence's tokens against the oracle's spec step."""
+    from ferrolm_amd.synth import random_model
+    from ferrolm_amd.weights import Config
+    cfg = Config(vocab=1024, hidden=1024, intermediate=2048, layers=2, heads=16, kv_heads=4, head_dim=64,
+                 rms_eps=1e-5, max_position=2048)
+    hm = _quantized(random_model(cfg, seed=21, std=0.03), kind)
+    rng = np.random.default_rng(22)
+    prompt = [int(x) for x in rng.integers(3, 1000, 40)]
+    table, blocks = scattered_table(64)
+    m = gpu.Model(ctx, hm)
+    kv = gpu.KvCache(ctx, hm.cfg, blocks)
+    out = gpu.forward(ctx, m, kv, [(prompt, 0, table, gpu.LOGITS_ALL)], hidden=True)
+    om = oracle.Model(hm)
+    ol, oh = om.forward(om.kv(blocks), [(prompt, 0, table, 2)], hidden=True)
+    assert np.abs(out.logits - ol).max() < 1e-4 * np.abs(ol).max(), kind
+    rel = np.linalg.norm(out.hidden - oh, axis=-1) / np.linalg.norm(oh, axis=-1)
+    assert rel.max() < 1e-4, rel.max()
+    prompts = [[int(x) for x in rng.integers(3, 1000, n)] for n in (40, 90, 17, 130)]
+    _batched_matches_oracle(ctx, hm, prompts, k=4, steps=6, kv_blocks=64, seed=23)
