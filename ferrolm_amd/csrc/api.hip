@@ -83,6 +83,7 @@ struct fg_ctx {
     size_t hmeta_cap = 0;
     hipEvent_t ev[3] = {nullptr, nullptr, nullptr};
     float last_us[3] = {0, 0, 0};
+    bool merge_in_o = true;  // small bf16 output projections merge the attention spans themselves
     // GEMV launch profiling (fg_profile)
     bool prof = false;
     std::vector<hipEvent_t> pev;
@@ -515,6 +516,16 @@ static int narrow_nt(const DMat& w, bool int8_pieces) {
 }
 static int qkv_dim(const fg_config& c) { return (c.heads + 2 * c.kv_heads) * c.head_dim; }
 
+// Whether the output projection merges the attention spans itself (one launch
+// less per layer): a bf16 projection of one pass of rows over at most 1024
+// inputs, when the partials each workgroup re-reads stay small (every
+// workgroup merges every head; the 135M draft reads about 40 KB per row).
+static bool merge_in_o(const fg_config& c, const Plan& P, const DMat& wo, bool mm) {
+    if (mm || wo.kind != BF16 || P.t > 4 || wo.kb > 32 || c.heads * c.head_dim > 1024) return false;
+    const size_t part_bytes = (size_t)P.t * c.heads * P.Wc * (c.head_dim + 2) * 4;  // bound: every row sees Wc spans
+    return part_bytes <= 160 * 1024;
+}
+
 static size_t layout_work(const fg_model* m, const Plan& P, Work& w, void* base) {
     const fg_config& c = m->cfg;
     const int t = P.t, H = c.hidden, S = std::max(P.S, 1);
@@ -631,10 +642,20 @@ static int run_forward(fg_ctx* ctx, const fg_model* m, fg_kv* kv, const Plan& P,
         aa.kc = kv->k + li * kv->layer_floats();
         aa.vc = kv->v + li * kv->layer_floats();
         Pieces po = pieces(w, cur ^ 1, l.wo.kb, passes);
-        launch_attention(st, aa, t, ck(l.wo), po);
+        const bool am = ctx->merge_in_o && merge_in_o(c, P, l.wo, mm);
+        launch_attention(st, aa, t, am ? -1 : ck(l.wo), po);
         cur ^= 1;
         // o projection + residual; pieces of mlp_norm * x for gate/up
         g = gemv_args(l.wo, pieces(w, cur, l.wo.kb, passes), t, w);
+        if (am) {
+            g.am = true;
+            g.apart = w.apart;
+            g.amrec = aa.mrec;
+            g.anh = nh;
+            g.ankv = nkv;
+            g.ahd = hd;
+            g.aqm = attn_qmax(hd);
+        }
         g.x = w.x;
         g.ldx = H;
         g.ss_out = w.ss;
@@ -735,6 +756,8 @@ int fg_ctx_create(int device, fg_ctx** out) {
     for (auto& e : c->ev) HIPCHK(hipEventCreate(&e));
     const char* ng = std::getenv("FERRO_NO_GRAPH");
     c->graphs = !(ng && ng[0] == '1');
+    const char* sm = std::getenv("FERRO_SEPARATE_MERGE");
+    c->merge_in_o = !(sm && sm[0] == '1');
     *out = c;
     return 0;
 }

@@ -114,6 +114,12 @@ struct GemvArgs {
     // ARGMAX
     float* logits = nullptr;
     float2* best = nullptr;
+    // RESID with am: the input is the attention output, merged in the workgroup
+    // from the span partials (AttnArgs::part / mrec) instead of read as pieces
+    bool am = false;
+    const float* apart = nullptr;
+    const int32_t* amrec = nullptr;
+    int anh = 0, ankv = 0, ahd = 0, aqm = 0;
 };
 
 // start/stop (optional) are recorded by the dispatch itself (hipExtLaunchKernelGGL),
@@ -146,7 +152,8 @@ struct AttnArgs {
     float scale;
 };
 // Attention over the paged cache (RoPE, K/V write of the new rows), then the
-// split merge straight into the output projection's pieces.
+// split merge straight into the output projection's pieces (consumer_kind < 0:
+// no merge, the output projection merges the spans itself).
 void launch_attention(hipStream_t st, const AttnArgs& a, int m, int consumer_kind, Pieces& out);
 
 void launch_argmax_final(hipStream_t st, const float2* best, int tiles, int rows, uint32_t* argmax_out,

@@ -37,10 +37,8 @@ typedef int8_t i8x8 __attribute__((ext_vector_type(8)));
 
 __device__ __forceinline__ float bf16_bits_to_f32(uint32_t h) { return __uint_as_float(h << 16); }
 
-__device__ __forceinline__ uint32_t f32_to_bf16_bits(float x) {
-    const uint32_t b = __float_as_uint(x);
-    return (b + 0x7FFFu + ((b >> 16) & 1u)) >> 16;
-}
+// round to nearest even (v_cvt_pk_bf16_f32)
+__device__ __forceinline__ uint32_t f32_to_bf16_bits(float x) { return __builtin_bit_cast(uint16_t, (__bf16)x); }
 
 // exp(x) by range reduction and the Cephes expf polynomial, the same
 // sequence of operations as the reference's kernels::exp (src/kernels.rs:609-637).
@@ -227,6 +225,70 @@ __device__ __forceinline__ void write_pieces_pair_kind(int kind, float x0, float
         write_pieces_pair<INT8>(x0, x1, mx, pair, kb, pass, passes, row, piece, lane, out, xs);
 }
 
+// Merge of the spans of one (row, query head, 8 dims) at input k0 of the
+// attention output: the lane takes spans phase, phase + 4, ... (phase 0..3),
+// and the four lanes of an aligned quad (phases 0..3 of the same row and
+// inputs, all active) combine their sums in a fixed order, so all four end
+// with the same bits. SB spans are loaded per round trip; the merge order
+// (the lane's spans in sequence) does not depend on SB.
+template <int SB>
+__device__ __forceinline__ void merge_spans(const float* __restrict__ part, const int32_t* __restrict__ mrec, int nh,
+                                            int nkv, int hd, int qm, int row, int k0, int phase, float (&v)[8]) {
+    const int hq = k0 / hd, d0 = k0 % hd;
+    const int G = nh / nkv, h = hq / G, j = hq % G;
+    const int4 mr = *(const int4*)(mrec + (size_t)row * 4);
+    const int qi = mr.x + j, wi0 = mr.y, ns = mr.z;
+    const size_t stride = (size_t)nkv * qm * (hd + 2);
+    const float* base = part + ((size_t)wi0 * nkv * qm + (size_t)h * qm + qi) * (hd + 2);
+    // merge of this lane's spans, SB per round trip: every load of a batch is
+    // issued (from clamped, always valid addresses) before the first is used,
+    // spans past ns are masked out; the running sums are rescaled once per
+    // batch, to the batch's maximum
+    float M = -INFINITY, L = 0.0f, O[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    for (int s0 = phase; s0 < ns; s0 += 4 * SB) {
+        float2 st[SB];
+        float ov[SB][8];
+#pragma unroll
+        for (int b = 0; b < SB; b++) {
+            const float* p = base + min(s0 + 4 * b, ns - 1) * stride;
+            st[b] = *(const float2*)p;
+            const float2 o01 = *(const float2*)(p + 2 + d0), o23 = *(const float2*)(p + 4 + d0);
+            const float2 o45 = *(const float2*)(p + 6 + d0), o67 = *(const float2*)(p + 8 + d0);
+            ov[b][0] = o01.x, ov[b][1] = o01.y, ov[b][2] = o23.x, ov[b][3] = o23.y;
+            ov[b][4] = o45.x, ov[b][5] = o45.y, ov[b][6] = o67.x, ov[b][7] = o67.y;
+        }
+        float nM = M;
+#pragma unroll
+        for (int b = 0; b < SB; b++) nM = s0 + 4 * b < ns ? fmaxf(nM, st[b].x) : nM;
+        const float fo = M == -INFINITY ? 0.0f : dev_exp(M - nM);
+        L *= fo;
+#pragma unroll
+        for (int e = 0; e < 8; e++) O[e] *= fo;
+#pragma unroll
+        for (int b = 0; b < SB; b++) {
+            const float w = s0 + 4 * b < ns && st[b].x != -INFINITY ? dev_exp(st[b].x - nM) : 0.0f;
+            L = fmaf(st[b].y, w, L);
+#pragma unroll
+            for (int e = 0; e < 8; e++) O[e] = fmaf(ov[b][e], w, O[e]);
+        }
+        M = nM;
+    }
+    // the four lanes of the quad, in a fixed order
+    float MA = fmaxf(M, lane_xor1(M));
+    MA = fmaxf(MA, lane_xor2(MA));
+    const float f = M == -INFINITY ? 0.0f : dev_exp(M - MA);
+    L *= f;
+    L += lane_xor1(L);
+    L += lane_xor2(L);
+#pragma unroll
+    for (int e = 0; e < 8; e++) {
+        O[e] *= f;
+        O[e] += lane_xor1(O[e]);
+        O[e] += lane_xor2(O[e]);
+        v[e] = O[e] / L;
+    }
+}
+
 // Pieces of g * x[rows_src[row]] (g, rows_src optional). One wave per
 // (k-block, pass).
 template <int CK>
@@ -332,7 +394,10 @@ void launch_embed(hipStream_t st, const uint32_t* tokens, int stride, const uint
 // four pieces of activation row l/16 of the pass) of column l%16 (output n).
 // ---------------------------------------------------------------------------
 
-template <int KIND, int NT, int EPI, int PG, int WMAX = 8>
+// AM: the input is the attention output, merged by the workgroup itself from
+// the span partials (instead of a separate merge kernel writing pieces):
+// bf16 weights, one pass, at most 1024 inputs.
+template <int KIND, int NT, int EPI, int PG, int WMAX = 8, bool AM = false>
 __global__ __launch_bounds__(64 * WMAX) void k_gemv(const GemvArgs a) {
     constexpr bool Q = KIND != BF16;
     // chunks loaded ahead per wave: about 16 B x 4 per lane and tile of weights in
@@ -351,6 +416,8 @@ __global__ __launch_bounds__(64 * WMAX) void k_gemv(const GemvArgs a) {
     __shared__ __align__(16) float et[16 * YS];  // epilogue inputs: x tile (EPI_RESID) or bias
     __shared__ __align__(16) float gs[32];       // g_next of this group's 32 columns (EPI_RESID)
     __shared__ __align__(16) float vt[16 * YS];  // finished values for the next consumer's pieces
+    constexpr int AMKB = 32;  // AM: the operand of up to 32 k-blocks, [kb][lane] bf16 pieces as in global memory
+    __shared__ __align__(16) u16x8 xm[AM ? AMKB * 64 : 1];
 
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, W = blockDim.x >> 6;
     const int tile0 = blockIdx.x * NT;
@@ -512,10 +579,66 @@ __global__ __launch_bounds__(64 * WMAX) void k_gemv(const GemvArgs a) {
             }
         }
     };
-    int c = c0;
-    for (; c + U <= c1; c += U) chunks(c, std::integral_constant<int, U>{});
-    if constexpr (U > 1)
-        for (; c < c1; c++) chunks(c, std::integral_constant<int, 1>{});
+    if constexpr (AM) {
+        // The weights of the wave's chunks are requested first; meanwhile every
+        // thread merges (row, 8 inputs, span phase) items and writes piece
+        // `phase` of the 8 merged values into xm at its operand slot (the four
+        // phases of an item are its four pieces), and each wave then reads its
+        // operand from xm. This is k_merge_pieces' arithmetic: the same bits
+        // wherever both take a row's spans in one batch (up to 20 spans).
+        static_assert(KIND == BF16 && PG == 1, "bf16 weights, one pass");
+        constexpr int AMC = 1;  // chunks per wave: AMKB k-blocks are at most 8 chunks, one per wave
+        const int wv = __builtin_amdgcn_readfirstlane(wave);
+        const int a0 = wv * KC / W, a1 = (wv + 1) * KC / W;
+        bf16x8 wm[AMC][NT][4];
+#pragma unroll
+        for (int u = 0; u < AMC; u++) {
+            const int cc = min(a0 + u, KC - 1);
+#pragma unroll
+            for (int t = 0; t < NT; t++)
+#pragma unroll
+                for (int j = 0; j < 4; j++)
+                    wm[u][t][j] = ((const bf16x8*)a.W)[((size_t)(tile0 + t) * KB + cc * 4 + j) * 64 + lane];
+        }
+        const int K = a.anh * a.ahd, per_row = K / 2;  // items per row: K / 8 input groups x 4 phases
+        // zero slots: rows past m, inputs past K
+        for (int i = threadIdx.x; i < KB * 64; i += blockDim.x) {
+            const int l = i & 63, row = (l & 15) >> 2, kin = (i >> 6) * 32 + (l >> 4) * 8;
+            if (row >= a.m || kin >= K) xm[i] = (u16x8){0, 0, 0, 0, 0, 0, 0, 0};
+        }
+        for (int i0 = 0; i0 < a.m * per_row; i0 += blockDim.x) {
+            const int item = i0 + threadIdx.x, row = item / per_row, rem = item % per_row;
+            const int k0 = (rem >> 2) * 8, phase = rem & 3;
+            if (row < a.m) {  // whole quads: per_row and blockDim are multiples of 4
+                float v[8];
+                merge_spans<5>(a.apart, a.amrec, a.anh, a.ankv, a.ahd, a.aqm, row, k0, phase, v);
+                u16x8 o;
+#pragma unroll
+                for (int e = 0; e < 8; e++) o[e] = (uint16_t)bf16_piece(v[e], phase);
+                xm[(k0 >> 5) * 64 + ((k0 & 31) >> 3) * 16 + row * 4 + phase] = o;
+            }
+        }
+        __syncthreads();
+#pragma unroll
+        for (int u = 0; u < AMC; u++) {
+            if (a0 + u < a1) {
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    const u16x8 o = xm[((a0 + u) * 4 + j) * 64 + lane];
+                    bf16x8 ab;
+                    __builtin_memcpy(&ab, &o, sizeof(ab));
+#pragma unroll
+                    for (int t = 0; t < NT; t++)
+                        accb[t][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ab, wm[u][t][j], accb[t][0], 0, 0, 0);
+                }
+            }
+        }
+    } else {
+        int c = c0;
+        for (; c + U <= c1; c += U) chunks(c, std::integral_constant<int, U>{});
+        if constexpr (U > 1)
+            for (; c < c1; c++) chunks(c, std::integral_constant<int, 1>{});
+    }
 
     // Park the prologue's values in LDS. Their loads completed with the main
     // loop's; reading them back from LDS later keeps the epilogue from waiting
@@ -1104,6 +1227,19 @@ static void gemv_kind(hipStream_t st, int epi, const DMat& w, const GemvArgs& a,
                 gemv_pg<KIND, 2, EPI_QKV>(st, w, a, e0, e1);
             break;
         case EPI_RESID:
+            if constexpr (KIND == BF16) {
+                if (a.am) {
+                    // the launch shape of the two-kernel path (waves = chunks, up to 8)
+                    const int W = std::max(1, std::min(8, w.kb / 4));
+                    if (a.nt == 1)
+                        launch_timed(k_gemv<BF16, 1, EPI_RESID, 1, 8, true>, dim3(w.n_tiles, 1, 1), dim3(64 * W), st,
+                                     a, e0, e1);
+                    else
+                        launch_timed(k_gemv<BF16, 2, EPI_RESID, 1, 8, true>, dim3(w.n_tiles / 2, 1, 1), dim3(64 * W),
+                                     st, a, e0, e1);
+                    break;
+                }
+            }
             if (a.nt == 1)
                 gemv_pg<KIND, 1, EPI_RESID>(st, w, a, e0, e1);
             else
@@ -1327,8 +1463,7 @@ __global__ __launch_bounds__(256) void k_attn(AttnArgs a) {
 
 // Merge of the spans of each (row, head) into the attention output, written
 // as the output projection's pieces. One wave per (k-block, pass); the four
-// lanes of a (row, 8 dims) pair (one per piece) share the spans and combine
-// their sums in a fixed order.
+// lanes of a (row, 8 dims) pair (one per piece) share the spans.
 template <int HD, int QM, int CK>
 __global__ __launch_bounds__(64) void k_merge_pieces(AttnArgs a, int m, void* __restrict__ out, float* __restrict__ xs,
                                                      int passes) {
@@ -1336,64 +1471,14 @@ __global__ __launch_bounds__(64) void k_merge_pieces(AttnArgs a, int m, void* __
     const int c = lane & 15, row = pass * 4 + (c >> 2), piece = c & 3;
     const int k0 = kb * 32 + (lane >> 4) * 8;
     float v[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-    if (row < m && k0 < a.nh * HD) {
-        const int hq = k0 / HD, d0 = k0 % HD;
-        const int G = a.nh / a.nkv, h = hq / G, j = hq % G;
-        const int4 mr = *(const int4*)(a.mrec + (size_t)row * 4);
-        const int qi = mr.x + j, wi0 = mr.y, ns = mr.z;
-        const size_t stride = (size_t)a.nkv * QM * (HD + 2);
-        const float* base = a.part + ((size_t)wi0 * a.nkv * QM + (size_t)h * QM + qi) * (HD + 2);
-        // online merge of this lane's spans (every fourth), SB per round trip:
-        // every load of a batch is issued (from clamped, always valid
-        // addresses) before the first is used; spans past ns are masked out
-        float M = -INFINITY, L = 0.0f, O[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-        constexpr int SB = 8;
-        for (int s0 = piece; s0 < ns; s0 += 4 * SB) {
-            float2 st[SB];
-            float ov[SB][8];
-#pragma unroll
-            for (int b = 0; b < SB; b++) {
-                const float* p = base + min(s0 + 4 * b, ns - 1) * stride;
-                st[b] = *(const float2*)p;
-                const float2 o01 = *(const float2*)(p + 2 + d0), o23 = *(const float2*)(p + 4 + d0);
-                const float2 o45 = *(const float2*)(p + 6 + d0), o67 = *(const float2*)(p + 8 + d0);
-                ov[b][0] = o01.x, ov[b][1] = o01.y, ov[b][2] = o23.x, ov[b][3] = o23.y;
-                ov[b][4] = o45.x, ov[b][5] = o45.y, ov[b][6] = o67.x, ov[b][7] = o67.y;
-            }
-#pragma unroll
-            for (int b = 0; b < SB; b++) {
-                const bool ok = s0 + 4 * b < ns;
-                const float nM = fmaxf(M, st[b].x);
-                const float fo = M == -INFINITY ? 0.0f : dev_exp(M - nM);
-                const float w = st[b].x == -INFINITY ? 0.0f : dev_exp(st[b].x - nM);
-                const float nL = fmaf(st[b].y, w, L * fo);
-#pragma unroll
-                for (int e = 0; e < 8; e++) O[e] = ok ? fmaf(ov[b][e], w, O[e] * fo) : O[e];
-                L = ok ? nL : L;
-                M = ok ? nM : M;
-            }
-        }
-        // the four lanes of the pair, in a fixed order
-        float MA = fmaxf(M, lane_xor1(M));
-        MA = fmaxf(MA, lane_xor2(MA));
-        const float f = M == -INFINITY ? 0.0f : dev_exp(M - MA);
-        L *= f;
-        L += lane_xor1(L);
-        L += lane_xor2(L);
-#pragma unroll
-        for (int e = 0; e < 8; e++) {
-            O[e] *= f;
-            O[e] += lane_xor1(O[e]);
-            O[e] += lane_xor2(O[e]);
-            v[e] = O[e] / L;
-        }
-    }
+    if (row < m && k0 < a.nh * HD) merge_spans<8>(a.part, a.mrec, a.nh, a.nkv, HD, QM, row, k0, piece, v);
     write_pieces<CK>(v, kb, pass, passes, row, piece, lane, out, xs);
 }
 
 template <int HD, int P, int QM>
 static void attention_hd(hipStream_t st, const AttnArgs& a, int m, int ck, Pieces& out) {
     hipLaunchKernelGGL((k_attn<HD, P, QM>), dim3(a.nkv, a.n_wi), dim3(256), 0, st, a);
+    if (ck < 0) return;  // the consumer merges the spans itself
     if (ck == BF16)
         hipLaunchKernelGGL((k_merge_pieces<HD, QM, BF16>), dim3(out.kb, out.passes), dim3(64), 0, st, a, m, out.a,
                            out.xs, out.passes);

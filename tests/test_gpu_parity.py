@@ -284,3 +284,55 @@ def test_gemm_path_forward_and_batched_steps(ctx, kind):
     assert rel.max() < 1e-4, rel.max()
     prompts = [[int(x) for x in rng.integers(3, 1000, n)] for n in (40, 90, 17, 130)]
     _batched_matches_oracle(ctx, hm, prompts, k=4, steps=6, kv_blocks=64, seed=23)
+
+
+@pytest.mark.parametrize("shape", [(576, 9, 3, 64), (512, 4, 2, 128), (256, 8, 8, 32)])
+def test_output_projection_merge_matches_separate_merge(ctx, shape, monkeypatch):
+    """Decode steps of 1 to 4 rows on bf16 models run the output projection
+    with the attention merge folded in (the span partials merged in each
+    workgroup); a context created with FERRO_SEPARATE_MERGE=1 runs the merge
+    kernel instead. The operands are built with the same arithmetic (both
+    merge a row's spans in one batch at these contexts), so logits, hidden
+    states and the cache agree bit for bit; both agree with the oracle."""
+    from ferrolm_amd.synth import random_model
+    from ferrolm_amd.weights import Config
+    hidden, heads, kv_heads, hd = shape
+    cfg = Config(vocab=512, hidden=hidden, intermediate=2 * hidden, layers=2, heads=heads, kv_heads=kv_heads,
+                 head_dim=hd, rms_eps=1e-5, max_position=2048)
+    hm = random_model(cfg, seed=31, std=0.05)
+    monkeypatch.setenv("FERRO_SEPARATE_MERGE", "1")
+    ctx2 = gpu.Context()
+    monkeypatch.delenv("FERRO_SEPARATE_MERGE")
+    table, blocks = scattered_table(340)
+    rng = np.random.default_rng(32)
+    prompt = [int(x) for x in rng.integers(3, 500, 320)]
+    runs = []
+    for c in (ctx, ctx2):
+        m = gpu.Model(c, hm)
+        kv = gpu.KvCache(c, hm.cfg, blocks)
+        gpu.forward(c, m, kv, [(prompt, 0, table, gpu.LOGITS_LAST)])
+        outs, pos = [], len(prompt)
+        for n in (1, 2, 3, 4):
+            toks = [int(x) for x in rng.integers(3, 500, n)] if c is ctx else runs[0][2][len(outs)]
+            o = gpu.forward(c, m, kv, [(toks, pos, table, gpu.LOGITS_ALL)], hidden=True)
+            outs.append((o.logits, o.hidden, toks))
+            pos += n
+        runs.append(([x[0] for x in outs], [x[1] for x in outs], [x[2] for x in outs],
+                     [kv.layer(i) for i in range(cfg.layers)]))
+        del kv, m
+    ctx2.close()
+    (l1, h1, t1, kv1), (l2, h2, t2, kv2) = runs
+    for a, b in zip(l1, l2):
+        assert np.array_equal(a, b)
+    for a, b in zip(h1, h2):
+        assert np.array_equal(a, b)
+    for (k1, v1), (k2, v2) in zip(kv1, kv2):
+        assert np.array_equal(k1, k2) and np.array_equal(v1, v2)
+    om = oracle.Model(hm)
+    okv = om.kv(blocks)
+    om.forward(okv, [(prompt, 0, table, 1)])
+    pos = len(prompt)
+    for toks, lg in zip(t1, l1):
+        ol = om.forward(okv, [(toks, pos, table, 2)])
+        assert np.abs(lg - ol).max() < 1e-4 * np.abs(ol).max()
+        pos += len(toks)
