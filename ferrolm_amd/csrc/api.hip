@@ -522,7 +522,7 @@ static int qkv_dim(const fg_config& c) { return (c.heads + 2 * c.kv_heads) * c.h
 // workgroup merges every head; the 135M draft reads about 40 KB per row).
 static bool merge_in_o(const fg_config& c, const Plan& P, const DMat& wo, bool mm) {
     if (mm || wo.kind != BF16 || P.t > 4 || wo.kb > 32 || c.heads * c.head_dim > 1024) return false;
-    const size_t part_bytes = (size_t)P.t * c.heads * P.Wc * (c.head_dim + 2) * 4;  // bound: every row sees Wc spans
+    const size_t part_bytes = (size_t)P.t * c.heads * P.Wc * (c.head_dim + 4) * 4;  // bound: every row sees Wc spans
     return part_bytes <= 160 * 1024;
 }
 
@@ -543,7 +543,7 @@ static size_t layout_work(const fg_model* m, const Plan& P, Work& w, void* base)
         w.pxs[i] = cv.take<float>((size_t)kb_max * passes * 4);
     }
     w.qkv = cv.take<float>((size_t)t * qkv_dim(c));
-    w.apart = cv.take<float>((size_t)std::max(P.Wc, 1) * c.kv_heads * attn_qmax(c.head_dim) * (c.head_dim + 2));
+    w.apart = cv.take<float>((size_t)std::max(P.Wc, 1) * c.kv_heads * attn_qmax(c.head_dim) * (c.head_dim + 4));
     w.logits = cv.take<float>((size_t)S * c.vocab);
     w.best = cv.take<float2>((size_t)(c.vocab / 32) * S);
     w.am = cv.take<uint32_t>(S);

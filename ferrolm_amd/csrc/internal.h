@@ -147,7 +147,7 @@ struct AttnArgs {
     // [rows][4] per row: first query index within its group, the group's first
     // work item, its number of spans, 0
     const int32_t* mrec;
-    float* part;  // [wi][nkv][attn_qmax(hd)][hd+2]
+    float* part;  // [wi][nkv][attn_qmax(hd)][hd+4]: max score, sum of exponentials, 0, 0, weighted values
     int n_wi, nh, nkv, hd, bs;
     float scale;
 };

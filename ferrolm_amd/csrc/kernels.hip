@@ -229,34 +229,43 @@ __device__ __forceinline__ void write_pieces_pair_kind(int kind, float x0, float
 // attention output: the lane takes spans phase, phase + 4, ... (phase 0..3),
 // and the four lanes of an aligned quad (phases 0..3 of the same row and
 // inputs, all active) combine their sums in a fixed order, so all four end
-// with the same bits. SB spans are loaded per round trip; the merge order
-// (the lane's spans in sequence) does not depend on SB.
+// with the same bits. mr is the row's merge record (first query index, first
+// work item, spans). Spans are loaded SB per round trip (load(s0), from
+// clamped, always valid addresses, every load issued before any is used) and
+// folded batch by batch (fold(s0)): the running sums are rescaled once per
+// batch, to the batch's maximum; spans past ns are masked out.
 template <int SB>
-__device__ __forceinline__ void merge_spans(const float* __restrict__ part, const int32_t* __restrict__ mrec, int nh,
-                                            int nkv, int hd, int qm, int row, int k0, int phase, float (&v)[8]) {
-    const int hq = k0 / hd, d0 = k0 % hd;
-    const int G = nh / nkv, h = hq / G, j = hq % G;
-    const int4 mr = *(const int4*)(mrec + (size_t)row * 4);
-    const int qi = mr.x + j, wi0 = mr.y, ns = mr.z;
-    const size_t stride = (size_t)nkv * qm * (hd + 2);
-    const float* base = part + ((size_t)wi0 * nkv * qm + (size_t)h * qm + qi) * (hd + 2);
-    // merge of this lane's spans, SB per round trip: every load of a batch is
-    // issued (from clamped, always valid addresses) before the first is used,
-    // spans past ns are masked out; the running sums are rescaled once per
-    // batch, to the batch's maximum
-    float M = -INFINITY, L = 0.0f, O[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-    for (int s0 = phase; s0 < ns; s0 += 4 * SB) {
-        float2 st[SB];
-        float ov[SB][8];
+struct SpanMerge {
+    const float* base;
+    size_t stride;
+    int ns, d0;
+    float M, L, O[8];
+    float2 st[SB];
+    float ov[SB][8];
+
+    __device__ __forceinline__ void init(const float* __restrict__ part, int4 mr, int nh, int nkv, int hd, int qm,
+                                         int k0) {
+        const int hq = k0 / hd, G = nh / nkv, h = hq / G, j = hq % G;
+        d0 = k0 % hd;
+        ns = mr.z;
+        stride = (size_t)nkv * qm * (hd + 4);
+        base = part + ((size_t)mr.y * nkv * qm + (size_t)h * qm + mr.x + j) * (hd + 4);
+        M = -INFINITY;
+        L = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 8; e++) O[e] = 0.0f;
+    }
+    __device__ __forceinline__ void load(int s0) {
 #pragma unroll
         for (int b = 0; b < SB; b++) {
             const float* p = base + min(s0 + 4 * b, ns - 1) * stride;
             st[b] = *(const float2*)p;
-            const float2 o01 = *(const float2*)(p + 2 + d0), o23 = *(const float2*)(p + 4 + d0);
-            const float2 o45 = *(const float2*)(p + 6 + d0), o67 = *(const float2*)(p + 8 + d0);
-            ov[b][0] = o01.x, ov[b][1] = o01.y, ov[b][2] = o23.x, ov[b][3] = o23.y;
-            ov[b][4] = o45.x, ov[b][5] = o45.y, ov[b][6] = o67.x, ov[b][7] = o67.y;
+            const float4 o0 = *(const float4*)(p + 4 + d0), o1 = *(const float4*)(p + 8 + d0);
+            ov[b][0] = o0.x, ov[b][1] = o0.y, ov[b][2] = o0.z, ov[b][3] = o0.w;
+            ov[b][4] = o1.x, ov[b][5] = o1.y, ov[b][6] = o1.z, ov[b][7] = o1.w;
         }
+    }
+    __device__ __forceinline__ void fold(int s0) {
         float nM = M;
 #pragma unroll
         for (int b = 0; b < SB; b++) nM = s0 + 4 * b < ns ? fmaxf(nM, st[b].x) : nM;
@@ -274,19 +283,34 @@ __device__ __forceinline__ void merge_spans(const float* __restrict__ part, cons
         M = nM;
     }
     // the four lanes of the quad, in a fixed order
-    float MA = fmaxf(M, lane_xor1(M));
-    MA = fmaxf(MA, lane_xor2(MA));
-    const float f = M == -INFINITY ? 0.0f : dev_exp(M - MA);
-    L *= f;
-    L += lane_xor1(L);
-    L += lane_xor2(L);
+    __device__ __forceinline__ void finish(float (&v)[8]) {
+        float MA = fmaxf(M, lane_xor1(M));
+        MA = fmaxf(MA, lane_xor2(MA));
+        const float f = M == -INFINITY ? 0.0f : dev_exp(M - MA);
+        L *= f;
+        L += lane_xor1(L);
+        L += lane_xor2(L);
+        const float il = 1.0f / L;
 #pragma unroll
-    for (int e = 0; e < 8; e++) {
-        O[e] *= f;
-        O[e] += lane_xor1(O[e]);
-        O[e] += lane_xor2(O[e]);
-        v[e] = O[e] / L;
+        for (int e = 0; e < 8; e++) {
+            O[e] *= f;
+            O[e] += lane_xor1(O[e]);
+            O[e] += lane_xor2(O[e]);
+            v[e] = O[e] * il;
+        }
     }
+};
+
+template <int SB>
+__device__ __forceinline__ void merge_spans(const float* __restrict__ part, int4 mr, int nh, int nkv, int hd, int qm,
+                                            int k0, int phase, float (&v)[8]) {
+    SpanMerge<SB> sm;
+    sm.init(part, mr, nh, nkv, hd, qm, k0);
+    for (int s0 = phase; s0 < sm.ns; s0 += 4 * SB) {
+        sm.load(s0);
+        sm.fold(s0);
+    }
+    sm.finish(v);
 }
 
 // Pieces of g * x[rows_src[row]] (g, rows_src optional). One wave per
@@ -422,6 +446,37 @@ __global__ __launch_bounds__(64 * WMAX) void k_gemv(const GemvArgs a) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, W = blockDim.x >> 6;
     const int tile0 = blockIdx.x * NT;
     const int pass0 = blockIdx.z * PG;
+    // AM: the merge records of the (at most four) rows (uniform loads; the
+    // records sit in a 64-word padded region) and the first span batch of the
+    // thread's first merge item are requested before anything else, so that
+    // the merge waits on nothing issued later (vector loads retire in order).
+    // Rows past m take the last row's partials (valid addresses, discarded).
+    constexpr int AMSB = 5;
+    SpanMerge<AMSB> sm;
+    int4 amr0, amr1, amr2, amr3;
+    const int am_per_row = AM ? a.anh * a.ahd / 2 : 1;  // items per row: 8 inputs x 4 phases
+    auto am_item = [&](int item, int& row, int& k0, int& phase) {
+        row = item / am_per_row;
+        const int rem = item % am_per_row;
+        k0 = (rem >> 2) * 8;
+        phase = rem & 3;
+    };
+    auto am_start = [&](int item) {
+        int row, k0, phase;
+        am_item(item, row, k0, phase);
+        const int r = min(row, a.m - 1);
+        const int4 mr = r == 0 ? amr0 : r == 1 ? amr1 : r == 2 ? amr2 : amr3;
+        sm.init(a.apart, mr, a.anh, a.ankv, a.ahd, a.aqm, k0);
+        sm.load(phase);
+    };
+    if constexpr (AM) {
+        const int4* mrp = (const int4*)a.amrec;
+        amr0 = mrp[0];
+        amr1 = mrp[1];
+        amr2 = mrp[2];
+        amr3 = mrp[3];
+        am_start(threadIdx.x);
+    }
     const int np = min(PG, a.p_total - pass0);
     const int KB = a.KB, KC = KB >> 2;
     const int c0 = wave * KC / W, c1 = (wave + 1) * KC / W;
@@ -600,18 +655,25 @@ __global__ __launch_bounds__(64 * WMAX) void k_gemv(const GemvArgs a) {
                 for (int j = 0; j < 4; j++)
                     wm[u][t][j] = ((const bf16x8*)a.W)[((size_t)(tile0 + t) * KB + cc * 4 + j) * 64 + lane];
         }
-        const int K = a.anh * a.ahd, per_row = K / 2;  // items per row: K / 8 input groups x 4 phases
+        const int K = a.anh * a.ahd;
         // zero slots: rows past m, inputs past K
         for (int i = threadIdx.x; i < KB * 64; i += blockDim.x) {
             const int l = i & 63, row = (l & 15) >> 2, kin = (i >> 6) * 32 + (l >> 4) * 8;
             if (row >= a.m || kin >= K) xm[i] = (u16x8){0, 0, 0, 0, 0, 0, 0, 0};
         }
-        for (int i0 = 0; i0 < a.m * per_row; i0 += blockDim.x) {
-            const int item = i0 + threadIdx.x, row = item / per_row, rem = item % per_row;
-            const int k0 = (rem >> 2) * 8, phase = rem & 3;
-            if (row < a.m) {  // whole quads: per_row and blockDim are multiples of 4
-                float v[8];
-                merge_spans<5>(a.apart, a.amrec, a.anh, a.ankv, a.ahd, a.aqm, row, k0, phase, v);
+        // whole quads take part in every step (am_per_row and blockDim are multiples of 4)
+        for (int i0 = 0; i0 < a.m * am_per_row; i0 += blockDim.x) {
+            if (i0 > 0) am_start(i0 + threadIdx.x);
+            int row, k0, phase;
+            am_item(i0 + threadIdx.x, row, k0, phase);
+            sm.fold(phase);
+            for (int s0 = phase + 4 * AMSB; s0 < sm.ns; s0 += 4 * AMSB) {
+                sm.load(s0);
+                sm.fold(s0);
+            }
+            float v[8];
+            sm.finish(v);
+            if (row < a.m) {
                 u16x8 o;
 #pragma unroll
                 for (int e = 0; e < 8; e++) o[e] = (uint16_t)bf16_piece(v[e], phase);
@@ -1437,7 +1499,7 @@ __global__ __launch_bounds__(256) void k_attn(AttnArgs a) {
         if (q < Q) {
             pr[q][o] = e;
             if (o == 0) {
-                float* dst = a.part + (((size_t)wi * a.nkv + h) * QM + q) * (HD + 2);
+                float* dst = a.part + (((size_t)wi * a.nkv + h) * QM + q) * (HD + 4);
                 dst[0] = mx;
                 dst[1] = sum;
             }
@@ -1457,7 +1519,7 @@ __global__ __launch_bounds__(256) void k_attn(AttnArgs a) {
             acc = fmaf(w.z, vs[4 * o4 + 2][d], acc);
             acc = fmaf(w.w, vs[4 * o4 + 3][d], acc);
         }
-        a.part[(((size_t)wi * a.nkv + h) * QM + q) * (HD + 2) + 2 + d] = acc;
+        a.part[(((size_t)wi * a.nkv + h) * QM + q) * (HD + 4) + 4 + d] = acc;
     }
 }
 
@@ -1471,7 +1533,8 @@ __global__ __launch_bounds__(64) void k_merge_pieces(AttnArgs a, int m, void* __
     const int c = lane & 15, row = pass * 4 + (c >> 2), piece = c & 3;
     const int k0 = kb * 32 + (lane >> 4) * 8;
     float v[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-    if (row < m && k0 < a.nh * HD) merge_spans<8>(a.part, a.mrec, a.nh, a.nkv, HD, QM, row, k0, piece, v);
+    if (row < m && k0 < a.nh * HD)
+        merge_spans<8>(a.part, *(const int4*)(a.mrec + (size_t)row * 4), a.nh, a.nkv, HD, QM, k0, piece, v);
     write_pieces<CK>(v, kb, pass, passes, row, piece, lane, out, xs);
 }
 
