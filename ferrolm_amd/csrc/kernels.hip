@@ -427,7 +427,7 @@ __global__ __launch_bounds__(64 * WMAX) void k_gemv(const GemvArgs a) {
     // chunks loaded ahead per wave: about 16 B x 4 per lane and tile of weights in
     // flight; with 16 waves (4 per SIMD, 128 VGPRs) half as many, the other waves
     // of the SIMD covering each one's wait
-    constexpr int U = PG == 1 ? (KIND == INT4 ? 4 : NT == 8 ? 1 : 2) / (WMAX == 16 ? 2 : 1) : 1;
+    constexpr int U = PG == 1 ? (KIND == INT4 ? 4 : NT >= 6 ? 1 : 2) / (WMAX == 16 ? 2 : 1) : 1;
     constexpr bool NEED_R = EPI == EPI_QKV || EPI == EPI_SILU || EPI == EPI_ARGMAX;
     constexpr int YS = NT * 16 > 64 ? NT * 16 : 64;  // row stride of the output tile in LDS
     // finished output columns per group (EPI_RESID, EPI_SILU): 16 or 32, a half
@@ -1314,8 +1314,14 @@ static void gemv_kind(hipStream_t st, int epi, const DMat& w, const GemvArgs& a,
                 gemv_pg<KIND, 4, EPI_SILU>(st, w, a, e0, e1);
             break;
         case EPI_ARGMAX:
-            // bf16 lm_head: 128 columns per group when decoding (fewer, fuller workgroups)
+            // bf16 lm_head when decoding: 96 or 128 columns per group (fewer, fuller
+            // workgroups); 96 when the groups then fill the 256 CUs evenly (a
+            // multiple of 256 groups)
             if constexpr (KIND == BF16) {
+                if (a.p_total == 1 && w.n_tiles % 6 == 0 && (w.n_tiles / 6) % 256 == 0) {
+                    gemv_pg<KIND, 6, EPI_ARGMAX>(st, w, a, e0, e1);
+                    break;
+                }
                 if (a.p_total == 1 && w.n_tiles % 8 == 0) {
                     gemv_pg<KIND, 8, EPI_ARGMAX>(st, w, a, e0, e1);
                     break;
@@ -1406,8 +1412,11 @@ __global__ __launch_bounds__(256) void k_attn(AttnArgs a) {
         const float* kp = src_of(p, 0);
         ku[it] = *(const float4*)(kp + d);
         kw[it] = *(const float4*)(kp + d + HALF);
-        kcs[it] = *(const float4*)(a.cos_t + (size_t)p * HALF + d);
-        ksn[it] = *(const float4*)(a.sin_t + (size_t)p * HALF + d);
+        // only new keys are rotated: cached positions all read the chunk's first
+        // position (one cache line instead of a table row each)
+        const int pr = max(p, cpos0);
+        kcs[it] = *(const float4*)(a.cos_t + (size_t)pr * HALF + d);
+        ksn[it] = *(const float4*)(a.sin_t + (size_t)pr * HALF + d);
     }
 #pragma unroll
     for (int it = 0; it < VIT; it++) {
