@@ -90,6 +90,17 @@ __device__ __forceinline__ float reduce_rows(float v) {
     }
     return v;
 }
+// out[j] = v of lane (l % 16) + 16 j, for every lane l.
+__device__ __forceinline__ void gather_rows(float v, float (&out)[4]) {
+    const uint32_t x = __float_as_uint(v);
+    const auto a = __builtin_amdgcn_permlane16_swap(x, x, false, false);  // rows (2r, 2r+1) of each half
+    const auto e = __builtin_amdgcn_permlane32_swap(a[0], a[0], false, false);
+    const auto o = __builtin_amdgcn_permlane32_swap(a[1], a[1], false, false);
+    out[0] = __uint_as_float(e[0]);
+    out[1] = __uint_as_float(o[0]);
+    out[2] = __uint_as_float(e[1]);
+    out[3] = __uint_as_float(o[1]);
+}
 // Max / sum over aligned groups of N lanes (4, 8, 16, 32 or 64).
 template <int N, bool MAX>
 __device__ __forceinline__ float group_reduce(float v) {
@@ -557,7 +568,7 @@ __global__ __launch_bounds__(64 * WMAX) void k_gemv(const GemvArgs a) {
         float sx[UU][4][PG];
         u32x4 wq[UU][NT][2];
         bf16x8 wb[UU][NT][4];
-        float4 sv[UU][NT];
+        float sv[UU][NT];  // group scale of (row lane % 16, k-block lane / 16) of the chunk
 #pragma unroll
         for (int u = 0; u < UU; u++) {
             const int cc = c + u, kb = cc * 4;
@@ -586,7 +597,7 @@ __global__ __launch_bounds__(64 * WMAX) void k_gemv(const GemvArgs a) {
 #pragma unroll
                     for (int j = 0; j < 4; j++) wb[u][t][j] = ((const bf16x8*)a.W)[(tile * KB + kb + j) * 64 + lane];
                 }
-                if (Q) sv[u][t] = ((const float4*)a.S)[(tile * KC + cc) * 16 + (lane & 15)];
+                if (Q) sv[u][t] = a.S[(tile * KC + cc) * 64 + (lane & 15) * 4 + (lane >> 4)];
             }
         }
         // keep the scheduler from sinking loads of the batch below its first MFMA
@@ -596,7 +607,10 @@ __global__ __launch_bounds__(64 * WMAX) void k_gemv(const GemvArgs a) {
 #pragma unroll
             for (int t = 0; t < NT; t++) {
                 if (Q) {
-                    const float svj[4] = {sv[u][t].x, sv[u][t].y, sv[u][t].z, sv[u][t].w};
+                    // each lane's row scales for the chunk's four k-blocks, gathered from
+                    // the four 16-lane rows (one scale per lane loaded: 256 B a wave)
+                    float svj[4];
+                    gather_rows(sv[u][t], svj);
                     long bq[4];
                     if (KIND == INT4) {
 #pragma unroll
@@ -1363,13 +1377,20 @@ void launch_gemv(hipStream_t st, int epi, const DMat& w, const GemvArgs& a, hipE
 // writes per query the span's max score, sum of exponentials and weighted
 // values; k_merge_pieces combines the spans.
 // ---------------------------------------------------------------------------
+// queries of a work item from which attention runs on MFMA (measured: the VALU
+// loops are faster for the 3 to 5 queries of decode steps, MFMA for the 20 of
+// an 8B GQA verify)
+constexpr int kAttnMfmaQueries = 16;
+
 template <int HD, int P, int QM>
 __global__ __launch_bounds__(256) void k_attn(AttnArgs a) {
     constexpr int HALF = HD / 2;
-    __shared__ __align__(16) float ks[P][HD + 4];  // rows 16-byte aligned; lanes' 16-byte reads hit distinct banks
-    __shared__ __align__(16) float vs[P][HD];
-    __shared__ __align__(16) float qs[QM][HD];
-    __shared__ __align__(16) float pr[QM][P];
+    // rows padded by 4 floats (16-byte aligned): lanes reading one column of
+    // consecutive rows (the MFMA operands) hit distinct banks
+    __shared__ __align__(16) float ks[P][HD + 4];
+    __shared__ __align__(16) float vs[P][HD + 4];
+    __shared__ __align__(16) float qs[QM][HD + 4];
+    __shared__ __align__(16) float pr[QM][P + 4];
     __shared__ int lim[QM];
 
     static_assert(P <= 64 && P % 16 == 0 && 64 % P == 0, "a span covers at most four cache blocks");
@@ -1482,13 +1503,37 @@ __global__ __launch_bounds__(256) void k_attn(AttnArgs a) {
             a.vc[at] = vs[o][d];
         }
     }
+    // From kAttnMfmaQueries queries on, the scores and the weighted values run on f32 MFMA
+    // (v_mfma_f32_16x16x4f32; A[i][k] in lane i + 16k, B[k][j] in lane j + 16k,
+    // D[4(l/16) + r][l%16] in register r of lane l) over 16 x 16 tiles, with
+    // operands from LDS; fewer queries take the VALU loops. Rows of qs and pr
+    // past Q hold stale values: they only reach output rows that are dropped.
+    const bool mf = Q >= kAttnMfmaQueries;
+    const int mtu = (Q + 15) >> 4;
+    if (mf) {
+        // scores, scaled, into pr
+        constexpr int NTP = P / 16;
+        for (int ti = wave; ti < mtu * NTP; ti += 4) {
+            const int mt = ti / NTP, nt = ti % NTP, kk = lane >> 4;
+            const float* qa = &qs[mt * 16 + (lane & 15)][kk];
+            const float* kb = &ks[nt * 16 + (lane & 15)][kk];
+            f32x4 c = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int d0 = 0; d0 < HD; d0 += 4) c = __builtin_amdgcn_mfma_f32_16x16x4f32(qa[d0], kb[d0], c, 0, 0, 0);
+#pragma unroll
+            for (int r = 0; r < 4; r++) pr[mt * 16 + 4 * kk + r][nt * 16 + (lane & 15)] = c[r] * a.scale;
+        }
+        __syncthreads();
+    }
     // Scores and their softmax statistics in one pass: item i = q * P + o, so
     // each wave holds whole queries (one per P lanes) and reduces them in
     // registers.
     for (int base = wave * 64; base < Q * P; base += 256) {
         const int i = base + lane, q = i / P, o = i % P, p = p0 + o;
         float sc = -INFINITY;
-        if (q < Q && p < p1 && p <= lim[q]) {
+        if (q < Q && p < p1 && p <= lim[q] && mf) {
+            sc = pr[q][o];
+        } else if (q < Q && p < p1 && p <= lim[q]) {
             const float4* kr = (const float4*)&ks[o][0];
             const float4* qr = (const float4*)&qs[q][0];
             float acc = 0.0f;
@@ -1515,6 +1560,25 @@ __global__ __launch_bounds__(256) void k_attn(AttnArgs a) {
         }
     }
     __syncthreads();
+    if (mf) {
+        // weighted values: O = P V
+        constexpr int NTD = HD / 16;
+        for (int ti = wave; ti < mtu * NTD; ti += 4) {
+            const int mt = ti / NTD, nd = ti % NTD, kk = lane >> 4;
+            const float* pa = &pr[mt * 16 + (lane & 15)][kk];
+            const float* vb = &vs[kk][nd * 16 + (lane & 15)];
+            f32x4 c = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int k0 = 0; k0 < P; k0 += 4)
+                c = __builtin_amdgcn_mfma_f32_16x16x4f32(pa[k0], vb[k0 * (HD + 4)], c, 0, 0, 0);
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const int q = mt * 16 + 4 * kk + r;
+                if (q < Q) a.part[(((size_t)wi * a.nkv + h) * QM + q) * (HD + 4) + 4 + nd * 16 + (lane & 15)] = c[r];
+            }
+        }
+        return;
+    }
     // weighted values
     for (int i = tid; i < Q * HD; i += 256) {
         const int q = i / HD, d = i % HD;
