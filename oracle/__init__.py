@@ -85,6 +85,8 @@ def lib():
             "or_rms_norm": (None, [f32p, f32p, C.c_int32, C.c_int32, C.c_float, f32p]),
             "or_silu_mul": (None, [f32p, C.c_int32, C.c_int32, f32p]),
             "or_argmax": (C.c_uint32, [f32p, C.c_int32]),
+            "or_distribution": (C.c_int32, [f32p, C.c_int32, C.c_float, C.c_float, C.c_int32, u32p, f32p]),
+            "or_draw": (C.c_uint32, [u32p, f32p, C.c_int32, C.POINTER(C.c_uint64)]),
             "or_set_threads": (None, [C.c_int32]),
             "or_quantize": (C.c_int32, [C.c_int32, C.c_int32, C.c_int32, f32p, f32p, u8p, f32p]),
             "or_dequantize": (None, [C.c_int32, C.c_int32, C.c_int32, u8p, f32p, f32p]),
@@ -296,3 +298,156 @@ def exp(x: float) -> float:
 def argmax(v: np.ndarray) -> int:
     v = np.ascontiguousarray(v, np.float32)
     return int(lib().or_argmax(ptr(v, f32p), len(v)))
+
+
+# ---------------------------------------------------------------------------
+# Sampling (src/sampler.rs:52-103) and the engine's sampling branch
+# (src/engine.rs:575-610, 658-717).
+# ---------------------------------------------------------------------------
+class Rng:
+    """The reference's Rng (src/rng.rs:5-36): xorshift64* seeded by
+    seed * 0x9E3779B97F4A7C15 | 1."""
+
+    def __init__(self, seed: int = 0, state: int | None = None):
+        self.s = C.c_uint64(lib().or_rng_new(seed) if state is None else state)
+
+    @property
+    def state(self) -> int:
+        return self.s.value
+
+    def uniform(self) -> float:
+        return lib().or_rng_uniform(C.byref(self.s))
+
+
+def distribution(logits, temperature: float, top_p: float, top_k: int):
+    """sampler::distribution: (tokens, probabilities) in the reference's order."""
+    logits = np.ascontiguousarray(logits, dtype=np.float32)
+    v = len(logits)
+    tok = np.zeros(v, np.uint32)
+    pr = np.zeros(v, np.float32)
+    n = lib().or_distribution(ptr(logits, f32p), v, temperature, top_p, top_k, ptr(tok, u32p), ptr(pr, f32p))
+    return tok[:n].copy(), pr[:n].copy()
+
+
+def draw(tok, pr, rng: Rng) -> int:
+    """sampler::draw over (tok, pr) in the given order."""
+    tok = np.ascontiguousarray(tok, dtype=np.uint32)
+    pr = np.ascontiguousarray(pr, dtype=np.float32)
+    return int(lib().or_draw(ptr(tok, u32p), ptr(pr, f32p), len(tok), C.byref(rng.s)))
+
+
+def sample(logits, params, rng: Rng) -> int:
+    """sampler::sample: params = (temperature, top_p, top_k); greedy when
+    temperature <= 0 (no draw from the generator)."""
+    t, top_p, top_k = params
+    if t <= 0.0:
+        return int(lib().or_argmax(ptr(np.ascontiguousarray(logits, np.float32), f32p), len(logits)))
+    return draw(*distribution(logits, t, top_p, top_k), rng)
+
+
+def _dense(tok, pr, vocab: int):
+    d = np.zeros(vocab, np.float32)
+    d[tok] = pr
+    return d
+
+
+def spec_step_sampled(target: Model, tkv: KvCache, draft: Model, dkv: KvCache, tokens, computed: int,
+                      draft_computed: int, blocks, draft_blocks, k: int, params, rng: Rng):
+    """One speculative step of Engine::propose + Engine::execute for one
+    sequence under `params` = (temperature, top_p, top_k), drawing from
+    `rng` in the reference's order: the k draft draws, then one uniform per
+    verified proposal whose draft probability is positive, then the
+    residual draw (src/engine.rs:575-594) or the bonus draw. Returns
+    (emitted ids, accepted, computed, draft_computed)."""
+    greedy = params[0] <= 0.0
+    vocab = target.cfg.vocab
+    tokens = [int(x) for x in tokens]
+    base = len(tokens)
+    drafts, qd = [], []
+    for r in range(k):
+        if r == 0:
+            tok, pos = tokens[draft_computed:], draft_computed
+        else:
+            tok, pos = [drafts[-1]], base + r - 1
+        lg = draft.forward(dkv, [(tok, pos, draft_blocks, 1)])[0]
+        if greedy:
+            t = int(lib().or_argmax(ptr(lg, f32p), vocab))
+        else:
+            tk, pr = distribution(lg, *params)
+            t = draw(tk, pr, rng)
+            qd.append(_dense(tk, pr, vocab))
+        drafts.append(t)
+    draft_computed = base + k - 1
+    rows = target.forward(tkv, [([tokens[computed]] + drafts, computed, blocks, 2)])
+    new, accepted = [], 0
+    for j, d in enumerate(drafts):
+        lg = rows[j]
+        if greedy:
+            t = int(lib().or_argmax(ptr(lg, f32p), vocab))
+            take = None if t == d else t
+        else:
+            pd = _dense(*distribution(lg, *params), vocab)
+            q = qd[j]
+            px, qx = pd[d], q[d]
+            if qx > 0 and rng.uniform() < float(min(np.float32(px / qx), np.float32(1.0))):
+                take = None
+            else:
+                mask = pd > q
+                if mask.any():
+                    rt = np.nonzero(mask)[0]
+                    take = draw(rt, (pd - q)[mask], rng)
+                else:
+                    rt = np.nonzero(pd > 0)[0]
+                    take = draw(rt, pd[rt], rng)
+        if take is None:
+            new.append(d)
+            accepted += 1
+        else:
+            new.append(int(take))
+            break
+    if accepted == k:
+        new.append(sample(rows[k], params, rng))
+    return new, accepted, base + accepted, min(draft_computed, base + accepted)
+
+
+def generate_sampled(target: Model, draft: Model | None, prompt, max_tokens: int, k: int, params, seed: int,
+                     kv_blocks: int = 256, max_batch_tokens: int = 512):
+    """One request through the engine loop with sampling parameters
+    (src/engine.rs:374-654, ignore_eos): chunked prefill, the first token
+    sampled from the prompt's last row, then speculative steps. Returns
+    (tokens, (proposed, accepted, steps))."""
+    rng = Rng(seed)
+    if draft is None:
+        k = 0
+    bs = 16
+    max_len = min(target.cfg.max_position, kv_blocks * bs)
+    tokens = [int(x) for x in prompt]
+    if not tokens or len(tokens) >= max_len:
+        raise ValueError("prompt does not fit")
+    tkv = target.kv(kv_blocks)
+    dkv = draft.kv(kv_blocks) if draft else None
+    table = list(range(kv_blocks))
+    computed = draft_computed = 0
+    out = []
+    proposed = acc_total = steps = 0
+    while len(out) < max_tokens and len(tokens) < max_len:
+        left = len(tokens) - computed
+        spec = left == 1 and k > 0 and len(tokens) + k < max_len and max_batch_tokens > k
+        if spec:
+            emit, a, computed, draft_computed = spec_step_sampled(target, tkv, draft, dkv, tokens, computed,
+                                                                  draft_computed, table, table, k, params, rng)
+            proposed += k
+            acc_total += a
+            steps += 1
+        else:
+            n = min(left, max_batch_tokens)
+            last = computed + n == len(tokens)
+            lg = target.forward(tkv, [(tokens[computed:computed + n], computed, table, 1 if last else 0)])
+            computed += n
+            emit = [sample(lg[0], params, rng)] if last else []
+        for t in emit:
+            tokens.append(t)
+            out.append(t)
+            if len(out) >= max_tokens or len(tokens) >= max_len:
+                break
+    return np.array(out, np.uint32), (proposed, acc_total, steps)

@@ -146,6 +146,82 @@ uint32_t or_argmax(const float* v, int32_t n) {
     return (uint32_t)best;
 }
 
+/* Sampling (src/sampler.rs:52-103). Keys of f32::total_cmp: the float's bits
+ * mapped so that unsigned order is the total order (NaNs at the ends). */
+static inline uint32_t total_key(float x) {
+    uint32_t b;
+    memcpy(&b, &x, 4);
+    return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+}
+typedef struct {
+    uint32_t t;
+    float v;
+} tok_val;
+/* value descending by total_cmp, then token ascending (src/sampler.rs:58) */
+static int cmp_desc(const void* a, const void* b) {
+    const tok_val *x = (const tok_val*)a, *y = (const tok_val*)b;
+    const uint32_t kx = total_key(x->v), ky = total_key(y->v);
+    if (kx != ky) return kx > ky ? -1 : 1;
+    return x->t < y->t ? -1 : (x->t > y->t);
+}
+
+/* sampler::distribution (src/sampler.rs:54-90): temperature, sort, top-k,
+ * exp(v - max) in f32 summed in f64, normalise in f64 then round to f32;
+ * top-p keeps the shortest prefix whose f32 running sum reaches top_p and
+ * renormalises it by its f32 sum. Returns the pair count. */
+int32_t or_distribution(const float* logits, int32_t vocab, float temperature, float top_p, int32_t top_k,
+                        uint32_t* tok_out, float* p_out) {
+    const float t = temperature > 1e-5f ? temperature : 1e-5f;
+    tok_val* v = (tok_val*)malloc((size_t)vocab * sizeof(tok_val));
+    for (int32_t i = 0; i < vocab; i++) {
+        v[i].t = (uint32_t)i;
+        v[i].v = logits[i] / t;
+    }
+    qsort(v, (size_t)vocab, sizeof(tok_val), cmp_desc);
+    int32_t n = vocab;
+    if (top_k > 0 && top_k < n) n = top_k;
+    const float mx = v[0].v;
+    double sum = 0.0;
+    for (int32_t i = 0; i < n; i++) {
+        v[i].v = expf(v[i].v - mx);
+        sum += (double)v[i].v;
+    }
+    for (int32_t i = 0; i < n; i++) v[i].v = (float)((double)v[i].v / sum);
+    if (top_p < 1.0f) {
+        float acc = 0.0f;
+        int32_t keep = n;
+        for (int32_t i = 0; i < n; i++) {
+            acc += v[i].v;
+            if (acc >= top_p) {
+                keep = i + 1;
+                break;
+            }
+        }
+        n = keep;
+        float s2 = 0.0f;
+        for (int32_t i = 0; i < n; i++) s2 += v[i].v;
+        for (int32_t i = 0; i < n; i++) v[i].v /= s2;
+    }
+    for (int32_t i = 0; i < n; i++) {
+        tok_out[i] = v[i].t;
+        p_out[i] = v[i].v;
+    }
+    free(v);
+    return n;
+}
+
+/* sampler::draw (src/sampler.rs:93-103): u in [0, f32 sum) scanned in order. */
+uint32_t or_draw(const uint32_t* tok, const float* p, int32_t n, uint64_t* rng) {
+    float s = 0.0f;
+    for (int32_t i = 0; i < n; i++) s += p[i];
+    float u = (float)or_rng_uniform(rng) * s;
+    for (int32_t i = 0; i < n; i++) {
+        if (u < p[i]) return tok[i];
+        u -= p[i];
+    }
+    return n > 0 ? tok[n - 1] : 0;
+}
+
 /* ------------------------------------------------------------------ */
 /* Matrices                                                            */
 /* ------------------------------------------------------------------ */

@@ -81,6 +81,12 @@ float or_exp(float x);
 float or_dot(const float* a, const float* b, int32_t n);
 void or_rms_norm(const float* x, const float* w, int32_t dim, int32_t rows, float eps, float* out);
 void or_silu_mul(const float* gate_up, int32_t inter, int32_t rows, float* out);
+/* sampler::distribution (src/sampler.rs:54-90): the (token, probability)
+ * pairs in the reference's order; returns their count (tok/p hold vocab). */
+int32_t or_distribution(const float* logits, int32_t vocab, float temperature, float top_p, int32_t top_k,
+                        uint32_t* tok_out, float* p_out);
+/* sampler::draw (src/sampler.rs:93-103) */
+uint32_t or_draw(const uint32_t* tok, const float* p, int32_t n, uint64_t* rng);
 uint32_t or_argmax(const float* v, int32_t n);
 void or_set_threads(int32_t n);
 

@@ -289,3 +289,88 @@ def test_spec_step_restarts_from_a_state():
         out, _, comp, dcomp = oracle.spec_step(m, tkv, d, dkv, tokens, comp, dcomp, tb, db, 3)
         tokens += [int(x) for x in out]
     assert tokens[len(p):len(p) + 12] == list(want)
+
+
+def test_sampler_filters_and_samples_in_proportion():
+    """src/sampler.rs:107-129: temperature 1, top_k 3, top_p 0.95 over
+    [2, 1, 0, -1] keeps tokens 0..2; 20000 draws from Rng(3) land within
+    0.015 of each probability and never on the filtered token."""
+    tok, pr = oracle.distribution(np.array([2.0, 1.0, 0.0, -1.0], np.float32), 1.0, 0.95, 3)
+    assert tok.tolist() == [0, 1, 2]
+    # closed form: softmax of [2, 1, 0], which already reaches the top_p mass
+    e = np.exp(np.array([2.0, 1.0, 0.0]))
+    assert np.allclose(pr, e / e.sum(), rtol=1e-6)
+    rng = oracle.Rng(3)
+    counts = np.zeros(4, int)
+    for _ in range(20000):
+        counts[oracle.draw(tok, pr, rng)] += 1
+    assert np.all(np.abs(counts[:3] / 20000 - pr) < 0.015)
+    assert counts[3] == 0
+
+
+def test_distribution_orders_ties_by_token_and_cuts_top_p():
+    # equal values keep token order; top_p stops at the first running sum that
+    # reaches it (src/sampler.rs:58, 74-82); temperature divides first
+    lg = np.array([0.0, 3.0, 3.0, 1.0, 3.0], np.float32)
+    tok, pr = oracle.distribution(lg, 0.5, 1.0, 0)
+    assert tok.tolist() == [1, 2, 4, 3, 0]
+    tok2, pr2 = oracle.distribution(lg, 0.5, 0.6, 0)
+    assert tok2.tolist() == [1, 2] and abs(float(pr2.sum()) - 1.0) < 1e-6
+    tok3, _ = oracle.distribution(lg, 0.5, 1.0, 2)
+    assert tok3.tolist() == [1, 2]
+
+
+def _reference_prompts(n, seed):
+    """tests/engine.rs:19-27: lengths between(1, 150), ids between(3, 511)."""
+    rng = ctypes.c_uint64(oracle.lib().or_rng_new(seed))
+    nxt = lambda: oracle.lib().or_rng_next(ctypes.byref(rng))
+    out = []
+    for _ in range(n):
+        ln = 1 + nxt() % 150
+        out.append([3 + nxt() % 509 for _ in range(ln)])
+    return out
+
+
+def exact_two_token_distribution(m, prompt, params):
+    """tests/engine.rs:163-194: the probability of each two-token continuation."""
+    def nxt(tokens):
+        kv = m.kv(16)
+        lg = m.forward(kv, [(tokens, 0, list(range(16)), 1)])[0]
+        return zip(*oracle.distribution(lg, *params))
+    out = []
+    for t1, p1 in nxt(prompt):
+        for t2, p2 in nxt(list(prompt) + [int(t1)]):
+            out.append(((int(t1), int(t2)), float(p1) * float(p2)))
+    return out
+
+
+def test_speculative_sampling_keeps_the_target_distribution():
+    """tests/engine.rs:196-243 on the oracle's engine loop: the first two
+    sampled tokens after a fixed prompt, 4000 requests (seeds 1..4000), with
+    and without a one-layer draft (k=3), against the exact distribution by a
+    chi-square test (16 outcomes, 0.1% critical value 37.7)."""
+    hm = load_model(GOLDEN / "llama-gqa")
+    m = oracle.Model(hm)
+    prompt = _reference_prompts(1, 5)[0]
+    params = (1.0, 1.0, 4)
+    exact = exact_two_token_distribution(m, prompt, params)
+    assert len(exact) == 16
+    n = 4000
+
+    def chi2(draft):
+        seen = {}
+        st = [0, 0]
+        for i in range(n):
+            toks, (prop, acc, _) = oracle.generate_sampled(m, draft, prompt, 2, 3, params, seed=i + 1, kv_blocks=600)
+            key = tuple(int(x) for x in toks)
+            seen[key] = seen.get(key, 0) + 1
+            st[0] += prop
+            st[1] += acc
+        assert set(seen) <= {s for s, _ in exact}, "impossible continuation sampled"
+        return sum((seen.get(s, 0) - p * n) ** 2 / (p * n) for s, p in exact), st
+
+    plain, _ = chi2(None)
+    spec, (proposed, accepted) = chi2(m.truncated(1))
+    assert 0 < accepted < proposed
+    assert plain < 37.7, plain
+    assert spec < 37.7, spec
