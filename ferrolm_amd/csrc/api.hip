@@ -77,6 +77,8 @@ struct fg_ctx {
     hipStream_t stream = nullptr;
     void* ws = nullptr;
     size_t ws_cap = 0;
+    void* sbuf = nullptr;  // sampling: the distributions of a step's rows
+    size_t sbuf_cap = 0;
     void* dmeta = nullptr;
     size_t dmeta_cap = 0;
     void* hmeta = nullptr;
@@ -768,6 +770,7 @@ void fg_ctx_destroy(fg_ctx* c) {
     (void)hipStreamSynchronize(c->stream);
     drop_graphs(c);
     if (c->ws) (void)hipFree(c->ws);
+    if (c->sbuf) (void)hipFree(c->sbuf);
     if (c->dmeta) (void)hipFree(c->dmeta);
     if (c->hmeta) (void)hipHostFree(c->hmeta);
     for (auto& e : c->ev)
@@ -959,12 +962,36 @@ int fg_forward(fg_ctx* ctx, const fg_model* m, fg_kv* kv, const fg_chunk* chunks
     return 0;
 }
 
-int fg_spec_step(fg_ctx* ctx, const fg_model* target, fg_kv* tkv, const fg_model* draft, fg_kv* dkv,
-                 const fg_spec_seq* seqs, int32_t n_seqs, int32_t k, uint32_t* out_tokens, int32_t* out_count,
-                 int32_t* out_accepted) {
+// Distributions of `rows` rows carved from the context's sampling buffer
+// starting at row `first` (the buffer holds `total` rows).
+static SampleRows sample_rows(void* buf, int total, int first) {
+    const size_t cap = kSampleCap;
+    uint8_t* b = (uint8_t*)buf;
+    SampleRows r;
+    r.tok = (uint32_t*)b + (size_t)first * cap;
+    r.pr = (float*)(b + (size_t)total * cap * 4) + (size_t)first * cap;
+    r.tok_id = (uint32_t*)(b + (size_t)total * cap * 8) + (size_t)first * cap;
+    r.pr_id = (float*)(b + (size_t)total * cap * 12) + (size_t)first * cap;
+    r.n = (int*)(b + (size_t)total * cap * 16) + first;
+    return r;
+}
+static size_t sample_bytes(int total) { return (size_t)total * kSampleCap * 16 + (size_t)total * 4; }
+static_assert(sizeof(SampleParams) == sizeof(fg_sampling), "fg_sampling is copied to the device as SampleParams");
+
+static int check_sampling(const fg_sampling* p, int n) {
+    for (int i = 0; i < n; i++)
+        if (p[i].temperature > 0.0f && (p[i].top_k < 1 || p[i].top_k > kSampleCap))
+            return fail(FG_E_ARG, "device sampling needs 1 <= top_k <= 1024 (0, no limit, is not supported)");
+    return 0;
+}
+
+static int spec_step(fg_ctx* ctx, const fg_model* target, fg_kv* tkv, const fg_model* draft, fg_kv* dkv,
+                     const fg_spec_seq* seqs, int32_t n_seqs, int32_t k, const fg_sampling* params, uint64_t* rng,
+                     uint32_t* out_tokens, int32_t* out_count, int32_t* out_accepted) {
     if (!ctx || !target || !tkv || !draft || !dkv || !seqs || n_seqs <= 0 || k <= 0 || !out_tokens || !out_count ||
-        !out_accepted)
+        !out_accepted || (params && !rng))
         return fail(FG_E_ARG, "bad argument");
+    const bool sampling = params != nullptr;
     if (draft->cfg.vocab != target->cfg.vocab) return fail(FG_E_SHAPE, "draft and target must share a vocabulary");
     int rc;
     if ((rc = check_model_kv(target, tkv)) || (rc = check_model_kv(draft, dkv))) return rc;
@@ -999,6 +1026,13 @@ int fg_spec_step(fg_ctx* ctx, const fg_model* target, fg_kv* tkv, const fg_model
     }
     const size_t o_vtok = words;
     words += (size_t)n_seqs * K1 + 64;
+    // sampling: parameters and generator states (uploaded with the plans; the
+    // states come back with the outputs)
+    words = (words + 15) / 16 * 16;  // 64-byte aligned parameters and states
+    const size_t o_prm = words;
+    if (sampling) words += (size_t)n_seqs * 4 + 64;
+    const size_t o_rng = words;
+    if (sampling) words += (size_t)n_seqs * 2 + 64;
     const size_t o_out = words;
     words += (size_t)n_seqs * K1 + 64;
     const size_t o_cnt = words;
@@ -1016,14 +1050,23 @@ int fg_spec_step(fg_ctx* ctx, const fg_model* target, fg_kv* tkv, const fg_model
         hv[s * K1] = seqs[s].tail[seqs[s].n_tail - 1];
         for (int j = 1; j < K1; j++) hv[s * K1 + j] = 0;
     }
+    if (sampling) {
+        memcpy(h + o_prm, params, (size_t)n_seqs * sizeof(SampleParams));
+        memcpy(h + o_rng, rng, (size_t)n_seqs * 8);
+    }
     HIPCHK(hipMemcpyAsync(ctx->dmeta, ctx->hmeta, o_out * 4, hipMemcpyHostToDevice, ctx->stream));
     size_t need = 0;
     Work w{};
     const fg_model* models[2] = {draft, target};
     for (int r = 0; r <= k; r++) need = std::max(need, layout_work(models[r == k], plans[r], w, nullptr));
     if ((rc = ensure(&ctx->ws, &ctx->ws_cap, need, ctx->stream, false))) return rc;
+    // sampling rows: the target's n_seqs*(k+1) verify rows, then k draft rounds of n_seqs
+    const int srows = n_seqs * K1 + k * n_seqs;
+    if (sampling && (rc = ensure(&ctx->sbuf, &ctx->sbuf_cap, sample_bytes(srows), ctx->stream, false))) return rc;
     int32_t* dm = (int32_t*)ctx->dmeta;
     uint32_t* vtok = (uint32_t*)(dm + o_vtok);
+    const SampleParams* dprm = (const SampleParams*)(dm + o_prm);
+    uint64_t* drng = (uint64_t*)(dm + o_rng);
     // The two phases as launch sequences (captured into graphs when enabled).
     auto draft_phase = [&]() -> int {
         for (int r = 0; r < k; r++) {
@@ -1031,20 +1074,34 @@ int fg_spec_step(fg_ctx* ctx, const fg_model* target, fg_kv* tkv, const fg_model
             const int32_t* meta = dm + base[r];
             const uint32_t* tok = r == 0 ? (const uint32_t*)(meta + plans[r].o_tok) : vtok + r;
             const int stride = r == 0 ? 1 : K1;
-            // the draft's greedy proposal d_{r+1} goes to verify row s, column r+1
-            int e = run_forward(ctx, draft, dkv, plans[r], meta, tok, stride, w, nullptr, (uint32_t*)(dm + o_am),
-                                vtok, K1, r + 1, nullptr);
+            // the draft's proposal d_{r+1} goes to verify row s, column r+1: the
+            // greedy argmax, replaced by a draw for sampled sequences
+            int e = run_forward(ctx, draft, dkv, plans[r], meta, tok, stride, w, sampling ? w.logits : nullptr,
+                                (uint32_t*)(dm + o_am), vtok, K1, r + 1, nullptr);
             if (e) return e;
+            if (sampling) {
+                SampleRows q = sample_rows(ctx->sbuf, srows, n_seqs * K1 + r * n_seqs);
+                launch_dist(ctx->stream, w.logits, n_seqs, draft->cfg.vocab, 1, dprm, q);
+                launch_draw(ctx->stream, n_seqs, dprm, q, drng, vtok, K1, r + 1);
+            }
         }
         return 0;
     };
     auto verify_phase = [&]() -> int {
         layout_work(target, plans[k], w, ctx->ws);
-        int e = run_forward(ctx, target, tkv, plans[k], dm + base[k], vtok, 1, w, nullptr, (uint32_t*)(dm + o_am),
-                            nullptr, 0, 0, nullptr);
+        int e = run_forward(ctx, target, tkv, plans[k], dm + base[k], vtok, 1, w, sampling ? w.logits : nullptr,
+                            (uint32_t*)(dm + o_am), nullptr, 0, 0, nullptr);
         if (e) return e;
-        launch_accept(ctx->stream, (const uint32_t*)(dm + o_am), vtok, n_seqs, k, (uint32_t*)(dm + o_out),
-                      dm + o_cnt, dm + o_acc);
+        if (sampling) {
+            SampleRows p = sample_rows(ctx->sbuf, srows, 0);
+            launch_dist(ctx->stream, w.logits, n_seqs * K1, target->cfg.vocab, K1, dprm, p);
+            SampleRows q = sample_rows(ctx->sbuf, srows, n_seqs * K1);
+            launch_accept_sampled(ctx->stream, n_seqs, k, dprm, vtok, (const uint32_t*)(dm + o_am), p, q, drng,
+                                  (uint32_t*)(dm + o_out), dm + o_cnt, dm + o_acc);
+        } else {
+            launch_accept(ctx->stream, (const uint32_t*)(dm + o_am), vtok, n_seqs, k, (uint32_t*)(dm + o_out),
+                          dm + o_cnt, dm + o_acc);
+        }
         return 0;
     };
     bool use_graph = ctx->graphs && !ctx->prof;
@@ -1054,7 +1111,8 @@ int fg_spec_step(fg_ctx* ctx, const fg_model* target, fg_kv* tkv, const fg_model
         // workspace and metadata allocations, and each plan's shapes
         std::vector<int64_t> sig = {n_seqs, k, (int64_t)target->serial, (int64_t)draft->serial,
                                     (int64_t)tkv->serial, (int64_t)dkv->serial, (int64_t)(uintptr_t)ctx->ws,
-                                    (int64_t)ctx->ws_cap, (int64_t)(uintptr_t)ctx->dmeta, (int64_t)ctx->dmeta_cap};
+                                    (int64_t)ctx->ws_cap, (int64_t)(uintptr_t)ctx->dmeta, (int64_t)ctx->dmeta_cap,
+                                    (int64_t)sampling, (int64_t)(uintptr_t)ctx->sbuf, (int64_t)ctx->sbuf_cap};
         for (int r = 0; r <= k; r++) {
             const Plan& P = plans[r];
             for (int64_t v : {(int64_t)P.t, (int64_t)P.S, (int64_t)P.Wc, (int64_t)P.words}) sig.push_back(v);
@@ -1110,8 +1168,9 @@ int fg_spec_step(fg_ctx* ctx, const fg_model* target, fg_kv* tkv, const fg_model
         return rc;
     HIPCHK(hipGetLastError());
     HIPCHK(hipEventRecord(ctx->ev[2], ctx->stream));
-    HIPCHK(hipMemcpyAsync(h + o_out, dm + o_out, (words - o_out) * 4, hipMemcpyDeviceToHost, ctx->stream));
+    HIPCHK(hipMemcpyAsync(h + o_rng, dm + o_rng, (words - o_rng) * 4, hipMemcpyDeviceToHost, ctx->stream));
     HIPCHK(hipStreamSynchronize(ctx->stream));
+    if (sampling) memcpy(rng, h + o_rng, (size_t)n_seqs * 8);
     memcpy(out_tokens, h + o_out, (size_t)n_seqs * K1 * 4);
     memcpy(out_count, h + o_cnt, (size_t)n_seqs * 4);
     memcpy(out_accepted, h + o_acc, (size_t)n_seqs * 4);
@@ -1122,6 +1181,77 @@ int fg_spec_step(fg_ctx* ctx, const fg_model* target, fg_kv* tkv, const fg_model
     ctx->last_us[1] = b * 1000.0f;
     ctx->last_us[2] = (a + b) * 1000.0f;
     return 0;
+}
+
+int fg_forward_sampled(fg_ctx* ctx, const fg_model* m, fg_kv* kv, const fg_chunk* chunks, int32_t n_chunks,
+                       const fg_sampling* params, uint64_t* rng, uint32_t* tokens_out, int32_t* rows_out) {
+    if (!ctx || !m || !kv || (!chunks && n_chunks > 0) || n_chunks < 0 || !tokens_out)
+        return fail(FG_E_ARG, "null argument");
+    int rc = check_model_kv(m, kv);
+    if (rc) return rc;
+    HIPCHK(hipSetDevice(ctx->device));
+    std::vector<ChunkIn> in(n_chunks);
+    for (int i = 0; i < n_chunks; i++) {
+        if (chunks[i].n > 0 && !chunks[i].tokens) return fail(FG_E_ARG, "chunk without tokens");
+        in[i] = ChunkIn{chunks[i].tokens, chunks[i].n, chunks[i].pos, chunks[i].blocks, chunks[i].n_blocks,
+                        chunks[i].logits};
+    }
+    Plan P;
+    if ((rc = build_plan(m->cfg, *kv, m->max_pos, in.data(), n_chunks, P))) return rc;
+    if (rows_out) *rows_out = P.S;
+    if (P.t == 0) return 0;
+    if (P.S > 0 && (!params || !rng)) return fail(FG_E_ARG, "sampling parameters and generator states required");
+    if (P.S > 0 && (rc = check_sampling(params, P.S))) return rc;
+    // the plan, then the selected rows' parameters and generator states
+    const size_t o_prm = P.words, o_rng = o_prm + (size_t)P.S * 4 + 64, words = o_rng + (size_t)P.S * 2 + 64;
+    if ((rc = ensure(&ctx->hmeta, &ctx->hmeta_cap, words * 4, ctx->stream, true))) return rc;
+    if ((rc = ensure(&ctx->dmeta, &ctx->dmeta_cap, words * 4, ctx->stream, false))) return rc;
+    int32_t* h = (int32_t*)ctx->hmeta;
+    pack_plan(P, h);
+    if (P.S > 0) {
+        memcpy(h + o_prm, params, (size_t)P.S * sizeof(SampleParams));
+        memcpy(h + o_rng, rng, (size_t)P.S * 8);
+    }
+    HIPCHK(hipMemcpyAsync(ctx->dmeta, ctx->hmeta, words * 4, hipMemcpyHostToDevice, ctx->stream));
+    Work w{};
+    const size_t need = layout_work(m, P, w, nullptr);
+    if ((rc = ensure(&ctx->ws, &ctx->ws_cap, need, ctx->stream, false))) return rc;
+    if (P.S > 0 && (rc = ensure(&ctx->sbuf, &ctx->sbuf_cap, sample_bytes(P.S), ctx->stream, false))) return rc;
+    layout_work(m, P, w, ctx->ws);
+    int32_t* dm = (int32_t*)ctx->dmeta;
+    rc = run_forward(ctx, m, kv, P, dm, (const uint32_t*)(dm + P.o_tok), 1, w, w.logits, nullptr, nullptr, 0, 0,
+                     nullptr);
+    if (rc) return rc;
+    if (P.S > 0) {
+        // greedy rows keep the argmax in w.am; sampled rows are drawn over it
+        SampleRows d = sample_rows(ctx->sbuf, P.S, 0);
+        const SampleParams* dprm = (const SampleParams*)(dm + o_prm);
+        launch_dist(ctx->stream, w.logits, P.S, m->cfg.vocab, 1, dprm, d);
+        launch_draw(ctx->stream, P.S, dprm, d, (uint64_t*)(dm + o_rng), w.am, 1, 0);
+        HIPCHK(hipGetLastError());
+        HIPCHK(hipMemcpyAsync(tokens_out, w.am, (size_t)P.S * 4, hipMemcpyDeviceToHost, ctx->stream));
+        HIPCHK(hipMemcpyAsync(h + o_rng, dm + o_rng, (size_t)P.S * 8, hipMemcpyDeviceToHost, ctx->stream));
+    }
+    HIPCHK(hipStreamSynchronize(ctx->stream));
+    if (P.S > 0) memcpy(rng, h + o_rng, (size_t)P.S * 8);
+    return 0;
+}
+
+int fg_spec_step(fg_ctx* ctx, const fg_model* target, fg_kv* tkv, const fg_model* draft, fg_kv* dkv,
+                 const fg_spec_seq* seqs, int32_t n_seqs, int32_t k, uint32_t* out_tokens, int32_t* out_count,
+                 int32_t* out_accepted) {
+    return spec_step(ctx, target, tkv, draft, dkv, seqs, n_seqs, k, nullptr, nullptr, out_tokens, out_count,
+                     out_accepted);
+}
+
+int fg_spec_step_sampled(fg_ctx* ctx, const fg_model* target, fg_kv* tkv, const fg_model* draft, fg_kv* dkv,
+                         const fg_spec_seq* seqs, int32_t n_seqs, int32_t k, const fg_sampling* params, uint64_t* rng,
+                         uint32_t* out_tokens, int32_t* out_count, int32_t* out_accepted) {
+    if (!params || !rng || n_seqs <= 0) return fail(FG_E_ARG, "sampling parameters and generator states required");
+    int rc = check_sampling(params, n_seqs);
+    if (rc) return rc;
+    return spec_step(ctx, target, tkv, draft, dkv, seqs, n_seqs, k, params, rng, out_tokens, out_count,
+                     out_accepted);
 }
 
 int fg_last_step_times(const fg_ctx* ctx, float* us3) {

@@ -166,4 +166,37 @@ void launch_accept(hipStream_t st, const uint32_t* argmax, const uint32_t* draft
 int attn_span(int hd);
 int attn_qmax(int hd);
 
+// ---------------------------------------------------------------------------
+// Sampling (sampling.hip). A row's distribution holds at most kSampleCap
+// pairs (top_k 1..kSampleCap), stored in the reference's order (tok, pr) and
+// in token order (tok_id, pr_id), each [row][kSampleCap], with n[row] pairs.
+// ---------------------------------------------------------------------------
+constexpr int kSampleCap = 1024;
+
+struct SampleParams {  // fg_sampling; temperature <= 0 is greedy
+    float temperature, top_p;
+    int32_t top_k, pad;
+};
+
+struct SampleRows {
+    uint32_t* tok;
+    float* pr;
+    uint32_t* tok_id;
+    float* pr_id;
+    int* n;
+};
+
+// distributions of `rows` logits rows (row r uses prm[r / rows_per_seq])
+void launch_dist(hipStream_t st, const float* logits, int rows, int vocab, int rows_per_seq, const SampleParams* prm,
+                 SampleRows& out);
+// a draw from each sampled row's distribution into out[r * out_stride + out_off]
+// (row r uses prm[r] and rng[r]); greedy rows are left as they are
+void launch_draw(hipStream_t st, int rows, const SampleParams* prm, const SampleRows& d, uint64_t* rng, uint32_t* out,
+                 int out_stride, int out_off);
+// the verify of a speculative step under sampling: p holds the target's
+// n_seqs*(k+1) verify rows, q the draft's k rounds ([round][seq] rows)
+void launch_accept_sampled(hipStream_t st, int n_seqs, int k, const SampleParams* prm, const uint32_t* vtok,
+                           const uint32_t* am, const SampleRows& p, const SampleRows& q, uint64_t* rng,
+                           uint32_t* out_tokens, int32_t* out_count, int32_t* out_accepted);
+
 }  // namespace fg

@@ -55,6 +55,36 @@ class FgSpecSeq(C.Structure):
                 ("blocks", u32p), ("n_blocks", C.c_int32), ("draft_blocks", u32p), ("n_draft_blocks", C.c_int32)]
 
 
+class FgSampling(C.Structure):
+    _fields_ = [("temperature", C.c_float), ("top_p", C.c_float), ("top_k", C.c_int32), ("reserved", C.c_int32)]
+
+
+u64p = C.POINTER(C.c_uint64)
+
+
+@dataclass
+class SamplingParams:
+    """The sampling fields of the reference's SamplingParams
+    (src/sampler.rs:8-19): temperature <= 0 is greedy; the device supports
+    top_k 1..1024. `seed` seeds the request's Rng (src/engine.rs:292-299)."""
+    temperature: float = 0.0
+    top_p: float = 1.0
+    top_k: int = 0
+    seed: int = 0
+
+    @property
+    def greedy(self) -> bool:
+        return self.temperature <= 0.0
+
+    def struct(self) -> FgSampling:
+        return FgSampling(self.temperature, self.top_p, self.top_k, 0)
+
+
+def rng_init(seed: int) -> int:
+    """Rng::new (src/rng.rs:8-10): the generator state of a seed."""
+    return ((seed * 0x9E3779B97F4A7C15) & 0xFFFFFFFFFFFFFFFF) | 1
+
+
 EXPORTS = {
     "fg_ctx_create": (C.c_int, [C.c_int, C.POINTER(C.c_void_p)]),
     "fg_ctx_destroy": (None, [C.c_void_p]),
@@ -74,6 +104,11 @@ EXPORTS = {
                              f32p]),
     "fg_spec_step": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.POINTER(FgSpecSeq),
                                C.c_int32, C.c_int32, u32p, i32p, i32p]),
+    "fg_spec_step_sampled": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p,
+                                       C.POINTER(FgSpecSeq), C.c_int32, C.c_int32, C.POINTER(FgSampling), u64p,
+                                       u32p, i32p, i32p]),
+    "fg_forward_sampled": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.POINTER(FgChunk), C.c_int32,
+                                     C.POINTER(FgSampling), u64p, u32p, i32p]),
     "fg_last_step_times": (C.c_int, [C.c_void_p, f32p]),
     "fg_profile": (C.c_int, [C.c_void_p, C.c_int32]),
     "fg_profile_read": (C.c_int, [C.c_void_p, C.c_int32, i32p, C.POINTER(C.c_int64), C.POINTER(C.c_double),
@@ -261,9 +296,41 @@ class SpecSeq:
     draft_blocks: np.ndarray
 
 
-def spec_step(ctx: Context, target: Model, tkv: KvCache, draft: Model, dkv: KvCache, seqs: list, k: int):
-    """One greedy speculative step on device. Returns (tokens per sequence,
-    accepted counts)."""
+def _sampling_arrays(params: list):
+    arr = (FgSampling * len(params))()
+    for i, p in enumerate(params):
+        arr[i] = p.struct()
+    return arr
+
+
+def forward_sampled(ctx: Context, model: Model, kv: KvCache, chunks, params: list, rng: np.ndarray) -> np.ndarray:
+    """Model::forward with each selected row sampled on the device
+    (fg_forward_sampled): params[r] for selected row r, rng (uint64, one
+    state per selected row) advanced in place. Returns the tokens."""
+    arr = (FgChunk * max(1, len(chunks)))()
+    keep = []
+    rows = 0
+    for i, (tok, pos, blocks, mode) in enumerate(chunks):
+        tok = np.ascontiguousarray(tok, dtype=np.uint32)
+        blocks = np.ascontiguousarray(blocks, dtype=np.uint32)
+        keep += [tok, blocks]
+        arr[i] = FgChunk(ptr(tok, u32p), len(tok), pos, ptr(blocks, u32p), len(blocks), mode)
+        rows += len(tok) if mode == LOGITS_ALL else (1 if mode == LOGITS_LAST and len(tok) else 0)
+    if len(params) != rows or rng.dtype != np.uint64 or len(rng) != rows or not rng.flags.c_contiguous:
+        raise ValueError("one parameter set and one uint64 generator state per selected row")
+    out = np.zeros(rows, np.uint32)
+    nrows = C.c_int32(0)
+    check(lib().fg_forward_sampled(ctx.h, model.h, kv.h, arr, len(chunks), _sampling_arrays(params),
+                                   rng.ctypes.data_as(u64p), ptr(out, u32p), C.byref(nrows)))
+    assert nrows.value == rows
+    return out
+
+
+def spec_step(ctx: Context, target: Model, tkv: KvCache, draft: Model, dkv: KvCache, seqs: list, k: int,
+              params: list | None = None, rng: np.ndarray | None = None):
+    """One speculative step on device (fg_spec_step, or fg_spec_step_sampled
+    with per-sequence params and uint64 generator states, advanced in place).
+    Returns (tokens per sequence, accepted counts)."""
     n = len(seqs)
     arr = (FgSpecSeq * n)()
     keep = []
@@ -277,8 +344,14 @@ def spec_step(ctx: Context, target: Model, tkv: KvCache, draft: Model, dkv: KvCa
     out = np.zeros((n, k + 1), np.uint32)
     cnt = np.zeros(n, np.int32)
     acc = np.zeros(n, np.int32)
-    check(lib().fg_spec_step(ctx.h, target.h, tkv.h, draft.h, dkv.h, arr, n, k, ptr(out, u32p), ptr(cnt, i32p),
-                             ptr(acc, i32p)))
+    if params is None:
+        check(lib().fg_spec_step(ctx.h, target.h, tkv.h, draft.h, dkv.h, arr, n, k, ptr(out, u32p), ptr(cnt, i32p),
+                                 ptr(acc, i32p)))
+    else:
+        if len(params) != n or rng is None or rng.dtype != np.uint64 or len(rng) != n or not rng.flags.c_contiguous:
+            raise ValueError("one parameter set and one uint64 generator state per sequence")
+        check(lib().fg_spec_step_sampled(ctx.h, target.h, tkv.h, draft.h, dkv.h, arr, n, k, _sampling_arrays(params),
+                                         rng.ctypes.data_as(u64p), ptr(out, u32p), ptr(cnt, i32p), ptr(acc, i32p)))
     return [out[i, :cnt[i]].copy() for i in range(n)], acc
 
 

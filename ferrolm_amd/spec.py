@@ -1,12 +1,15 @@
-"""Greedy speculative generation over the device path.
+"""Speculative generation over the device path.
 
-A host-side mirror of the reference engine's greedy loop
-(Engine::schedule/execute/propose, src/engine.rs:395-717): chunked prompt
-prefill under the token budget, then speculative steps of k draft proposals
-verified in one target pass, with the reference's rollback of the
-`computed` / `draft_computed` counters (src/engine.rs:613-615). `Runner`
-drives one request; `Batch` drives several that decode together, every step
-one device speculative step over all of them. The device does all model work
+A host-side mirror of the reference engine's loop (Engine::schedule/execute/
+propose, src/engine.rs:395-717): chunked prompt prefill under the token
+budget, then speculative steps of k draft proposals verified in one target
+pass, with the reference's rollback of the `computed` / `draft_computed`
+counters (src/engine.rs:613-615). `Runner` drives one request; `Batch` drives
+several that decode together, every step one device speculative step over
+all of them. Requests are greedy unless given SamplingParams; then every draw
+(the prompt's first token, the draft proposals, acceptance, residual and
+bonus draws) happens on the device from the request's generator state, which
+these loops carry between steps. The device does all model work
 (ferrolm_amd.gpu); these loops only do the reference's bookkeeping.
 """
 from __future__ import annotations
@@ -72,8 +75,12 @@ class Batch:
     shuffled pool shared by all sequences."""
 
     def __init__(self, ctx: gpu.Context, target: gpu.Model, draft: gpu.Model, prompts, k: int, kv_blocks: int,
-                 seed: int = 0, tkv=None, dkv=None):
+                 seed: int = 0, tkv=None, dkv=None, params: list | None = None):
         self.ctx, self.target, self.draft, self.k = ctx, target, draft, k
+        # per-sequence sampling (None: every sequence greedy)
+        self.params = params if params is not None and any(not p.greedy for p in params) else None
+        self.rng = (np.array([gpu.rng_init(p.seed) for p in params], np.uint64) if self.params is not None
+                    else None)
         self.max_len = target.cfg.max_position
         self.tkv = tkv or gpu.KvCache(ctx, target.cfg, kv_blocks)
         self.dkv = dkv or gpu.KvCache(ctx, draft.cfg, kv_blocks)
@@ -108,9 +115,16 @@ class Batch:
                 else:
                     work.insert(0, (i, pos + n))
                 room -= n
-            o = gpu.forward(self.ctx, self.target, self.tkv, chunks, logits=False)
-            for r, i in enumerate(rows):
-                first[i] = int(o.argmax[r])
+            if self.params is None:
+                o = gpu.forward(self.ctx, self.target, self.tkv, chunks, logits=False)
+                for r, i in enumerate(rows):
+                    first[i] = int(o.argmax[r])
+            else:
+                st = np.ascontiguousarray(self.rng[rows])
+                toks = gpu.forward_sampled(self.ctx, self.target, self.tkv, chunks, [self.params[i] for i in rows], st)
+                self.rng[rows] = st
+                for r, i in enumerate(rows):
+                    first[i] = int(toks[r])
         for i, t in enumerate(self.tokens):
             self.computed[i] = len(t)
             t.append(first[i])
@@ -129,7 +143,8 @@ class Batch:
             seqs.append(gpu.SpecSeq(tail=np.array(t[self.dcomp[i]:], np.uint32), draft_pos=self.dcomp[i],
                                     pos=self.computed[i], blocks=np.array(self.tb[i], np.uint32),
                                     draft_blocks=np.array(self.db[i], np.uint32)))
-        toks, acc = gpu.spec_step(self.ctx, self.target, self.tkv, self.draft, self.dkv, seqs, k)
+        toks, acc = gpu.spec_step(self.ctx, self.target, self.tkv, self.draft, self.dkv, seqs, k, self.params,
+                                  self.rng)
         t_us = gpu.last_step_times(self.ctx)
         st = self.stats
         st.draft_us.append(float(t_us[0]))
@@ -153,8 +168,11 @@ class Runner:
     """One request through the engine's greedy loop (ignore_eos)."""
 
     def __init__(self, ctx: gpu.Context, target: gpu.Model, draft: gpu.Model | None, prompt, k: int,
-                 kv_blocks: int = 1024, max_batch_tokens: int = 512, max_seqs: int = 64, tkv=None, dkv=None):
+                 kv_blocks: int = 1024, max_batch_tokens: int = 512, max_seqs: int = 64, tkv=None, dkv=None,
+                 params: gpu.SamplingParams | None = None):
         self.ctx, self.target, self.draft = ctx, target, draft
+        self.params = params if params is not None and not params.greedy else None
+        self.rng = np.array([gpu.rng_init(params.seed)], np.uint64) if self.params is not None else None
         self.k = k if draft is not None else 0
         self.bs = 16
         self.max_len = min(target.cfg.max_position, kv_blocks * self.bs)
@@ -190,7 +208,8 @@ class Runner:
             seq = gpu.SpecSeq(tail=np.array(self.tokens[self.dcomp:], np.uint32), draft_pos=self.dcomp,
                               pos=self.computed, blocks=np.array(self.tb, np.uint32),
                               draft_blocks=np.array(self.db, np.uint32))
-            toks, acc = gpu.spec_step(self.ctx, self.target, self.tkv, self.draft, self.dkv, [seq], k)
+            toks, acc = gpu.spec_step(self.ctx, self.target, self.tkv, self.draft, self.dkv, [seq], k,
+                                      None if self.params is None else [self.params], self.rng)
             t_us = gpu.last_step_times(self.ctx)
             st = self.stats
             st.draft_us.append(float(t_us[0]))
@@ -206,11 +225,15 @@ class Runner:
             self.dcomp = min(base + k - 1, base + a)
         else:
             last = self.computed + n == len(self.tokens)
-            o = gpu.forward(self.ctx, self.target, self.tkv,
-                            [(self.tokens[self.computed:self.computed + n], self.computed, self.tb,
-                              gpu.LOGITS_LAST if last else gpu.LOGITS_NONE)], logits=False)
+            chunk = (self.tokens[self.computed:self.computed + n], self.computed, self.tb,
+                     gpu.LOGITS_LAST if last else gpu.LOGITS_NONE)
+            if last and self.params is not None:
+                emitted = [int(gpu.forward_sampled(self.ctx, self.target, self.tkv, [chunk], [self.params],
+                                                   self.rng)[0])]
+            else:
+                o = gpu.forward(self.ctx, self.target, self.tkv, [chunk], logits=False)
+                emitted = [int(o.argmax[0])] if last else []
             self.computed += n
-            emitted = [int(o.argmax[0])] if last else []
         out = []
         for t in emitted:
             if len(self.tokens) >= self.max_len:
@@ -231,7 +254,8 @@ class Runner:
 def generate(ctx: gpu.Context, target: gpu.Model, draft: gpu.Model | None, prompt, max_tokens: int, k: int,
              kv_blocks: int = 1024, max_batch_tokens: int = 512, stats: GenStats | None = None, **kw):
     """The generated ids (the first from the prompt's prefill), stopping at
-    max_tokens or the context limit (src/engine.rs:633-636)."""
+    max_tokens or the context limit (src/engine.rs:633-636). params=
+    SamplingParams samples instead of decoding greedily."""
     r = Runner(ctx, target, draft, prompt, k, kv_blocks, max_batch_tokens, **kw)
     while len(r.generated) < max_tokens and len(r.tokens) < r.max_len:
         r.step()

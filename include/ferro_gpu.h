@@ -106,6 +106,19 @@ typedef struct {
     int32_t n_draft_blocks;
 } fg_spec_seq;
 
+/* The sampling fields of SamplingParams (src/sampler.rs:8-19, :34-38):
+ * temperature <= 0 is greedy; otherwise logits are divided by
+ * max(temperature, 1e-5), cut to the top_k largest (1..1024 on the device:
+ * the reference's 0, no limit, needs a whole-vocabulary sort and is
+ * refused with FG_E_ARG) and to the shortest prefix whose probability
+ * reaches top_p (1 keeps all). */
+typedef struct {
+    float temperature;
+    float top_p;
+    int32_t top_k;
+    int32_t reserved;
+} fg_sampling;
+
 /* ---- context ---------------------------------------------------------- */
 /* Engine::new's device side: binds `device`, creates the stream and
  * workspace. No reference counterpart beyond Pool::new (src/pool.rs:45). */
@@ -174,6 +187,34 @@ int fg_spec_step(fg_ctx* ctx, const fg_model* target, fg_kv* target_kv,
                  const fg_spec_seq* seqs, int32_t n_seqs, int32_t k,
                  uint32_t* out_tokens, int32_t* out_count,
                  int32_t* out_accepted);
+
+/* fg_spec_step under per-sequence sampling (Engine::propose and
+ * Engine::execute with !params.greedy(), src/engine.rs:575-610, 691-700):
+ * each draft round draws its proposal from sampler::distribution of the
+ * draft's logits; proposal j is accepted when its draft probability q is
+ * positive and a uniform draw is below min(1, p/q) under the target's
+ * distribution p of verify row j; the first rejection emits a draw from
+ * max(0, p - q) in token order (from p when that is empty) and ends the
+ * step; k acceptances add a draw from the target's last row. rng[s] is the
+ * state of sequence s's Rng (src/rng.rs:5-16; Rng::new(seed) =
+ * seed * 0x9E3779B97F4A7C15 | 1), advanced on the device in the
+ * reference's order and written back. Sequences with temperature <= 0 are
+ * verified greedily as in fg_spec_step and draw nothing. */
+int fg_spec_step_sampled(fg_ctx* ctx, const fg_model* target, fg_kv* target_kv,
+                         const fg_model* draft, fg_kv* draft_kv,
+                         const fg_spec_seq* seqs, int32_t n_seqs, int32_t k,
+                         const fg_sampling* params, uint64_t* rng,
+                         uint32_t* out_tokens, int32_t* out_count,
+                         int32_t* out_accepted);
+
+/* fg_forward whose selected rows are sampled on the device
+ * (sampler::sample, src/sampler.rs:105-111; the engine's step of a prompt's
+ * last chunk, src/engine.rs:549-560): params[r] and rng[r] (advanced in
+ * place) belong to selected row r, tokens_out[r] receives its token. */
+int fg_forward_sampled(fg_ctx* ctx, const fg_model* m, fg_kv* kv,
+                       const fg_chunk* chunks, int32_t n_chunks,
+                       const fg_sampling* params, uint64_t* rng,
+                       uint32_t* tokens_out, int32_t* rows_out);
 
 /* Device time in microseconds of the last fg_spec_step's phases, measured
  * with HIP events on the context stream: [0] draft rounds, [1] verify

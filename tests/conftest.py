@@ -22,3 +22,41 @@ def ctx():
     c = gpu.Context(0)
     yield c
     c.close()
+
+
+def reference_prompts(n, seed):
+    """tests/engine.rs:19-27 of the reference: n prompts from Rng(seed),
+    lengths between(1, 150), ids between(3, 511)."""
+    import ctypes
+    import oracle
+    rng = ctypes.c_uint64(oracle.lib().or_rng_new(seed))
+    nxt = lambda: oracle.lib().or_rng_next(ctypes.byref(rng))
+    out = []
+    for _ in range(n):
+        ln = 1 + nxt() % 150
+        out.append([3 + nxt() % 509 for _ in range(ln)])
+    return out
+
+
+def exact_two_token_distribution(m, prompt, params):
+    """tests/engine.rs:163-194 of the reference on the oracle model m: the
+    probability of each two-token continuation of prompt under params =
+    (temperature, top_p, top_k)."""
+    import oracle
+
+    def nxt(tokens):
+        kv = m.kv(16)
+        lg = m.forward(kv, [(tokens, 0, list(range(16)), 1)])[0]
+        return zip(*oracle.distribution(lg, *params))
+
+    out = []
+    for t1, p1 in nxt(prompt):
+        for t2, p2 in nxt(list(prompt) + [int(t1)]):
+            out.append(((int(t1), int(t2)), float(p1) * float(p2)))
+    return out
+
+
+def chi_square(counts: dict, exact, n: int) -> float:
+    """Pearson's statistic of observed continuation counts against exact."""
+    assert set(counts) <= {s for s, _ in exact}, "impossible continuation sampled"
+    return sum((counts.get(s, 0) - p * n) ** 2 / (p * n) for s, p in exact)

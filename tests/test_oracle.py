@@ -11,7 +11,7 @@ import pytest
 import oracle
 from ferrolm_amd.weights import BF16, INT4, INT8, Matrix, bf16_to_f32, f32_to_bf16, load_model
 
-from conftest import FIXTURES, GOLDEN
+from conftest import FIXTURES, GOLDEN, chi_square, exact_two_token_distribution, reference_prompts
 
 
 def scattered(tokens, bs=16):
@@ -320,30 +320,6 @@ def test_distribution_orders_ties_by_token_and_cuts_top_p():
     assert tok3.tolist() == [1, 2]
 
 
-def _reference_prompts(n, seed):
-    """tests/engine.rs:19-27: lengths between(1, 150), ids between(3, 511)."""
-    rng = ctypes.c_uint64(oracle.lib().or_rng_new(seed))
-    nxt = lambda: oracle.lib().or_rng_next(ctypes.byref(rng))
-    out = []
-    for _ in range(n):
-        ln = 1 + nxt() % 150
-        out.append([3 + nxt() % 509 for _ in range(ln)])
-    return out
-
-
-def exact_two_token_distribution(m, prompt, params):
-    """tests/engine.rs:163-194: the probability of each two-token continuation."""
-    def nxt(tokens):
-        kv = m.kv(16)
-        lg = m.forward(kv, [(tokens, 0, list(range(16)), 1)])[0]
-        return zip(*oracle.distribution(lg, *params))
-    out = []
-    for t1, p1 in nxt(prompt):
-        for t2, p2 in nxt(list(prompt) + [int(t1)]):
-            out.append(((int(t1), int(t2)), float(p1) * float(p2)))
-    return out
-
-
 def test_speculative_sampling_keeps_the_target_distribution():
     """tests/engine.rs:196-243 on the oracle's engine loop: the first two
     sampled tokens after a fixed prompt, 4000 requests (seeds 1..4000), with
@@ -351,7 +327,7 @@ def test_speculative_sampling_keeps_the_target_distribution():
     chi-square test (16 outcomes, 0.1% critical value 37.7)."""
     hm = load_model(GOLDEN / "llama-gqa")
     m = oracle.Model(hm)
-    prompt = _reference_prompts(1, 5)[0]
+    prompt = reference_prompts(1, 5)[0]
     params = (1.0, 1.0, 4)
     exact = exact_two_token_distribution(m, prompt, params)
     assert len(exact) == 16
@@ -366,8 +342,7 @@ def test_speculative_sampling_keeps_the_target_distribution():
             seen[key] = seen.get(key, 0) + 1
             st[0] += prop
             st[1] += acc
-        assert set(seen) <= {s for s, _ in exact}, "impossible continuation sampled"
-        return sum((seen.get(s, 0) - p * n) ** 2 / (p * n) for s, p in exact), st
+        return chi_square(seen, exact, n), st
 
     plain, _ = chi2(None)
     spec, (proposed, accepted) = chi2(m.truncated(1))
