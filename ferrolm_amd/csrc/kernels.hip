@@ -913,14 +913,15 @@ __device__ __forceinline__ uint32_t bf16x2_i8(uint32_t w, int b) {
 // The GEMM epilogues on the finished 64 x 64 tile yt (rows [row0, row0 + rows),
 // columns from col0): 1/rms from the producers' sums of squares, then the
 // GEMV's epilogues (internal.h) with the next operand in the MM format.
-template <int EPI, int NTHR>
+template <int EPI, int NTHR, int MR>
 __device__ void gemm_epilogue(const GemvArgs& a, float* yt, float* part, float* rs, int row0, int rows, int col0) {
     constexpr bool NEED_R = EPI == EPI_QKV || EPI == EPI_SILU || EPI == EPI_ARGMAX;
     constexpr int YS = 68;
+    static_assert(MR * 4 <= NTHR, "four lanes per row");
     const int tid = threadIdx.x;
     __syncthreads();
     // 1/rms of each row from the producers' sums of squares: four lanes per row
-    if (NEED_R && tid < 256) {
+    if (NEED_R && tid < MR * 4) {
         const int rr = tid >> 2, q4 = tid & 3, row = row0 + rr;
         float v = 0.0f;
         if (rr < rows) {
@@ -933,7 +934,7 @@ __device__ void gemm_epilogue(const GemvArgs& a, float* yt, float* part, float* 
     __syncthreads();
 
     if (EPI == EPI_STORE || EPI == EPI_QKV) {
-        for (int idx = tid; idx < 64 * 64; idx += NTHR) {
+        for (int idx = tid; idx < MR * 64; idx += NTHR) {
             const int rr = idx >> 6, cc = idx & 63, row = row0 + rr, col = col0 + cc;
             if (rr < rows && col < a.N) {
                 float v = yt[rr * YS + cc];
@@ -945,7 +946,7 @@ __device__ void gemm_epilogue(const GemvArgs& a, float* yt, float* part, float* 
         return;
     }
     if (EPI == EPI_ARGMAX) {
-        for (int idx = tid; idx < 64 * 64; idx += NTHR) {
+        for (int idx = tid; idx < MR * 64; idx += NTHR) {
             const int rr = idx >> 6, cc = idx & 63, row = row0 + rr, col = col0 + cc;
             const float v = yt[rr * YS + cc] * rs[rr];
             if (rr < rows && col < a.N && a.logits) a.logits[(size_t)row * a.N + col] = v;
@@ -953,7 +954,7 @@ __device__ void gemm_epilogue(const GemvArgs& a, float* yt, float* part, float* 
         }
         __syncthreads();
         // (max, first index) of each row in each 32-column tile
-        if (tid < 128) {
+        if (tid < MR * 2) {
             const int rr = tid >> 1, j = tid & 1, row = row0 + rr;
             if (rr < rows && col0 + j * 32 < a.N) {
                 const float* yr = &yt[rr * YS + j * 32];
@@ -974,7 +975,7 @@ __device__ void gemm_epilogue(const GemvArgs& a, float* yt, float* part, float* 
     // GEMM's MM pieces (two bf16 pieces per value) in 16-byte slots.
     constexpr int OC = EPI == EPI_RESID ? 64 : 32;
     float* vt = part;  // free again after the tree
-    for (int idx = tid; idx < 64 * OC; idx += NTHR) {
+    for (int idx = tid; idx < MR * OC; idx += NTHR) {
         const int rr = idx / OC, cc = idx % OC, row = row0 + rr;
         const bool live = rr < rows && (EPI == EPI_SILU || col0 + cc < a.N);
         if (EPI == EPI_RESID) {
@@ -991,7 +992,7 @@ __device__ void gemm_epilogue(const GemvArgs& a, float* yt, float* part, float* 
         }
     }
     __syncthreads();
-    if (EPI == EPI_RESID && tid < 256) {
+    if (EPI == EPI_RESID && tid < MR * 4) {
         // each row's sum of squares over the group's columns: four lanes per row
         const int rr = tid >> 2, q4 = tid & 3, row = row0 + rr;
         float ssq = 0.0f;
@@ -1007,7 +1008,7 @@ __device__ void gemm_epilogue(const GemvArgs& a, float* yt, float* part, float* 
         // slot (k-block, row tile, piece h, lane q8 * 16 + row % 16) holds 8 values
         const int prt = (a.pa_passes + 3) >> 2, kb0 = col0 / 32;
         constexpr int Q8 = OC / 8;
-        for (int idx = tid; idx < 64 * Q8 * 2; idx += NTHR) {
+        for (int idx = tid; idx < MR * Q8 * 2; idx += NTHR) {
             const int h = idx & 1, q8 = (idx >> 1) % Q8, rr = (idx >> 1) / Q8, row = row0 + rr;
             if (rr >= rows) continue;
             const int kb = (EPI == EPI_RESID ? kb0 : (int)blockIdx.x) + q8 / 4;
@@ -1021,8 +1022,8 @@ __device__ void gemm_epilogue(const GemvArgs& a, float* yt, float* part, float* 
         if (blockIdx.x == gridDim.x - 1) {
             const int covered = EPI == EPI_RESID ? (a.N + 31) / 32 : (int)gridDim.x;
             const u16x8 z = {0, 0, 0, 0, 0, 0, 0, 0};
-            for (int idx = tid; idx < (a.pa_kb - covered) * 64 * 8; idx += NTHR) {
-                const int kb = covered + idx / 512, rem = idx % 512, h = rem & 1, q8 = (rem >> 1) & 3,
+            for (int idx = tid; idx < (a.pa_kb - covered) * MR * 8; idx += NTHR) {
+                const int kb = covered + idx / (MR * 8), rem = idx % (MR * 8), h = rem & 1, q8 = (rem >> 1) & 3,
                           rr = rem >> 3, row = row0 + rr;
                 if (rr < rows)
                     ((u16x8*)a.pa)[(((size_t)kb * prt + (row >> 4)) * 2 + h) * 64 + q8 * 16 + (row & 15)] = z;
@@ -1036,11 +1037,11 @@ __global__ __launch_bounds__(512) void k_gemm(const GemvArgs a) {
     constexpr int NW = 8, NTHR = 64 * NW;
     constexpr bool Q = KIND != BF16;
     constexpr bool NEED_R = EPI == EPI_QKV || EPI == EPI_SILU || EPI == EPI_ARGMAX;
-    constexpr int YS = 68;  // LDS row stride of the 64 x 64 tile
+    constexpr int YS = 68;  // LDS row stride of the 16 RTW x 64 tile
     // the cross-wave tree: four partial tiles (the lanes' layout), then the tile
-    __shared__ __align__(16) float part[4 * 64 * 64];
-    __shared__ __align__(16) float yt[64 * YS];
-    __shared__ float rs[64];
+    __shared__ __align__(16) float part[4 * RTW * 4 * 256];
+    __shared__ __align__(16) float yt[16 * RTW * YS];
+    __shared__ float rs[16 * RTW];
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: scalar registers, no divergence
@@ -1135,13 +1136,13 @@ __global__ __launch_bounds__(512) void k_gemm(const GemvArgs a) {
         for (int i = 0; i < RTW; i++)
 #pragma unroll
             for (int t = 0; t < 4; t++)
-                *(f32x4*)&part[((slot * 16 + i * 4 + t) * 64 + lane) * 4] = acc[i][t];
+                *(f32x4*)&part[((slot * RTW * 4 + i * 4 + t) * 64 + lane) * 4] = acc[i][t];
     };
     auto take = [&](int slot) {
 #pragma unroll
         for (int i = 0; i < RTW; i++)
 #pragma unroll
-            for (int t = 0; t < 4; t++) acc[i][t] += *(const f32x4*)&part[((slot * 16 + i * 4 + t) * 64 + lane) * 4];
+            for (int t = 0; t < 4; t++) acc[i][t] += *(const f32x4*)&part[((slot * RTW * 4 + i * 4 + t) * 64 + lane) * 4];
     };
     if (wave >= 4) put(wave - 4);
     __syncthreads();
@@ -1179,7 +1180,7 @@ __global__ __launch_bounds__(512) void k_gemm(const GemvArgs a) {
                 for (int r = 0; r < 4; r++) yt[(i * 16 + 4 * (lane >> 4) + r) * YS + t * 16 + (lane & 15)] = acc[i][t][r];
     }
     if (ks > 1) return;
-    gemm_epilogue<EPI, NTHR>(a, yt, part, rs, row0, rows, col0);
+    gemm_epilogue<EPI, NTHR, 16 * RTW>(a, yt, part, rs, row0, rows, col0);
 }
 
 // The split-K sum (splits in order, so the result does not depend on which
@@ -1220,7 +1221,7 @@ __global__ __launch_bounds__(256) void k_gemm_finish(const GemvArgs a) {
             }
         *(float4*)&yt[rr * YS + cc] = live ? t : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     }
-    gemm_epilogue<EPI, 256>(a, yt, vt, rs, row0, rows, col0);
+    gemm_epilogue<EPI, 256, 16 * RTW>(a, yt, vt, rs, row0, rows, col0);
 }
 
 template <int KIND, int RTW>
@@ -1256,17 +1257,20 @@ static void gemm_rtw(hipStream_t st, int epi, const DMat& w, const GemvArgs& a0,
     }
 }
 
-// Row tiles per workgroup: as few groups of at most four as cover the rows,
-// each as small as that allows (rows past m cost loads and MFMAs).
+// Row tiles per workgroup: as few groups of at most five as cover the rows
+// (each group reads every weight tile once), each as small as that allows
+// (rows past m cost loads and MFMAs).
 template <int KIND>
 static void gemm_kind(hipStream_t st, int epi, const DMat& w, const GemvArgs& a, hipEvent_t e0, hipEvent_t e1) {
-    const int rt = (a.p_total + 3) / 4, groups = (rt + 3) / 4, rtw = (rt + groups - 1) / groups;
+    const int rt = (a.p_total + 3) / 4, groups = (rt + 4) / 5, rtw = (rt + groups - 1) / groups;
     if (rtw <= 2)
         gemm_rtw<KIND, 2>(st, epi, w, a, (rt + 1) / 2, e0, e1);
     else if (rtw == 3)
         gemm_rtw<KIND, 3>(st, epi, w, a, (rt + 2) / 3, e0, e1);
+    else if (rtw == 4)
+        gemm_rtw<KIND, 4>(st, epi, w, a, (rt + 3) / 4, e0, e1);
     else
-        gemm_rtw<KIND, 4>(st, epi, w, a, groups, e0, e1);
+        gemm_rtw<KIND, 5>(st, epi, w, a, groups, e0, e1);
 }
 
 template <int KIND, int NT, int EPI>

@@ -38,7 +38,7 @@ def test_matmul_matches_oracle(ctx, kind, n, k):
     dm = gpu.Mat(ctx, w)
     deq = w.to_f32().astype(np.float64)
     rng = np.random.default_rng(k)
-    for m in [1, 2, 3, 4, 5, 8, 13, 17, 40, 70]:  # past 16 rows: the GEMM (split K for the small n)
+    for m in [1, 2, 3, 4, 5, 8, 13, 17, 40, 70, 100, 160]:  # past 16 rows: the GEMM (split K for the small n)
         x = rng.standard_normal((m, k)).astype(np.float32)
         x[:, ::7] *= 20.0  # a few large channels, as activations have
         y = dm.matmul(x)
