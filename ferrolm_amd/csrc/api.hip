@@ -395,6 +395,7 @@ struct ChunkIn {
 
 struct Plan {
     int t = 0, S = 0, W = 0;
+    int ns = 1;  // attention sub-spans per work item (k_attn's NS)
     int Wc = 0;  // work items launched: W rounded up to 16, the extra records empty, so
                  // the launch shapes (and a captured step graph) last for 16 more spans
     // wrec: one 16-word record per attention work item (a span of one row
@@ -412,9 +413,27 @@ static int build_plan(const fg_config& c, const fg_kv& kv, int max_pos, const Ch
     const int bs = kv.block_size;
     const int group = c.heads / c.kv_heads;
     const int rg = std::max(1, std::min(16, attn_qmax(c.head_dim) / group));
-    const int span = attn_span(c.head_dim);
-    if (bs != 16 || span % bs || span / bs > 8) return fail(FG_E_SHAPE, "attention spans need 16-token blocks");
+    const int span1 = attn_span(c.head_dim);
+    if (bs != 16 || span1 % bs || span1 / bs > 8) return fail(FG_E_SHAPE, "attention spans need 16-token blocks");
     P = Plan();
+    // Work items of one span, or, when they would be more than 1024 workgroups
+    // and a row group reaches kAttnMfmaQueries queries (GQA verify batches,
+    // prefill chunks), of 128 positions: 2 or 4 sub-spans whose loads overlap
+    // the scoring of the previous one. Otherwise one span per work item
+    // (measured: fewer, longer items are slower for the few queries of a
+    // decode step, cfg3 verify 3.02 against 2.73 ms; cfg4's 20-query items
+    // gain, verify 11.2 to 10.0 ms).
+    int64_t w1 = 0;
+    int maxq = 0;
+    for (int ci = 0; ci < nch; ci++)
+        for (int r0 = 0; r0 < ch[ci].n; r0 += rg) {
+            const int nr = std::min(rg, ch[ci].n - r0);
+            const int64_t L = (int64_t)ch[ci].pos + r0 + nr;
+            w1 += (L + span1 - 1) / span1;
+            maxq = std::max(maxq, nr * group);
+        }
+    P.ns = w1 * c.kv_heads > 1024 && maxq >= kAttnMfmaQueries ? 128 / span1 : 1;
+    const int span = span1 * P.ns;
     for (int ci = 0; ci < nch; ci++) {
         const ChunkIn& k = ch[ci];
         if (k.n < 0 || k.pos < 0) return fail(FG_E_ARG, "negative chunk length or position");
@@ -618,6 +637,7 @@ static int run_forward(fg_ctx* ctx, const fg_model* m, fg_kv* kv, const Plan& P,
     aa.mrec = meta + P.o_mrec;
     aa.part = w.apart;
     aa.n_wi = P.Wc;
+    aa.ns = P.ns;
     aa.nh = nh;
     aa.nkv = nkv;
     aa.hd = hd;
@@ -1115,7 +1135,8 @@ static int spec_step(fg_ctx* ctx, const fg_model* target, fg_kv* tkv, const fg_m
                                     (int64_t)sampling, (int64_t)(uintptr_t)ctx->sbuf, (int64_t)ctx->sbuf_cap};
         for (int r = 0; r <= k; r++) {
             const Plan& P = plans[r];
-            for (int64_t v : {(int64_t)P.t, (int64_t)P.S, (int64_t)P.Wc, (int64_t)P.words}) sig.push_back(v);
+            for (int64_t v : {(int64_t)P.t, (int64_t)P.S, (int64_t)P.Wc, (int64_t)P.words, (int64_t)P.ns})
+                sig.push_back(v);
         }
         for (auto& g : ctx->gsets)
             if (g.sig == sig) gset = &g;

@@ -141,7 +141,8 @@ struct AttnArgs {
     const float* sin_t;
     // [n_wi][16] per work item: row0, nrows (the row group), crow0, cpos0 (first
     // row and position of the group's chunk; rows of a chunk hold consecutive
-    // positions), p0, p1 (the span), 0, 0, then the span's cache block ids.
+    // positions), p0, p1 (the span, at most 128 positions), 0, 0, then the
+    // span's cache block ids (up to 8).
     // A record with nrows 0 is an unused slot.
     const int32_t* wrec;
     // [rows][4] per row: first query index within its group, the group's first
@@ -149,6 +150,7 @@ struct AttnArgs {
     const int32_t* mrec;
     float* part;  // [wi][nkv][attn_qmax(hd)][hd+4]: max score, sum of exponentials, 0, 0, weighted values
     int n_wi, nh, nkv, hd, bs;
+    int ns;  // sub-spans of attn_span(hd) positions per work item (1, 2 or 4; at most 128 positions)
     float scale;
 };
 // Attention over the paged cache (RoPE, K/V write of the new rows), then the
@@ -165,6 +167,12 @@ void launch_accept(hipStream_t st, const uint32_t* argmax, const uint32_t* draft
 // group x GQA group), by head dim.
 int attn_span(int hd);
 int attn_qmax(int hd);
+// Queries of a work item from which attention runs on MFMA (measured: the VALU
+// loops are faster for the 3 to 5 queries of decode steps, MFMA for the 20 of
+// an 8B GQA verify). Plans whose row groups reach it take work items of
+// several sub-spans when the launch is large (k_attn's NS): the loads of the
+// next sub-span then overlap MFMA work worth hiding them behind.
+constexpr int kAttnMfmaQueries = 16;
 
 // ---------------------------------------------------------------------------
 // Sampling (sampling.hip). A row's distribution holds at most kSampleCap

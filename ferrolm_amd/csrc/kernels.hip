@@ -1381,13 +1381,14 @@ void launch_gemv(hipStream_t st, int epi, const DMat& w, const GemvArgs& a, hipE
 // writes per query the span's max score, sum of exponentials and weighted
 // values; k_merge_pieces combines the spans.
 // ---------------------------------------------------------------------------
-// queries of a work item from which attention runs on MFMA (measured: the VALU
-// loops are faster for the 3 to 5 queries of decode steps, MFMA for the 20 of
-// an 8B GQA verify)
-constexpr int kAttnMfmaQueries = 16;
-
-template <int HD, int P, int QM>
-__global__ __launch_bounds__(256) void k_attn(AttnArgs a) {
+// A work item covers NS consecutive sub-spans of P positions (at most 128
+// positions: the eight cache blocks of its record). With NS > 1 the next
+// sub-span's keys and values are loaded into registers while the current one
+// is scored from LDS, and the softmax runs online across sub-spans: a
+// running max and sum per query, the weighted values rescaled by
+// exp(old max - new max) (flash-decoding within the work item).
+template <int HD, int P, int QM, int NS>
+__global__ __launch_bounds__(256, 2) void k_attn(AttnArgs a) {
     constexpr int HALF = HD / 2;
     // rows padded by 4 floats (16-byte aligned): lanes reading one column of
     // consecutive rows (the MFMA operands) hit distinct banks
@@ -1396,14 +1397,16 @@ __global__ __launch_bounds__(256) void k_attn(AttnArgs a) {
     __shared__ __align__(16) float qs[QM][HD + 4];
     __shared__ __align__(16) float pr[QM][P + 4];
     __shared__ int lim[QM];
+    __shared__ float mrun[NS > 1 ? QM : 1], lrun[NS > 1 ? QM : 1], fac[NS > 1 ? QM : 1];
 
-    static_assert(P <= 64 && P % 16 == 0 && 64 % P == 0, "a span covers at most four cache blocks");
+    static_assert(P <= 64 && P % 16 == 0 && 64 % P == 0, "a sub-span covers at most four cache blocks");
+    static_assert(NS * P <= 128, "a work item covers at most the eight cache blocks of its record");
     // grid (kv head, work item): every real item is dispatched before the
     // launch's unused capacity slots, which exit at once
     const int h = blockIdx.x, wi = blockIdx.y;
     // the work item's record: one 64-byte read, everything else is arithmetic
     const int4* rec = (const int4*)(a.wrec + (size_t)wi * 16);
-    const int4 r0 = rec[0], r1 = rec[1], rb = rec[2];
+    const int4 r0 = rec[0], r1 = rec[1], rb = rec[2], rb2 = rec[3];
     const int row0 = r0.x, nrows = r0.y, crow0 = r0.z, cpos0 = r0.w;
     const int p0 = r1.x, p1 = r1.y;
     if (nrows == 0) return;  // an unused slot of the launch's capacity
@@ -1411,16 +1414,26 @@ __global__ __launch_bounds__(256) void k_attn(AttnArgs a) {
     const int Q = nrows * G;
     const int qd = a.nh * HD, kvd = a.nkv * HD;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    auto blk = [&](int j) -> size_t { return (uint32_t)(j == 0 ? rb.x : j == 1 ? rb.y : j == 2 ? rb.z : rb.w); };
+    auto blk = [&](int j) -> size_t {
+        const int4 b = j < 4 ? rb : rb2;
+        const int jj = j & 3;
+        return (uint32_t)(jj == 0 ? b.x : jj == 1 ? b.y : jj == 2 ? b.z : b.w);
+    };
     // rows of a chunk hold consecutive positions: row r sees positions <= its own
     const int pos_of_row0 = cpos0 + row0 - crow0;
-    for (int q = tid; q < Q; q += 256) lim[q] = pos_of_row0 + q / G;
-    // Every load of the span is issued before anything waits on one: the keys
+    for (int q = tid; q < Q; q += 256) {
+        lim[q] = pos_of_row0 + q / G;
+        if (NS > 1) {
+            mrun[q] = -INFINITY;
+            lrun[q] = 0.0f;
+        }
+    }
+    // A sub-span's loads are all issued before anything waits on one: the keys
     // and values (from the cache, or from the q/k/v rows for this chunk's new
-    // positions) with the cos/sin of their positions into registers, then q.
-    // One round trip. The loads take no branches (a value loaded under a
-    // condition gets copied at the join, which waits on it): positions past
-    // the span read its last position, and the LDS stores below select.
+    // positions) with the cos/sin of their positions, into registers. The
+    // loads take no branches (a value loaded under a condition gets copied at
+    // the join, which waits on it): positions past the sub-span read its last
+    // position, and the LDS stores below select.
     constexpr int KI = P * (HALF / 4), KIT = (KI + 255) / 256;
     constexpr int VI = P * (HD / 4), VIT = (VI + 255) / 256;
     float4 ku[KIT], kw[KIT], kcs[KIT], ksn[KIT], vv[VIT];
@@ -1430,25 +1443,28 @@ __global__ __launch_bounds__(256) void k_attn(AttnArgs a) {
         return cached ? (col ? a.vc : a.kc) + ((blk((p - p0) >> 4) * a.nkv + h) * 16 + (p & 15)) * HD
                       : a.qkv + crow * a.ld + qd + col + h * HD;
     };
+    auto load_sub = [&](int sp0, int sp1) {
 #pragma unroll
-    for (int it = 0; it < KIT; it++) {
-        const int i = min(tid + it * 256, KI - 1);
-        const int d = (i % (HALF / 4)) * 4, p = min(p0 + i / (HALF / 4), p1 - 1);
-        const float* kp = src_of(p, 0);
-        ku[it] = *(const float4*)(kp + d);
-        kw[it] = *(const float4*)(kp + d + HALF);
-        // only new keys are rotated: cached positions all read the chunk's first
-        // position (one cache line instead of a table row each)
-        const int pr = max(p, cpos0);
-        kcs[it] = *(const float4*)(a.cos_t + (size_t)pr * HALF + d);
-        ksn[it] = *(const float4*)(a.sin_t + (size_t)pr * HALF + d);
-    }
+        for (int it = 0; it < KIT; it++) {
+            const int i = min(tid + it * 256, KI - 1);
+            const int d = (i % (HALF / 4)) * 4, p = min(sp0 + i / (HALF / 4), sp1 - 1);
+            const float* kp = src_of(p, 0);
+            ku[it] = *(const float4*)(kp + d);
+            kw[it] = *(const float4*)(kp + d + HALF);
+            // only new keys are rotated: cached positions all read the chunk's first
+            // position (one cache line instead of a table row each)
+            const int pr = max(p, cpos0);
+            kcs[it] = *(const float4*)(a.cos_t + (size_t)pr * HALF + d);
+            ksn[it] = *(const float4*)(a.sin_t + (size_t)pr * HALF + d);
+        }
 #pragma unroll
-    for (int it = 0; it < VIT; it++) {
-        const int i = min(tid + it * 256, VI - 1);
-        const int d = (i % (HD / 4)) * 4, p = min(p0 + i / (HD / 4), p1 - 1);
-        vv[it] = *(const float4*)(src_of(p, kvd) + d);
-    }
+        for (int it = 0; it < VIT; it++) {
+            const int i = min(tid + it * 256, VI - 1);
+            const int d = (i % (HD / 4)) * 4, p = min(sp0 + i / (HD / 4), sp1 - 1);
+            vv[it] = *(const float4*)(src_of(p, kvd) + d);
+        }
+    };
+    load_sub(p0, min(p0 + P, p1));
     // q, rotated: 4 (d, d + HALF) pairs per item
     for (int i = tid; i < Q * (HALF / 4); i += 256) {
         const int q = i / (HALF / 4), d = (i % (HALF / 4)) * 4, r = q / G, j = q % G, row = row0 + r;
@@ -1465,48 +1481,6 @@ __global__ __launch_bounds__(256) void k_attn(AttnArgs a) {
             qs[q][d + HALF + e] = __fadd_rn(__fmul_rn(a2[e], cc[e]), __fmul_rn(a1[e], ss[e]));
         }
     }
-    // keys (rotated when new) and values to LDS
-#pragma unroll
-    for (int it = 0; it < KIT; it++) {
-        const int i = tid + it * 256;
-        if (i < KI) {
-            const int o = i / (HALF / 4), d = (i % (HALF / 4)) * 4, p = p0 + o;
-            const float a1[4] = {ku[it].x, ku[it].y, ku[it].z, ku[it].w};
-            const float a2[4] = {kw[it].x, kw[it].y, kw[it].z, kw[it].w};
-            const float cc[4] = {kcs[it].x, kcs[it].y, kcs[it].z, kcs[it].w};
-            const float ss[4] = {ksn[it].x, ksn[it].y, ksn[it].z, ksn[it].w};
-            const bool live = p < p1, rot = live && p >= cpos0;
-#pragma unroll
-            for (int e = 0; e < 4; e++) {
-                const float r1 = rot ? __fadd_rn(__fmul_rn(a1[e], cc[e]), __fmul_rn(-a2[e], ss[e])) : a1[e];
-                const float r2 = rot ? __fadd_rn(__fmul_rn(a2[e], cc[e]), __fmul_rn(a1[e], ss[e])) : a2[e];
-                ks[o][d + e] = live ? r1 : 0.0f;
-                ks[o][d + HALF + e] = live ? r2 : 0.0f;
-            }
-        }
-    }
-#pragma unroll
-    for (int it = 0; it < VIT; it++) {
-        const int i = tid + it * 256;
-        if (i < VI) {
-            const bool live = p0 + i / (HD / 4) < p1;
-            *(float4*)&vs[i / (HD / 4)][(i % (HD / 4)) * 4] =
-                make_float4(live ? vv[it].x : 0.0f, live ? vv[it].y : 0.0f, live ? vv[it].z : 0.0f,
-                            live ? vv[it].w : 0.0f);
-        }
-    }
-    __syncthreads();
-    // this group's new rows in the span go to the cache
-    {
-        const int n0 = max(max(p0, cpos0), cpos0 + row0 - crow0);
-        const int n1 = min(p1, cpos0 + row0 + nrows - crow0);
-        for (int i = tid; i < (n1 - n0) * HD; i += 256) {
-            const int p = n0 + i / HD, d = i % HD, o = p - p0;
-            const size_t at = ((blk(o >> 4) * a.nkv + h) * 16 + (p & 15)) * HD + d;
-            a.kc[at] = ks[o][d];
-            a.vc[at] = vs[o][d];
-        }
-    }
     // From kAttnMfmaQueries queries on, the scores and the weighted values run on f32 MFMA
     // (v_mfma_f32_16x16x4f32; A[i][k] in lane i + 16k, B[k][j] in lane j + 16k,
     // D[4(l/16) + r][l%16] in register r of lane l) over 16 x 16 tiles, with
@@ -1514,89 +1488,191 @@ __global__ __launch_bounds__(256) void k_attn(AttnArgs a) {
     // past Q hold stale values: they only reach output rows that are dropped.
     const bool mf = Q >= kAttnMfmaQueries;
     const int mtu = (Q + 15) >> 4;
-    if (mf) {
-        // scores, scaled, into pr
-        constexpr int NTP = P / 16;
-        for (int ti = wave; ti < mtu * NTP; ti += 4) {
-            const int mt = ti / NTP, nt = ti % NTP, kk = lane >> 4;
-            const float* qa = &qs[mt * 16 + (lane & 15)][kk];
-            const float* kb = &ks[nt * 16 + (lane & 15)][kk];
-            f32x4 c = {0.0f, 0.0f, 0.0f, 0.0f};
+    constexpr int NTD = HD / 16;
+    constexpr int TPW = ((QM + 15) / 16 * NTD + 3) / 4;  // weighted-value tiles per wave (MFMA)
+    constexpr int OI = (QM * HD + 255) / 256;            // weighted values per thread (VALU)
+    f32x4 oc[TPW];
+    float ov[OI];
 #pragma unroll
-            for (int d0 = 0; d0 < HD; d0 += 4) c = __builtin_amdgcn_mfma_f32_16x16x4f32(qa[d0], kb[d0], c, 0, 0, 0);
+    for (int j = 0; j < TPW; j++) oc[j] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-            for (int r = 0; r < 4; r++) pr[mt * 16 + 4 * kk + r][nt * 16 + (lane & 15)] = c[r] * a.scale;
+    for (int j = 0; j < OI; j++) ov[j] = 0.0f;
+    float* partq = a.part + ((size_t)wi * a.nkv + h) * QM * (HD + 4);
+    for (int s = 0; s < NS; s++) {
+        const int sp0 = p0 + s * P;
+        if (sp0 >= p1) break;
+        const int sp1 = min(sp0 + P, p1);
+        if (s > 0) __syncthreads();  // the previous sub-span's readers of ks, vs and pr are done
+        // keys (rotated when new) and values to LDS
+#pragma unroll
+        for (int it = 0; it < KIT; it++) {
+            const int i = tid + it * 256;
+            if (i < KI) {
+                const int o = i / (HALF / 4), d = (i % (HALF / 4)) * 4, p = sp0 + o;
+                const float a1[4] = {ku[it].x, ku[it].y, ku[it].z, ku[it].w};
+                const float a2[4] = {kw[it].x, kw[it].y, kw[it].z, kw[it].w};
+                const float cc[4] = {kcs[it].x, kcs[it].y, kcs[it].z, kcs[it].w};
+                const float ss[4] = {ksn[it].x, ksn[it].y, ksn[it].z, ksn[it].w};
+                const bool live = p < sp1, rot = live && p >= cpos0;
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    const float r1 = rot ? __fadd_rn(__fmul_rn(a1[e], cc[e]), __fmul_rn(-a2[e], ss[e])) : a1[e];
+                    const float r2 = rot ? __fadd_rn(__fmul_rn(a2[e], cc[e]), __fmul_rn(a1[e], ss[e])) : a2[e];
+                    ks[o][d + e] = live ? r1 : 0.0f;
+                    ks[o][d + HALF + e] = live ? r2 : 0.0f;
+                }
+            }
+        }
+#pragma unroll
+        for (int it = 0; it < VIT; it++) {
+            const int i = tid + it * 256;
+            if (i < VI) {
+                const bool live = sp0 + i / (HD / 4) < sp1;
+                *(float4*)&vs[i / (HD / 4)][(i % (HD / 4)) * 4] =
+                    make_float4(live ? vv[it].x : 0.0f, live ? vv[it].y : 0.0f, live ? vv[it].z : 0.0f,
+                                live ? vv[it].w : 0.0f);
+            }
         }
         __syncthreads();
-    }
-    // Scores and their softmax statistics in one pass: item i = q * P + o, so
-    // each wave holds whole queries (one per P lanes) and reduces them in
-    // registers.
-    for (int base = wave * 64; base < Q * P; base += 256) {
-        const int i = base + lane, q = i / P, o = i % P, p = p0 + o;
-        float sc = -INFINITY;
-        if (q < Q && p < p1 && p <= lim[q] && mf) {
-            sc = pr[q][o];
-        } else if (q < Q && p < p1 && p <= lim[q]) {
-            const float4* kr = (const float4*)&ks[o][0];
-            const float4* qr = (const float4*)&qs[q][0];
-            float acc = 0.0f;
+        // the next sub-span's loads fly while this one is scored
+        if (NS > 1 && sp1 < p1) load_sub(sp1, min(sp1 + P, p1));
+        // this group's new rows in the sub-span go to the cache
+        {
+            const int n0 = max(max(sp0, cpos0), cpos0 + row0 - crow0);
+            const int n1 = min(sp1, cpos0 + row0 + nrows - crow0);
+            for (int i = tid; i < (n1 - n0) * HD; i += 256) {
+                const int p = n0 + i / HD, d = i % HD, o = p - sp0;
+                const size_t at = ((blk((p - p0) >> 4) * a.nkv + h) * 16 + (p & 15)) * HD + d;
+                a.kc[at] = ks[o][d];
+                a.vc[at] = vs[o][d];
+            }
+        }
+        if (mf) {
+            // scores, scaled, into pr
+            constexpr int NTP = P / 16;
+            for (int ti = wave; ti < mtu * NTP; ti += 4) {
+                const int mt = ti / NTP, nt = ti % NTP, kk = lane >> 4;
+                const float* qa = &qs[mt * 16 + (lane & 15)][kk];
+                const float* kb = &ks[nt * 16 + (lane & 15)][kk];
+                f32x4 c = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-            for (int e4 = 0; e4 < HD / 4; e4++) {
-                const float4 kv = kr[e4], qv = qr[e4];
-                acc = fmaf(qv.x, kv.x, acc);
-                acc = fmaf(qv.y, kv.y, acc);
-                acc = fmaf(qv.z, kv.z, acc);
-                acc = fmaf(qv.w, kv.w, acc);
+                for (int d0 = 0; d0 < HD; d0 += 4) c = __builtin_amdgcn_mfma_f32_16x16x4f32(qa[d0], kb[d0], c, 0, 0, 0);
+#pragma unroll
+                for (int r = 0; r < 4; r++) pr[mt * 16 + 4 * kk + r][nt * 16 + (lane & 15)] = c[r] * a.scale;
             }
-            sc = acc * a.scale;
+            __syncthreads();
         }
-        const float mx = group_reduce<P, true>(sc);
-        const float e = (sc == -INFINITY) ? 0.0f : dev_exp(sc - mx);
-        const float sum = group_reduce<P, false>(e);
-        if (q < Q) {
-            pr[q][o] = e;
-            if (o == 0) {
-                float* dst = a.part + (((size_t)wi * a.nkv + h) * QM + q) * (HD + 4);
-                dst[0] = mx;
-                dst[1] = sum;
+        // Scores and their softmax statistics in one pass: item i = q * P + o, so
+        // each wave holds whole queries (one per P lanes) and reduces them in
+        // registers. Across sub-spans the exponentials are taken against the
+        // running max, and the running sum is rescaled to it.
+        for (int base = wave * 64; base < Q * P; base += 256) {
+            const int i = base + lane, q = i / P, o = i % P, p = sp0 + o;
+            float sc = -INFINITY;
+            if (q < Q && p < sp1 && p <= lim[q] && mf) {
+                sc = pr[q][o];
+            } else if (q < Q && p < sp1 && p <= lim[q]) {
+                const float4* kr = (const float4*)&ks[o][0];
+                const float4* qr = (const float4*)&qs[q][0];
+                float acc = 0.0f;
+#pragma unroll
+                for (int e4 = 0; e4 < HD / 4; e4++) {
+                    const float4 kv = kr[e4], qv = qr[e4];
+                    acc = fmaf(qv.x, kv.x, acc);
+                    acc = fmaf(qv.y, kv.y, acc);
+                    acc = fmaf(qv.z, kv.z, acc);
+                    acc = fmaf(qv.w, kv.w, acc);
+                }
+                sc = acc * a.scale;
+            }
+            float mx = group_reduce<P, true>(sc), mold = -INFINITY;
+            if (NS > 1) {
+                mold = q < Q ? mrun[q] : -INFINITY;
+                mx = fmaxf(mold, mx);
+            }
+            const float e = (sc == -INFINITY) ? 0.0f : dev_exp(sc - mx);
+            const float sum = group_reduce<P, false>(e);
+            if (q < Q) {
+                pr[q][o] = e;
+                if (o == 0) {
+                    if (NS == 1) {
+                        partq[q * (HD + 4)] = mx;
+                        partq[q * (HD + 4) + 1] = sum;
+                    } else {
+                        const float f = mold == -INFINITY ? 0.0f : dev_exp(mold - mx);
+                        fac[q] = f;
+                        lrun[q] = fmaf(lrun[q], f, sum);
+                        mrun[q] = mx;
+                    }
+                }
+            }
+        }
+        __syncthreads();
+        if (mf) {
+            // weighted values: O = fac O + P V, tile ti = wave + 4 j
+#pragma unroll
+            for (int j = 0; j < TPW; j++) {
+                const int ti = wave + 4 * j;
+                if (ti < mtu * NTD) {
+                    const int mt = ti / NTD, nd = ti % NTD, kk = lane >> 4;
+                    if (NS > 1) {
+#pragma unroll
+                        for (int r = 0; r < 4; r++) oc[j][r] *= fac[mt * 16 + 4 * kk + r];
+                    }
+                    const float* pa = &pr[mt * 16 + (lane & 15)][kk];
+                    const float* vb = &vs[kk][nd * 16 + (lane & 15)];
+#pragma unroll
+                    for (int k0 = 0; k0 < P; k0 += 4)
+                        oc[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(pa[k0], vb[k0 * (HD + 4)], oc[j], 0, 0, 0);
+                }
+            }
+        } else {
+            // weighted values: item tid + 256 j is (query, dim)
+#pragma unroll
+            for (int j = 0; j < OI; j++) {
+                const int i = tid + j * 256;
+                if (i < Q * HD) {
+                    const int q = i / HD, d = i % HD;
+                    const float4* prr = (const float4*)&pr[q][0];
+                    float acc = NS > 1 ? ov[j] * fac[q] : 0.0f;
+#pragma unroll
+                    for (int o4 = 0; o4 < P / 4; o4++) {
+                        const float4 w = prr[o4];
+                        acc = fmaf(w.x, vs[4 * o4][d], acc);
+                        acc = fmaf(w.y, vs[4 * o4 + 1][d], acc);
+                        acc = fmaf(w.z, vs[4 * o4 + 2][d], acc);
+                        acc = fmaf(w.w, vs[4 * o4 + 3][d], acc);
+                    }
+                    ov[j] = acc;
+                }
             }
         }
     }
-    __syncthreads();
+    // the work item's partial: max score, sum of exponentials, weighted values
+    if (NS > 1)
+        for (int q = tid; q < Q; q += 256) {
+            partq[q * (HD + 4)] = mrun[q];
+            partq[q * (HD + 4) + 1] = lrun[q];
+        }
     if (mf) {
-        // weighted values: O = P V
-        constexpr int NTD = HD / 16;
-        for (int ti = wave; ti < mtu * NTD; ti += 4) {
-            const int mt = ti / NTD, nd = ti % NTD, kk = lane >> 4;
-            const float* pa = &pr[mt * 16 + (lane & 15)][kk];
-            const float* vb = &vs[kk][nd * 16 + (lane & 15)];
-            f32x4 c = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-            for (int k0 = 0; k0 < P; k0 += 4)
-                c = __builtin_amdgcn_mfma_f32_16x16x4f32(pa[k0], vb[k0 * (HD + 4)], c, 0, 0, 0);
+        for (int j = 0; j < TPW; j++) {
+            const int ti = wave + 4 * j;
+            if (ti < mtu * NTD) {
+                const int mt = ti / NTD, nd = ti % NTD, kk = lane >> 4;
 #pragma unroll
-            for (int r = 0; r < 4; r++) {
-                const int q = mt * 16 + 4 * kk + r;
-                if (q < Q) a.part[(((size_t)wi * a.nkv + h) * QM + q) * (HD + 4) + 4 + nd * 16 + (lane & 15)] = c[r];
+                for (int r = 0; r < 4; r++) {
+                    const int q = mt * 16 + 4 * kk + r;
+                    if (q < Q) partq[q * (HD + 4) + 4 + nd * 16 + (lane & 15)] = oc[j][r];
+                }
             }
         }
-        return;
-    }
-    // weighted values
-    for (int i = tid; i < Q * HD; i += 256) {
-        const int q = i / HD, d = i % HD;
-        const float4* prr = (const float4*)&pr[q][0];
-        float acc = 0.0f;
+    } else {
 #pragma unroll
-        for (int o4 = 0; o4 < P / 4; o4++) {
-            const float4 w = prr[o4];
-            acc = fmaf(w.x, vs[4 * o4][d], acc);
-            acc = fmaf(w.y, vs[4 * o4 + 1][d], acc);
-            acc = fmaf(w.z, vs[4 * o4 + 2][d], acc);
-            acc = fmaf(w.w, vs[4 * o4 + 3][d], acc);
+        for (int j = 0; j < OI; j++) {
+            const int i = tid + j * 256;
+            if (i < Q * HD) partq[(i / HD) * (HD + 4) + 4 + i % HD] = ov[j];
         }
-        a.part[(((size_t)wi * a.nkv + h) * QM + q) * (HD + 4) + 4 + d] = acc;
     }
 }
 
@@ -1617,7 +1693,12 @@ __global__ __launch_bounds__(64) void k_merge_pieces(AttnArgs a, int m, void* __
 
 template <int HD, int P, int QM>
 static void attention_hd(hipStream_t st, const AttnArgs& a, int m, int ck, Pieces& out) {
-    hipLaunchKernelGGL((k_attn<HD, P, QM>), dim3(a.nkv, a.n_wi), dim3(256), 0, st, a);
+    if (a.ns >= 4 && 4 * P <= 128)
+        hipLaunchKernelGGL((k_attn<HD, P, QM, (4 * P <= 128 ? 4 : 1)>), dim3(a.nkv, a.n_wi), dim3(256), 0, st, a);
+    else if (a.ns >= 2 && 2 * P <= 128)
+        hipLaunchKernelGGL((k_attn<HD, P, QM, (2 * P <= 128 ? 2 : 1)>), dim3(a.nkv, a.n_wi), dim3(256), 0, st, a);
+    else
+        hipLaunchKernelGGL((k_attn<HD, P, QM, 1>), dim3(a.nkv, a.n_wi), dim3(256), 0, st, a);
     if (ck < 0) return;  // the consumer merges the spans itself
     if (ck == BF16)
         hipLaunchKernelGGL((k_merge_pieces<HD, QM, BF16>), dim3(out.kb, out.passes), dim3(64), 0, st, a, m, out.a,

@@ -336,3 +336,33 @@ def test_output_projection_merge_matches_separate_merge(ctx, shape, monkeypatch)
         ol = om.forward(okv, [(toks, pos, table, 2)])
         assert np.abs(lg - ol).max() < 1e-4 * np.abs(ol).max()
         pos += len(toks)
+
+
+@pytest.mark.parametrize("hd,heads,kv_heads,n", [(64, 16, 4, 1100), (128, 8, 2, 700)], ids=["hd64", "hd128"])
+def test_long_gqa_prefill_runs_multi_span_attention(ctx, hd, heads, kv_heads, n):
+    """A prefill of n tokens whose row groups hold 32 queries (8 rows x GQA 4)
+    launches more than 1024 attention work items of one span, so each item
+    covers 128 positions: 2 (hd 64) or 4 (hd 128) sub-spans whose loads
+    overlap the previous sub-span's scores, merged online. All logits and the
+    hidden states against the oracle, and the cache slots."""
+    from ferrolm_amd.synth import random_model
+    from ferrolm_amd.weights import Config
+    cfg = Config(vocab=512, hidden=heads * hd, intermediate=512, layers=2, heads=heads, kv_heads=kv_heads,
+                 head_dim=hd, rms_eps=1e-5, rope_theta=500000.0, max_position=2048)
+    hm = random_model(cfg, seed=51, std=0.05)
+    prompt = [int(x) for x in np.random.default_rng(52).integers(3, 500, n)]
+    table, blocks = scattered_table(n)
+    m = gpu.Model(ctx, hm)
+    kv = gpu.KvCache(ctx, hm.cfg, blocks)
+    out = gpu.forward(ctx, m, kv, [(prompt, 0, table, gpu.LOGITS_ALL)], hidden=True)
+    om = oracle.Model(hm)
+    okv = om.kv(blocks)
+    ol, oh = om.forward(okv, [(prompt, 0, table, 2)], hidden=True)
+    assert np.abs(out.logits - ol).max() < 1e-4 * np.abs(ol).max()
+    rel = np.linalg.norm(out.hidden - oh, axis=-1) / np.linalg.norm(oh, axis=-1)
+    assert rel.max() < 1e-4, rel.max()
+    for li in range(cfg.layers):
+        gk, gv = kv.layer(li)
+        ok, ov = okv.layer(li)
+        assert np.abs(gk - ok).max() <= 1e-4 * np.abs(ok).max()
+        assert np.abs(gv - ov).max() <= 1e-4 * np.abs(ov).max()
