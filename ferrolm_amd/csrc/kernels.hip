@@ -34,6 +34,26 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint16_t u16x8 __attribute__((ext_vector_type(8)));
 typedef int8_t i8x8 __attribute__((ext_vector_type(8)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+
+// A load marked non-temporal (NT) or plain. Data read once per step (quantized
+// weights and their scales, the lm_heads, the KV cache) is loaded
+// non-temporally: such lines are not kept in the 256 MB memory-side cache,
+// which then holds what a step reads again (a bf16 draft's layer weights,
+// 212 MB at 135M, read by every draft round). Measured: a 200 MB buffer stays
+// resident across a 1.2 GB non-temporal stream and is evicted by a plain one.
+template <bool NT, typename T>
+__device__ __forceinline__ T ld_nt(const T* p) {
+    if constexpr (NT)
+        return __builtin_nontemporal_load(p);
+    else
+        return *p;
+}
+__device__ __forceinline__ float4 ld_nt_f4(const float* p) {
+    const f32x4 v = __builtin_nontemporal_load((const f32x4*)p);
+    return make_float4(v[0], v[1], v[2], v[3]);
+}
 
 __device__ __forceinline__ float bf16_bits_to_f32(uint32_t h) { return __uint_as_float(h << 16); }
 
@@ -435,6 +455,8 @@ void launch_embed(hipStream_t st, const uint32_t* tokens, int stride, const uint
 template <int KIND, int NT, int EPI, int PG, int WMAX = 8, bool AM = false>
 __global__ __launch_bounds__(64 * WMAX) void k_gemv(const GemvArgs a) {
     constexpr bool Q = KIND != BF16;
+    // weights read once per step: quantized ones and the lm_heads (non-temporal loads)
+    constexpr bool WNT = Q || EPI == EPI_ARGMAX;
     // chunks loaded ahead per wave: about 16 B x 4 per lane and tile of weights in
     // flight; with 16 waves (4 per SIMD, 128 VGPRs) half as many, the other waves
     // of the SIMD covering each one's wait
@@ -589,15 +611,16 @@ __global__ __launch_bounds__(64 * WMAX) void k_gemv(const GemvArgs a) {
             for (int t = 0; t < NT; t++) {
                 const size_t tile = tile0 + t;
                 if (KIND == INT4) {
-                    wq[u][t][0] = ((const u32x4*)a.W)[(tile * KC + cc) * 64 + lane];
+                    wq[u][t][0] = ld_nt<WNT>((const u32x4*)a.W + (tile * KC + cc) * 64 + lane);
                 } else if (KIND == INT8) {
-                    wq[u][t][0] = ((const u32x4*)a.W)[(tile * (KB >> 1) + 2 * cc) * 64 + lane];
-                    wq[u][t][1] = ((const u32x4*)a.W)[(tile * (KB >> 1) + 2 * cc + 1) * 64 + lane];
+                    wq[u][t][0] = ld_nt<WNT>((const u32x4*)a.W + (tile * (KB >> 1) + 2 * cc) * 64 + lane);
+                    wq[u][t][1] = ld_nt<WNT>((const u32x4*)a.W + (tile * (KB >> 1) + 2 * cc + 1) * 64 + lane);
                 } else {
 #pragma unroll
-                    for (int j = 0; j < 4; j++) wb[u][t][j] = ((const bf16x8*)a.W)[(tile * KB + kb + j) * 64 + lane];
+                    for (int j = 0; j < 4; j++)
+                        wb[u][t][j] = ld_nt<WNT>((const bf16x8*)a.W + (tile * KB + kb + j) * 64 + lane);
                 }
-                if (Q) sv[u][t] = a.S[(tile * KC + cc) * 64 + (lane & 15) * 4 + (lane >> 4)];
+                if (Q) sv[u][t] = ld_nt<WNT>(a.S + (tile * KC + cc) * 64 + (lane & 15) * 4 + (lane >> 4));
             }
         }
         // keep the scheduler from sinking loads of the batch below its first MFMA
@@ -1036,6 +1059,7 @@ template <int KIND, int EPI, int RTW>
 __global__ __launch_bounds__(512) void k_gemm(const GemvArgs a) {
     constexpr int NW = 8, NTHR = 64 * NW;
     constexpr bool Q = KIND != BF16;
+    constexpr bool WNT = Q || EPI == EPI_ARGMAX;  // weights read once per step: non-temporal
     constexpr bool NEED_R = EPI == EPI_QKV || EPI == EPI_SILU || EPI == EPI_ARGMAX;
     constexpr int YS = 68;  // LDS row stride of the 16 RTW x 64 tile
     // the cross-wave tree: four partial tiles (the lanes' layout), then the tile
@@ -1087,14 +1111,19 @@ __global__ __launch_bounds__(512) void k_gemm(const GemvArgs a) {
 #pragma unroll
         for (int t = 0; t < 4; t++) {
             const size_t tile = t_[t];
-            if (KIND == INT4)
-                w4[t] = ((const uint2*)a.W)[((tile * KC + c) * 64 + lane) * 2 + half];
-            else if (KIND == INT8)
-                w8[t] = ((const u32x4*)a.W)[(tile * (KB >> 1) + pr) * 64 + lane];
-            else
+            if (KIND == INT4) {
+                const u32x2 v = ld_nt<WNT>((const u32x2*)a.W + ((tile * KC + c) * 64 + lane) * 2 + half);
+                w4[t] = make_uint2(v[0], v[1]);
+            } else if (KIND == INT8) {
+                w8[t] = ld_nt<WNT>((const u32x4*)a.W + (tile * (KB >> 1) + pr) * 64 + lane);
+            } else {
 #pragma unroll
-                for (int j = 0; j < 2; j++) wb[t][j] = ((const bf16x8*)a.W)[(tile * KB + kb0 + j) * 64 + lane];
-            if (Q) sv[t] = ((const float2*)a.S)[((tile * KC + c) * 16 + (lane & 15)) * 2 + half];
+                for (int j = 0; j < 2; j++) wb[t][j] = ld_nt<WNT>((const bf16x8*)a.W + (tile * KB + kb0 + j) * 64 + lane);
+            }
+            if (Q) {
+                const f32x2 v = ld_nt<WNT>((const f32x2*)a.S + ((tile * KC + c) * 16 + (lane & 15)) * 2 + half);
+                sv[t] = make_float2(v[0], v[1]);
+            }
         }
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
@@ -1449,8 +1478,8 @@ __global__ __launch_bounds__(256, 2) void k_attn(AttnArgs a) {
             const int i = min(tid + it * 256, KI - 1);
             const int d = (i % (HALF / 4)) * 4, p = min(sp0 + i / (HALF / 4), sp1 - 1);
             const float* kp = src_of(p, 0);
-            ku[it] = *(const float4*)(kp + d);
-            kw[it] = *(const float4*)(kp + d + HALF);
+            ku[it] = ld_nt_f4(kp + d);
+            kw[it] = ld_nt_f4(kp + d + HALF);
             // only new keys are rotated: cached positions all read the chunk's first
             // position (one cache line instead of a table row each)
             const int pr = max(p, cpos0);
@@ -1461,7 +1490,7 @@ __global__ __launch_bounds__(256, 2) void k_attn(AttnArgs a) {
         for (int it = 0; it < VIT; it++) {
             const int i = min(tid + it * 256, VI - 1);
             const int d = (i % (HD / 4)) * 4, p = min(sp0 + i / (HD / 4), sp1 - 1);
-            vv[it] = *(const float4*)(src_of(p, kvd) + d);
+            vv[it] = ld_nt_f4(src_of(p, kvd) + d);
         }
     };
     load_sub(p0, min(p0 + P, p1));
