@@ -60,6 +60,8 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-profile", action="store_true")
     ap.add_argument("--batch", type=int, default=0, help="sequences for configs 3/4 (default: the config's own)")
+    ap.add_argument("--awq", action="store_true",
+                    help="time the AWQ alpha search (fg_awq_search) of one 1.7B-shape layer instead")
     ap.add_argument("--copy-calib", type=int, default=0, metavar="MIB",
                     help="only run a plain device copy of MIB MiB and exit (calibrates rocprofv3 FETCH_SIZE/WRITE_SIZE)")
     a = ap.parse_args()
@@ -77,6 +79,9 @@ def main() -> int:
         torch.cuda.synchronize()
         log(f"copy calibration: 3 x torch.neg over {a.copy_calib} MiB")
         return 0
+
+    if a.awq:
+        return run_awq(a)
 
     from ferrolm_amd import gpu, spec, synth
     from ferrolm_amd.weights import KIND_NAMES
@@ -290,6 +295,78 @@ def run_batched(a, wl, ctx, target, draft) -> int:
                                f"shuffled 16-token blocks", "batch": B, "k": k},
         "verify_step_us": round(verify_us, 2), "draft_us": round(draft_us, 2), "acceptance": round(acceptance, 4),
         "roofline": roofline, "cpu_baseline": None, "parity": None,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+def run_awq(a) -> int:
+    """--awq: the AWQ alpha search with its final quantization (fg_awq_search,
+    src/awq.rs:152-217) over the four projections of one layer of the
+    SmolLM2-1.7B shape (q/k/v 6144x2048, o 2048x2048, gate/up 16384x2048,
+    down 2048x8192), int4, 256 calibration rows per projection (N(0, 1), 1% of
+    the channels x 20; the reference's calibrate keeps 256 rows in its test).
+    value = layers per second, wall time of the four calls, host-device copies
+    included. cpu_baseline: the C oracle's search over the same four
+    projections on the host cores, whose alphas, errors, codes and scales
+    must equal the device's (parity)."""
+    from ferrolm_amd import gpu, host
+    from ferrolm_amd.weights import INT4, bf16_to_f32, shape
+
+    cfg = shape("smollm2-1.7b")
+    H, inter = cfg.hidden, cfg.intermediate
+    projs = [("qkv", (cfg.heads + 2 * cfg.kv_heads) * cfg.head_dim, H), ("o", H, cfg.heads * cfg.head_dim),
+             ("gate_up", 2 * inter, H), ("down", H, inter)]
+    m = 256
+    rng = np.random.default_rng(a.seed)
+    mats = []
+    for i, (name, rows, kdim) in enumerate(projs):
+        w = bf16_to_f32(host.random_bf16(a.seed, 900 + i, rows, kdim, 0.02))
+        x = rng.standard_normal((m, kdim)).astype(np.float32)
+        x[:, rng.choice(kdim, kdim // 100, replace=False)] *= 20.0
+        mats.append((name, w, x))
+    ctx = gpu.Context(0)
+    gpu.awq_search(ctx, INT4, mats[1][1][:64, :256].copy(), mats[1][2][:16, :256].copy())  # warm the path
+    per, res = {}, {}
+    t_all = time.perf_counter()
+    for name, w, x in mats:
+        t = time.perf_counter()
+        res[name] = gpu.awq_search(ctx, INT4, w, x)
+        per[name] = time.perf_counter() - t
+        log(f"device awq search {name} {w.shape[0]}x{w.shape[1]}: {per[name] * 1e3:.1f} ms, alpha {res[name][1]:.1f}")
+    dev = time.perf_counter() - t_all
+    t = time.perf_counter()
+    gpu.quantize(ctx, INT4, mats[2][1])
+    tq = time.perf_counter() - t
+    cpu, parity = None, None
+    if not a.no_cpu:
+        import oracle
+        threads = int(os.environ.get("OMP_NUM_THREADS", len(os.sched_getaffinity(0))))
+        oracle.threads(threads)
+        same = 0
+        tc = time.perf_counter()
+        for name, w, x in mats:
+            o = oracle.awq_search(INT4, w, x)
+            d = res[name]
+            same += int(d[1] == o[1] and d[2] == o[2] and d[3] == o[3] and np.array_equal(d[0], o[0])
+                        and np.array_equal(d[4].q, o[4].q) and np.array_equal(d[4].s, o[4].s))
+        ce = time.perf_counter() - tc
+        cpu = {"value": round(1.0 / ce, 4), "unit": "layers/s", "cores": threads, "kind": "port",
+               "sample": f"the same four projections, C oracle, {threads} threads, {ce:.1f}s"}
+        parity = {"projections_compared": len(mats), "projections_identical": same}
+        log(f"cpu baseline: {ce:.1f} s per layer; parity {same}/{len(mats)}")
+    flops = sum(2.0 * m * w.shape[0] * w.shape[1] * 12 for _, w, _ in mats)
+    line = {
+        "metric": "AWQ alpha search + quantization, one SmolLM2-1.7B-shape layer, int4, 256 calibration rows",
+        "value": round(1.0 / dev, 3), "unit": "layers/s", "n_gpus": 1, "steps": 1, "warmup": 1,
+        "ms_per_step": round(dev * 1e3, 2), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "f32", "data": "synthetic",
+        "config": {"workload": "awq: 4 projections of one 1.7B-shape layer, int4, m=256", "calibration_rows": m},
+        "per_projection_ms": {k: round(v * 1e3, 1) for k, v in per.items()},
+        "alphas": {k: r[1] for k, r in res.items()},
+        "quantize_gate_up_ms": round(tq * 1e3, 2),
+        "matmul_fma_tflops": round(flops / dev / 1e12, 2),
+        "roofline": None, "cpu_baseline": cpu, "parity": parity,
     }
     print(json.dumps(line), flush=True)
     return 0

@@ -3,6 +3,7 @@
 // speculative step. Each entry point names the reference interface it
 // replaces in the header.
 #include "ferro_gpu.h"
+#include "ferro_host.h"
 #include "internal.h"
 
 #include <algorithm>
@@ -1403,6 +1404,135 @@ int fg_matmul_device(fg_ctx* ctx, const fg_mat* w, const float* x_dev, int32_t m
     layout_mat(d, m, p, &xb, &yb, &bb, wk, ctx->ws);
     matmul_launch(ctx, d, p, wk, x_dev, m, nullptr, y_dev);
     HIPCHK(hipGetLastError());
+    return 0;
+}
+
+// ---- load-time quantization on the device --------------------------------
+
+namespace {
+// A device allocation freed when it leaves scope (hipFree waits for the
+// device, so queued work that uses it has finished).
+struct DevBuf {
+    void* p = nullptr;
+    DevBuf() = default;
+    DevBuf(const DevBuf&) = delete;
+    ~DevBuf() {
+        if (p) (void)hipFree(p);
+    }
+    float* f() const { return (float*)p; }
+    uint8_t* u8() const { return (uint8_t*)p; }
+};
+}  // namespace
+
+static int dev_alloc(DevBuf& b, size_t bytes) {
+    if (hipMalloc(&b.p, std::max<size_t>(bytes, 256)) != hipSuccess) {
+        b.p = nullptr;
+        (void)hipGetLastError();
+        return fail(FG_E_NOMEM, "device allocation failed");
+    }
+    return 0;
+}
+
+static int quant_shape(int32_t kind, int32_t rows, int32_t cols) {
+    if (kind != FG_INT8 && kind != FG_INT4) return fail(FG_E_ARG, "format must be FG_INT8 or FG_INT4");
+    if (rows <= 0 || cols <= 0) return fail(FG_E_ARG, "empty matrix");
+    if (rows % 32 || cols % 32) return fail(FG_E_SHAPE, "quantized matrices need rows and cols that are multiples of 32");
+    return 0;
+}
+
+int fg_quantize(fg_ctx* ctx, int32_t kind, int32_t rows, int32_t cols, const float* w, const float* importance,
+                uint8_t* q, float* s) {
+    if (!ctx || !w || !q || !s) return fail(FG_E_ARG, "null pointer");
+    int rc;
+    if ((rc = quant_shape(kind, rows, cols))) return rc;
+    HIPCHK(hipSetDevice(ctx->device));
+    hipStream_t st = ctx->stream;
+    const size_t n = (size_t)rows * cols, qb = kind == FG_INT8 ? n : n / 2, sn = n / 32;
+    DevBuf dw, di, dq, ds;
+    if ((rc = dev_alloc(dw, n * 4)) || (rc = dev_alloc(di, (size_t)cols * 4)) || (rc = dev_alloc(dq, qb)) ||
+        (rc = dev_alloc(ds, sn * 4)))
+        return rc;
+    HIPCHK(hipMemcpyAsync(dw.p, w, n * 4, hipMemcpyHostToDevice, st));
+    if (importance) HIPCHK(hipMemcpyAsync(di.p, importance, (size_t)cols * 4, hipMemcpyHostToDevice, st));
+    launch_quantize(st, kind, rows, cols, dw.f(), importance ? di.f() : nullptr, dq.u8(), ds.f());
+    HIPCHK(hipGetLastError());
+    HIPCHK(hipMemcpyAsync(q, dq.p, qb, hipMemcpyDeviceToHost, st));
+    HIPCHK(hipMemcpyAsync(s, ds.p, sn * 4, hipMemcpyDeviceToHost, st));
+    HIPCHK(hipStreamSynchronize(st));
+    return 0;
+}
+
+int fg_awq_search(fg_ctx* ctx, int32_t kind, int32_t rows, int32_t k, const float* w, int32_t m, const float* cal,
+                  float* scales, fg_awq_choice* choice, uint8_t* q, float* s) {
+    if (!ctx || !w || !cal || !scales || !choice || !q || !s) return fail(FG_E_ARG, "null pointer");
+    int rc;
+    if ((rc = quant_shape(kind, rows, k))) return rc;
+    if (m <= 0) return fail(FG_E_ARG, "no calibration rows");
+    HIPCHK(hipSetDevice(ctx->device));
+    hipStream_t st = ctx->stream;
+    const size_t rk = (size_t)rows * k, mk = (size_t)m * k, ny = (size_t)m * rows;
+    const size_t qb = kind == FG_INT8 ? rk : rk / 2, sn = rk / 32;
+    // channel statistics on the host (f64 sums in row order)
+    std::vector<float> am(k), sq(k), sc(k), imp(k), best_s(k);
+    fh_awq_stats(cal, m, k, am.data(), sq.data());
+    constexpr int kSteps = 11;  // alpha = 0, 0.1, ..., 1
+    DevBuf dw, dws, dx, dxs, dyref, dy, dsc, dimp, dq, ds, derr;
+    if ((rc = dev_alloc(dw, rk * 4)) || (rc = dev_alloc(dws, rk * 4)) || (rc = dev_alloc(dx, mk * 4)) ||
+        (rc = dev_alloc(dxs, mk * 4)) || (rc = dev_alloc(dyref, ny * 4)) || (rc = dev_alloc(dy, kSteps * ny * 4)) ||
+        (rc = dev_alloc(dsc, (size_t)k * 4)) || (rc = dev_alloc(dimp, (size_t)k * 4)) || (rc = dev_alloc(dq, qb)) ||
+        (rc = dev_alloc(ds, sn * 4)) || (rc = dev_alloc(derr, kSteps * 8)))
+        return rc;
+    HIPCHK(hipMemcpyAsync(dw.p, w, rk * 4, hipMemcpyHostToDevice, st));
+    HIPCHK(hipMemcpyAsync(dx.p, cal, mk * 4, hipMemcpyHostToDevice, st));
+    // the reference output, with the unquantized weights as bf16 (Matrix::from_f32)
+    launch_mm_exact(st, BF16, dx.f(), m, k, dw.f(), nullptr, nullptr, rows, dyref.f());
+    HIPCHK(hipGetLastError());
+    // imp = sq / s^2 + 1e-8 and the scaled operands, then the quantizer (apply, src/awq.rs:152-165)
+    auto apply = [&](const float* sv) -> int {
+        for (int32_t c = 0; c < k; c++) imp[c] = sq[c] / (sv[c] * sv[c]) + 1e-8f;
+        HIPCHK(hipMemcpyAsync(dsc.p, sv, (size_t)k * 4, hipMemcpyHostToDevice, st));
+        HIPCHK(hipMemcpyAsync(dimp.p, imp.data(), (size_t)k * 4, hipMemcpyHostToDevice, st));
+        launch_scale_cols(st, dw.f(), (int64_t)rk, k, dsc.f(), 0, dws.f());
+        launch_quantize(st, kind, rows, k, dws.f(), dimp.f(), dq.u8(), ds.f());
+        HIPCHK(hipGetLastError());
+        return 0;
+    };
+    // every alpha's product first, then their error sums side by side
+    std::vector<std::vector<float>> scs(kSteps);
+    for (int step = 0; step < kSteps; step++) {
+        scs[step].resize(k);
+        fh_awq_scales(am.data(), k, (float)step / 10.0f, scs[step].data());
+        if ((rc = apply(scs[step].data()))) return rc;
+        launch_scale_cols(st, dx.f(), (int64_t)mk, k, dsc.f(), 1, dxs.f());
+        launch_mm_exact(st, kind, dxs.f(), m, k, nullptr, dq.u8(), ds.f(), rows, dy.f() + (size_t)step * ny);
+        HIPCHK(hipGetLastError());
+        // the scales and importance buffers are rewritten by the next step's copies
+        HIPCHK(hipStreamSynchronize(st));
+    }
+    launch_sq_err(st, dy.f(), (int64_t)ny, kSteps, dyref.f(), (int64_t)ny, (double*)derr.p);
+    HIPCHK(hipGetLastError());
+    double errs[kSteps];
+    HIPCHK(hipMemcpyAsync(errs, derr.p, sizeof(errs), hipMemcpyDeviceToHost, st));
+    HIPCHK(hipStreamSynchronize(st));
+    double best = INFINITY, plain = errs[0];
+    float best_alpha = 0.0f;
+    bool have = false;
+    for (int step = 0; step < kSteps; step++)
+        if (!have || errs[step] < best) {  // the first minimum, as the reference's search
+            have = true;
+            best = errs[step];
+            best_alpha = (float)step / 10.0f;
+            best_s = scs[step];
+        }
+    if ((rc = apply(best_s.data()))) return rc;
+    HIPCHK(hipMemcpyAsync(q, dq.p, qb, hipMemcpyDeviceToHost, st));
+    HIPCHK(hipMemcpyAsync(s, ds.p, sn * 4, hipMemcpyDeviceToHost, st));
+    HIPCHK(hipStreamSynchronize(st));
+    std::memcpy(scales, best_s.data(), (size_t)k * 4);
+    choice->alpha = best_alpha;
+    choice->_pad = 0;
+    choice->error_plain = plain;
+    choice->error_awq = best;
     return 0;
 }
 

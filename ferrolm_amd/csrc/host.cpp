@@ -149,4 +149,38 @@ int fh_quantize(int32_t kind, int32_t rows, int32_t cols, const float* w, const 
     return 0;
 }
 
+// stats (src/awq.rs:128-142): f64 sums in row order, divided by max(m, 1).
+int fh_awq_stats(const float* cal, int32_t m, int32_t k, float* abs_mean, float* sq_mean) {
+    if (!cal || !abs_mean || !sq_mean || m < 0 || k <= 0) return FG_E_ARG;
+    std::vector<double> a((size_t)k, 0.0), q((size_t)k, 0.0);
+    for (int32_t i = 0; i < m; i++)
+        for (int32_t c = 0; c < k; c++) {
+            const float v = cal[(size_t)i * k + c];
+            a[c] += (double)std::fabs(v);
+            q[c] += (double)v * (double)v;
+        }
+    const double n = (double)std::max(m, 1);
+    for (int32_t c = 0; c < k; c++) {
+        abs_mean[c] = (float)(a[c] / n);
+        sq_mean[c] = (float)(q[c] / n);
+    }
+    return 0;
+}
+
+// scales (src/awq.rs:144-150): f32 powf (libm, as f32::powf), f32::max/min
+// fold, normalised by max(sqrt(max * min), 1e-8), floored at 1e-4.
+int fh_awq_scales(const float* abs_mean, int32_t k, float alpha, float* s) {
+    if (!abs_mean || !s || k <= 0) return FG_E_ARG;
+    float mx = 0.0f, mn = 3.40282347e38f;
+    for (int32_t c = 0; c < k; c++) {
+        const float v = powf(std::fmax(abs_mean[c], 1e-5f), alpha);
+        s[c] = v;
+        mx = std::fmax(mx, v);
+        mn = std::fmin(mn, v);
+    }
+    const float norm = std::fmax(std::sqrt(mx * mn), 1e-8f);
+    for (int32_t c = 0; c < k; c++) s[c] = std::fmax(s[c] / norm, 1e-4f);
+    return 0;
+}
+
 }  // extern "C"

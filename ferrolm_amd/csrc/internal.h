@@ -207,4 +207,17 @@ void launch_accept_sampled(hipStream_t st, int n_seqs, int k, const SampleParams
                            const uint32_t* am, const SampleRows& p, const SampleRows& q, uint64_t* rng,
                            uint32_t* out_tokens, int32_t* out_count, int32_t* out_accepted);
 
+// Load-time quantization and the AWQ search (quant.hip). w, imp, x are f32
+// device arrays; q / s the QMatrix codes and scales (src/quant.rs:64-76).
+void launch_quantize(hipStream_t st, int kind, int rows, int cols, const float* w, const float* imp, uint8_t* q,
+                     float* s);
+void launch_scale_cols(hipStream_t st, const float* src, int64_t n, int k, const float* s, int div, float* dst);
+// kind BF16: W is wf (f32, rounded to bf16 as read); INT8/INT4: the QMatrix q, s
+void launch_mm_exact(hipStream_t st, int kind, const float* x, int m, int K, const float* wf, const uint8_t* q,
+                     const float* s, int rows, float* y);
+// out[b] = mean over t < n of (y[b * ystride + t] - yref[t])^2, f64, summed in t order
+// (n a multiple of 4, ystride of 4)
+void launch_sq_err(hipStream_t st, const float* y, int64_t ystride, int count, const float* yref, int64_t n,
+                   double* out);
+
 }  // namespace fg

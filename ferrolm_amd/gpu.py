@@ -12,7 +12,7 @@ from pathlib import Path
 
 import numpy as np
 
-from .weights import BF16, Config, HostModel, Matrix
+from .weights import BF16, INT8, Config, HostModel, Matrix
 
 PKG = Path(__file__).resolve().parent
 LIB_PATH = PKG / "libferro_gpu.so"
@@ -60,6 +60,11 @@ class FgSampling(C.Structure):
 
 
 u64p = C.POINTER(C.c_uint64)
+
+
+class FgAwqChoice(C.Structure):
+    _fields_ = [("alpha", C.c_float), ("_pad", C.c_int32), ("error_plain", C.c_double),
+                ("error_awq", C.c_double)]
 
 
 @dataclass
@@ -117,6 +122,9 @@ EXPORTS = {
     "fg_mat_destroy": (None, [C.c_void_p]),
     "fg_matmul": (C.c_int, [C.c_void_p, C.c_void_p, f32p, C.c_int32, f32p, f32p]),
     "fg_matmul_device": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_int32, C.c_void_p]),
+    "fg_quantize": (C.c_int, [C.c_void_p, C.c_int32, C.c_int32, C.c_int32, f32p, f32p, u8p, f32p]),
+    "fg_awq_search": (C.c_int, [C.c_void_p, C.c_int32, C.c_int32, C.c_int32, f32p, C.c_int32, f32p, f32p,
+                                C.POINTER(FgAwqChoice), u8p, f32p]),
 }
 
 _lib = None
@@ -413,3 +421,37 @@ class Mat:
 
     def __del__(self):
         self.close()
+
+
+def _qmatrix_buffers(kind: int, rows: int, cols: int):
+    q = np.zeros(rows * cols // (1 if kind == INT8 else 2), np.uint8)
+    s = np.zeros(rows * cols // 32, np.float32)
+    return q, s
+
+
+def quantize(ctx: Context, kind: int, w: np.ndarray, importance: np.ndarray | None = None) -> Matrix:
+    """QMatrix::quantize (src/quant.rs:78-143) on the device (fg_quantize):
+    the reference's codes and scales for a rows x cols f32 matrix."""
+    w = np.ascontiguousarray(w, np.float32)
+    rows, cols = w.shape
+    q, s = _qmatrix_buffers(kind, rows, cols)
+    imp = None if importance is None else np.ascontiguousarray(importance, np.float32)
+    check(lib().fg_quantize(ctx.h, kind, rows, cols, ptr(w, f32p), ptr(imp, f32p), ptr(q, u8p), ptr(s, f32p)))
+    return Matrix(kind, rows, cols, q=q, s=s)
+
+
+def awq_search(ctx: Context, kind: int, w: np.ndarray, cal: np.ndarray):
+    """awq::search + apply (src/awq.rs:152-217) on the device
+    (fg_awq_search): returns (scales, alpha, error_plain, error_awq, Matrix)
+    for weights w (rows x k) and calibration rows cal (m x k)."""
+    w = np.ascontiguousarray(w, np.float32)
+    cal = np.ascontiguousarray(cal, np.float32)
+    rows, k = w.shape
+    if cal.ndim != 2 or cal.shape[1] != k:
+        raise FgError("calibration rows must have the projection's input width")
+    q, s = _qmatrix_buffers(kind, rows, k)
+    sc = np.zeros(k, np.float32)
+    ch = FgAwqChoice()
+    check(lib().fg_awq_search(ctx.h, kind, rows, k, ptr(w, f32p), cal.shape[0], ptr(cal, f32p), ptr(sc, f32p),
+                              C.byref(ch), ptr(q, u8p), ptr(s, f32p)))
+    return sc, float(ch.alpha), float(ch.error_plain), float(ch.error_awq), Matrix(kind, rows, k, q=q, s=s)

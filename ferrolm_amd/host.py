@@ -1,5 +1,6 @@
 """ctypes binding of the load-time host routines (include/ferro_host.h):
-synthetic weights and the group-32 quantizer. They run on the CPU."""
+synthetic weights, the group-32 quantizer and the AWQ channel statistics and
+scales. They run on the CPU."""
 from __future__ import annotations
 
 import ctypes as C
@@ -26,6 +27,11 @@ def lib():
         l.fh_quantize.restype = C.c_int
         l.fh_quantize.argtypes = [C.c_int32, C.c_int32, C.c_int32, C.POINTER(C.c_float), C.POINTER(C.c_float),
                                   C.POINTER(C.c_uint8), C.POINTER(C.c_float)]
+        l.fh_awq_stats.restype = C.c_int
+        l.fh_awq_stats.argtypes = [C.POINTER(C.c_float), C.c_int32, C.c_int32, C.POINTER(C.c_float),
+                                   C.POINTER(C.c_float)]
+        l.fh_awq_scales.restype = C.c_int
+        l.fh_awq_scales.argtypes = [C.POINTER(C.c_float), C.c_int32, C.c_float, C.POINTER(C.c_float)]
         _lib = l
     return _lib
 
@@ -52,3 +58,23 @@ def quantize(kind: int, w: np.ndarray, importance: np.ndarray | None = None) -> 
     check(lib().fh_quantize(kind, rows, cols, ptr(w, C.POINTER(C.c_float)), ptr(imp, C.POINTER(C.c_float)),
                             ptr(q, C.POINTER(C.c_uint8)), ptr(s, C.POINTER(C.c_float))))
     return Matrix(kind, rows, cols, q=q, s=s)
+
+
+def awq_stats(cal: np.ndarray):
+    """stats (src/awq.rs:128-142): mean |x| and mean x^2 per input channel."""
+    cal = np.ascontiguousarray(cal, np.float32)
+    m, k = cal.shape
+    a = np.zeros(k, np.float32)
+    q = np.zeros(k, np.float32)
+    fp = C.POINTER(C.c_float)
+    check(lib().fh_awq_stats(ptr(cal, fp), m, k, ptr(a, fp), ptr(q, fp)))
+    return a, q
+
+
+def awq_scales(abs_mean: np.ndarray, alpha: float) -> np.ndarray:
+    """scales (src/awq.rs:144-150) for one alpha."""
+    abs_mean = np.ascontiguousarray(abs_mean, np.float32)
+    s = np.zeros(abs_mean.size, np.float32)
+    fp = C.POINTER(C.c_float)
+    check(lib().fh_awq_scales(ptr(abs_mean, fp), abs_mean.size, alpha, ptr(s, fp)))
+    return s

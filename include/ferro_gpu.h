@@ -248,6 +248,35 @@ int fg_matmul(fg_ctx* ctx, const fg_mat* w, const float* x, int32_t m,
 int fg_matmul_device(fg_ctx* ctx, const fg_mat* w, const float* x_dev,
                      int32_t m, float* y_dev);
 
+/* ---- load-time quantization on the device ------------------------------ */
+/* QMatrix::quantize (src/quant.rs:78-143) on the device, bit for bit the
+ * reference's codes and scales: fh_quantize's contract (ferro_host.h), host
+ * buffers in and out. kind FG_INT8 or FG_INT4; rows and cols multiples of
+ * 32 (else FG_E_SHAPE); importance (cols floats) may be NULL. */
+int fg_quantize(fg_ctx* ctx, int32_t kind, int32_t rows, int32_t cols, const float* w,
+                const float* importance, uint8_t* q, float* s);
+
+/* What the AWQ search chose for one projection (awq::Choice,
+ * src/awq.rs:24-31, without the layer name). */
+typedef struct {
+    float alpha;
+    int32_t _pad;
+    double error_plain, error_awq;
+} fg_awq_choice;
+
+/* awq::search + apply (src/awq.rs:152-217) on the device: for alpha in
+ * 0, 0.1, ..., 1 the scales (mean |x|)^alpha of the m calibration rows
+ * cal (m x k), the weights w (rows x k f32) quantized with their columns
+ * times the scales, and the mean squared error of that projection of the
+ * scaled rows against the unquantized (bf16) one; the first minimum wins.
+ * Writes the chosen scales (k floats, to be folded into the producer of the
+ * projection's input), the choice, and the quantized matrix (QMatrix codes
+ * q and scales s, as fg_quantize). The errors and codes equal the
+ * reference's bit for bit. */
+int fg_awq_search(fg_ctx* ctx, int32_t kind, int32_t rows, int32_t k, const float* w,
+                  int32_t m, const float* cal, float* scales, fg_awq_choice* choice,
+                  uint8_t* q, float* s);
+
 #ifdef __cplusplus
 }
 #endif

@@ -31,6 +31,15 @@ uint64_t fh_stream_seed(uint64_t seed, uint64_t tensor, uint64_t block);
 int fh_quantize(int32_t kind, int32_t rows, int32_t cols, const float* w,
                 const float* importance, uint8_t* q, float* s);
 
+/* AWQ channel statistics (src/awq.rs:128-142): mean |x| and mean x^2 of
+ * each of the k input channels over the m calibration rows (cal, m x k),
+ * summed in f64 in row order. */
+int fh_awq_stats(const float* cal, int32_t m, int32_t k, float* abs_mean, float* sq_mean);
+
+/* AWQ scales for one alpha (src/awq.rs:144-150): max(a, 1e-5)^alpha,
+ * normalised so that max * min = 1, floored at 1e-4. */
+int fh_awq_scales(const float* abs_mean, int32_t k, float alpha, float* s);
+
 #ifdef __cplusplus
 }
 #endif

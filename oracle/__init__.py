@@ -23,7 +23,7 @@ from pathlib import Path
 
 import numpy as np
 
-from ferrolm_amd.weights import BF16, HostModel, Matrix
+from ferrolm_amd.weights import BF16, INT8, HostModel, Matrix
 
 HERE = Path(__file__).resolve().parent
 LIB = HERE / "liboracle.so"
@@ -99,6 +99,12 @@ def lib():
             "or_kv_read": (C.c_int32, [C.c_void_p, C.c_int32, f32p, f32p]),
             "or_kv_write_layer": (C.c_int32, [C.c_void_p, C.c_int32, f32p, f32p]),
             "or_forward": (C.c_int32, [C.c_void_p, C.c_void_p, C.POINTER(OrChunk), C.c_int32, f32p, f32p]),
+            "or_forward_taps": (C.c_int32, [C.c_void_p, C.c_void_p, C.POINTER(OrChunk), C.c_int32, f32p, f32p,
+                                            f32p]),
+            "or_awq_stats": (None, [f32p, C.c_int32, C.c_int32, f32p, f32p]),
+            "or_awq_scales": (None, [f32p, C.c_int32, C.c_float, f32p]),
+            "or_awq_search": (C.c_int32, [C.c_int32, C.c_int32, C.c_int32, f32p, C.c_int32, f32p, f32p,
+                                          f32p, C.POINTER(C.c_double), u8p, f32p]),
             "or_generate": (C.c_int32, [C.c_void_p, C.c_void_p, u32p, C.c_int32, C.c_int32, C.c_int32,
                                         C.c_int32, C.c_int32, u32p, i32p, i64p]),
             "or_spec_step": (C.c_int32, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, u32p, C.c_int32, i32p,
@@ -172,10 +178,13 @@ class Model:
     def kv(self, blocks: int, block_size: int = 16) -> "KvCache":
         return KvCache(self.cfg, blocks, block_size)
 
-    def forward(self, kv: "KvCache", chunks, hidden: bool = False):
+    def forward(self, kv: "KvCache", chunks, hidden: bool = False, taps: bool = False):
         """chunks: list of (tokens, pos, blocks, logits_mode) with logits_mode
         0 none, 1 last, 2 all. Returns logits [rows, vocab] (and the hidden
-        states [(layers+1), t, hidden] if asked)."""
+        states [(layers+1), t, hidden] if asked; and, with taps, per layer
+        the four projection inputs of Model::record, src/model.rs:312-333:
+        a list of [xn (t x hidden), attention (t x heads*hd), xn (t x
+        hidden), act (t x intermediate)])."""
         arr = (OrChunk * len(chunks))()
         keep = []
         rows = 0
@@ -189,10 +198,26 @@ class Model:
             t += len(tok)
         logits = np.zeros((rows, self.cfg.vocab), dtype=np.float32)
         hid = np.zeros((self.cfg.layers + 1, t, self.cfg.hidden), dtype=np.float32) if hidden else None
-        n = lib().or_forward(self.h, kv.h, arr, len(chunks), ptr(logits, f32p), ptr(hid, f32p))
+        c = self.cfg
+        H, qd, inter = c.hidden, c.heads * c.head_dim, c.intermediate
+        per = t * (2 * H + qd + inter)
+        tp = np.zeros(c.layers * per, dtype=np.float32) if taps else None
+        n = lib().or_forward_taps(self.h, kv.h, arr, len(chunks), ptr(logits, f32p), ptr(hid, f32p),
+                                  ptr(tp, f32p))
         if n < 0:
             raise ValueError("chunk overruns its cache blocks")
-        return (logits, hid) if hidden else logits
+        out = [logits]
+        if hidden:
+            out.append(hid)
+        if taps:
+            lay = []
+            for li in range(c.layers):
+                b = tp[li * per:(li + 1) * per]
+                o = [0, t * H, t * (H + qd), t * (2 * H + qd), per]
+                lay.append([b[o[0]:o[1]].reshape(t, H), b[o[1]:o[2]].reshape(t, qd),
+                            b[o[2]:o[3]].reshape(t, H), b[o[3]:o[4]].reshape(t, inter)])
+            out.append(lay)
+        return out[0] if len(out) == 1 else tuple(out)
 
 
 class KvCache:
@@ -451,3 +476,80 @@ def generate_sampled(target: Model, draft: Model | None, prompt, max_tokens: int
             if len(out) >= max_tokens or len(tokens) >= max_len:
                 break
     return np.array(out, np.uint32), (proposed, acc_total, steps)
+
+
+# ---------------------------------------------------------------------------
+# Calibration capture and AWQ (src/model.rs:56-70, 364-392; src/awq.rs)
+# ---------------------------------------------------------------------------
+
+def calibrate(m: Model, seqs, max_rows: int):
+    """Model::calibrate (src/awq.rs:38-62): each sequence's forward from
+    position 0 in a fresh cache, keeping up to max_rows input rows per
+    projection by Model::record's reservoir sampling (src/model.rs:364-392:
+    one xorshift generator shared by every layer and projection, advanced
+    for each row past the first max_rows). Returns per layer the four lists
+    [qkv, o, gate_up, down] of rows, as float32 arrays [rows, width]."""
+    rng = 0x9E3779B97F4A7C15
+    mask = (1 << 64) - 1
+    layers = [[[] for _ in range(4)] for _ in range(m.cfg.layers)]
+    seen = [[0] * 4 for _ in range(m.cfg.layers)]
+    for s in seqs:
+        s = [int(v) for v in s]
+        nb = (len(s) + 15) // 16
+        kv = m.kv(nb)
+        _, taps = m.forward(kv, [(s, 0, list(range(nb)), 0)], taps=True)
+        for li in range(m.cfg.layers):
+            for which in range(4):
+                for r in taps[li][which]:
+                    n = seen[li][which]
+                    seen[li][which] += 1
+                    if n < max_rows:
+                        layers[li][which].append(r.copy())
+                    else:
+                        rng ^= (rng << 13) & mask
+                        rng ^= rng >> 7
+                        rng ^= (rng << 17) & mask
+                        j = rng % (n + 1)
+                        if j < max_rows:
+                            layers[li][which][j] = r.copy()
+    return [[np.stack(rows).astype(np.float32) if rows else np.zeros((0, 0), np.float32) for rows in l]
+            for l in layers]
+
+
+def awq_stats(cal: np.ndarray):
+    """stats (src/awq.rs:128-142): mean |x| and mean x^2 per channel."""
+    cal = np.ascontiguousarray(cal, np.float32)
+    m, k = cal.shape
+    a = np.zeros(k, np.float32)
+    q = np.zeros(k, np.float32)
+    lib().or_awq_stats(ptr(cal, f32p), m, k, ptr(a, f32p), ptr(q, f32p))
+    return a, q
+
+
+def awq_scales(abs_mean: np.ndarray, alpha: float) -> np.ndarray:
+    """scales (src/awq.rs:144-150) for one alpha."""
+    abs_mean = np.ascontiguousarray(abs_mean, np.float32)
+    s = np.zeros(abs_mean.size, np.float32)
+    lib().or_awq_scales(ptr(abs_mean, f32p), abs_mean.size, alpha, ptr(s, f32p))
+    return s
+
+
+def awq_search(kind: int, w: np.ndarray, cal: np.ndarray):
+    """search + apply (src/awq.rs:152-217): returns (scales, alpha,
+    error_plain, error_awq, Matrix) for weights w (rows x k, f32) and
+    calibration rows cal (m x k)."""
+    w = np.ascontiguousarray(w, np.float32)
+    cal = np.ascontiguousarray(cal, np.float32)
+    rows, k = w.shape
+    m = cal.shape[0]
+    assert cal.shape[1] == k
+    bpk = 32 if kind == INT8 else 16
+    q = np.zeros(rows // 32 * k * bpk, np.uint8)
+    s = np.zeros(rows // 32 * (k // 32) * 32, np.float32)
+    sc = np.zeros(k, np.float32)
+    alpha = C.c_float()
+    errs = (C.c_double * 2)()
+    if lib().or_awq_search(kind, rows, k, ptr(w, f32p), m, ptr(cal, f32p), ptr(sc, f32p), C.byref(alpha), errs,
+                           ptr(q, u8p), ptr(s, f32p)):
+        raise ValueError("awq_search: bad shape")
+    return sc, float(alpha.value), float(errs[0]), float(errs[1]), Matrix(kind, rows, k, q=q, s=s)

@@ -19,6 +19,7 @@
  */
 #include "ferro_oracle.h"
 
+#include <float.h>
 #include <math.h>
 #include <omp.h>
 #include <stdlib.h>
@@ -509,6 +510,112 @@ int32_t or_matmul(const or_matrix_desc* d, const float* x, int32_t m, const floa
 }
 
 /* ------------------------------------------------------------------ */
+/* AWQ: src/awq.rs:128-217                                              */
+/* ------------------------------------------------------------------ */
+
+/* stats (src/awq.rs:128-142): mean |x| and mean x^2 per input channel, f64
+ * sums taken in row order, divided by max(rows, 1), rounded to f32. */
+void or_awq_stats(const float* cal, int32_t m, int32_t k, float* abs_mean, float* sq_mean) {
+    double* a = (double*)calloc((size_t)k, sizeof(double));
+    double* q = (double*)calloc((size_t)k, sizeof(double));
+    for (int32_t i = 0; i < m; i++)
+        for (int32_t c = 0; c < k; c++) {
+            const float v = cal[(size_t)i * k + c];
+            a[c] += (double)fabsf(v);
+            q[c] += (double)v * (double)v;
+        }
+    const double n = (double)(m > 1 ? m : 1);
+    for (int32_t c = 0; c < k; c++) {
+        abs_mean[c] = (float)(a[c] / n);
+        sq_mean[c] = (float)(q[c] / n);
+    }
+    free(a);
+    free(q);
+}
+
+/* scales (src/awq.rs:144-150): max(a, 1e-5)^alpha (f32 powf), divided by
+ * max(sqrt(max * min), 1e-8), floored at 1e-4. */
+void or_awq_scales(const float* abs_mean, int32_t k, float alpha, float* s) {
+    float mx = 0.0f, mn = FLT_MAX;
+    for (int32_t c = 0; c < k; c++) {
+        const float v = powf(fmaxf(abs_mean[c], 1e-5f), alpha);
+        s[c] = v;
+        mx = fmaxf(mx, v);
+        mn = fminf(mn, v);
+    }
+    const float norm = fmaxf(sqrtf(mx * mn), 1e-8f);
+    for (int32_t c = 0; c < k; c++) s[c] = fmaxf(s[c] / norm, 1e-4f);
+}
+
+/* apply (src/awq.rs:152-165): quantize w (rows x k) with its columns times
+ * s, importance sq / s^2 + 1e-8. */
+static int32_t awq_apply(int32_t kind, int32_t rows, int32_t k, const float* w, const float* s, const float* sq,
+                         float* ws, float* imp, uint8_t* q, float* sc) {
+    for (int32_t r = 0; r < rows; r++)
+        for (int32_t c = 0; c < k; c++) ws[(size_t)r * k + c] = w[(size_t)r * k + c] * s[c];
+    for (int32_t c = 0; c < k; c++) imp[c] = sq[c] / (s[c] * s[c]) + 1e-8f;
+    return or_quantize(kind, rows, k, ws, imp, q, sc);
+}
+
+/* search + apply (src/awq.rs:167-217): alpha in 0, 0.1, ..., 1; per alpha
+ * the quantized projection of the scaled calibration rows against the
+ * unquantized (bf16) projection, mean squared error summed in f64 in output
+ * order; the first minimum wins. Writes the chosen scales (k), alpha,
+ * errs[0] = error at alpha 0 (plain), errs[1] = chosen error, and the
+ * quantized matrix in the QMatrix layout. */
+int32_t or_awq_search(int32_t kind, int32_t rows, int32_t k, const float* w, int32_t m, const float* cal,
+                      float* scales_out, float* alpha_out, double* errs, uint8_t* q, float* s) {
+    if (kind == OR_BF16 || rows <= 0 || k <= 0 || m <= 0 || rows % PANEL || k % GROUP) return -1;
+    const size_t rk = (size_t)rows * k, qb = (size_t)rows / PANEL * k * bytes_per_k(kind);
+    const size_t sn = (size_t)rows / PANEL * (k / GROUP) * PANEL, ny = (size_t)m * rows;
+    float *am = (float*)malloc((size_t)k * 4), *sq = (float*)malloc((size_t)k * 4);
+    float *sc = (float*)malloc((size_t)k * 4), *best_s = (float*)malloc((size_t)k * 4);
+    float *imp = (float*)malloc((size_t)k * 4), *ws = (float*)malloc(rk * 4);
+    float *xs = (float*)malloc((size_t)m * k * 4), *yref = (float*)malloc(ny * 4), *y = (float*)malloc(ny * 4);
+    uint16_t* wb = (uint16_t*)malloc(rk * 2);
+    uint8_t* qt = (uint8_t*)malloc(qb);
+    float* st = (float*)malloc(sn * 4);
+    or_awq_stats(cal, m, k, am, sq);
+    /* the reference output, with the unquantized weights (Matrix::from_f32: bf16) */
+    for (size_t i = 0; i < rk; i++) wb[i] = or_f32_to_bf16(w[i]);
+    or_matrix_desc dref = {OR_BF16, rows, k, 0, wb, NULL, NULL};
+    or_matmul(&dref, cal, m, NULL, yref);
+    double best = INFINITY, plain = 0.0;
+    float best_alpha = 0.0f;
+    int have = 0;
+    for (int32_t step = 0; step <= 10; step++) {
+        const float alpha = (float)step / 10.0f;
+        or_awq_scales(am, k, alpha, sc);
+        awq_apply(kind, rows, k, w, sc, sq, ws, imp, qt, st);
+        for (int32_t i = 0; i < m; i++)
+            for (int32_t c = 0; c < k; c++) xs[(size_t)i * k + c] = cal[(size_t)i * k + c] / sc[c];
+        or_matrix_desc dq = {kind, rows, k, 0, NULL, qt, st};
+        or_matmul(&dq, xs, m, NULL, y);
+        double err = 0.0;
+        for (size_t i = 0; i < ny; i++) {
+            const double d = (double)(y[i] - yref[i]);
+            err += d * d;
+        }
+        err /= (double)ny;
+        if (step == 0) plain = err;
+        if (!have || err < best) {
+            have = 1;
+            best = err;
+            best_alpha = alpha;
+            memcpy(best_s, sc, (size_t)k * 4);
+        }
+    }
+    awq_apply(kind, rows, k, w, best_s, sq, ws, imp, q, s);
+    memcpy(scales_out, best_s, (size_t)k * 4);
+    *alpha_out = best_alpha;
+    errs[0] = plain;
+    errs[1] = best;
+    free(am); free(sq); free(sc); free(best_s); free(imp); free(ws); free(xs); free(yref); free(y); free(wb);
+    free(qt); free(st);
+    return 0;
+}
+
+/* ------------------------------------------------------------------ */
 /* Model                                                                */
 /* ------------------------------------------------------------------ */
 typedef struct {
@@ -754,6 +861,11 @@ static void rope(float* x, const float* cs, const float* sn, int32_t hd) {
 /* Model::forward: src/model.rs:267-362 */
 int32_t or_forward(const or_model* m, or_kv* kv, const or_chunk* chunks, int32_t n_chunks, float* logits_out,
                    float* hidden_out) {
+    return or_forward_taps(m, kv, chunks, n_chunks, logits_out, hidden_out, NULL);
+}
+
+int32_t or_forward_taps(const or_model* m, or_kv* kv, const or_chunk* chunks, int32_t n_chunks, float* logits_out,
+                        float* hidden_out, float* proj_out) {
     const or_config* c = &m->cfg;
     int32_t H = c->hidden, hd = c->head_dim, nh = c->heads, nkv = c->kv_heads, I = c->intermediate;
     int32_t q_dim = nh * hd, qkv_dim = (nh + 2 * nkv) * hd, half = hd / 2;
@@ -812,7 +924,10 @@ int32_t or_forward(const or_model* m, or_kv* kv, const or_chunk* chunks, int32_t
 
     for (int32_t li = 0; li < m->n_layers; li++) {
         const olayer* l = &m->layers[li];
+        /* Model::record's four projection inputs (src/model.rs:312,323,329,333) */
+        float* tap = proj_out ? proj_out + (size_t)li * t * (2 * H + q_dim + I) : NULL;
         or_rms_norm(x, l->attn_norm, H, t, c->rms_eps, xn);
+        if (tap) memcpy(tap, xn, (size_t)t * H * 4);
         omat_matmul(&l->wqkv, xn, t, l->bqkv, qkv);
         for (r = 0; r < t; r++) {
             float* row = qkv + (size_t)r * qkv_dim;
@@ -833,11 +948,14 @@ int32_t or_forward(const or_model* m, or_kv* kv, const or_chunk* chunks, int32_t
             }
             free(scores);
         }
+        if (tap) memcpy(tap + (size_t)t * H, att, (size_t)t * q_dim * 4);
         omat_matmul(&l->wo, att, t, NULL, proj);
         for (size_t i = 0; i < (size_t)t * H; i++) x[i] += proj[i];
         or_rms_norm(x, l->mlp_norm, H, t, c->rms_eps, xn);
+        if (tap) memcpy(tap + (size_t)t * (H + q_dim), xn, (size_t)t * H * 4);
         omat_matmul(&l->w_gate_up, xn, t, NULL, gate_up);
         or_silu_mul(gate_up, I, t, act);
+        if (tap) memcpy(tap + (size_t)t * (2 * H + q_dim), act, (size_t)t * I * 4);
         omat_matmul(&l->w_down, act, t, NULL, proj);
         for (size_t i = 0; i < (size_t)t * H; i++) x[i] += proj[i];
         if (hidden_out) memcpy(hidden_out + (size_t)(li + 1) * t * H, x, (size_t)t * H * 4);

@@ -125,6 +125,22 @@ int32_t or_kv_write_layer(or_kv* kv, int32_t layer, const float* k, const float*
 int32_t or_forward(const or_model* m, or_kv* kv, const or_chunk* chunks,
                    int32_t n_chunks, float* logits_out, float* hidden_out);
 
+/* The same forward, also writing Model::record's four projection inputs
+ * (src/model.rs:312,323,329,333) of every row: per layer, [rows x hidden
+ * (q/k/v input)][rows x heads*head_dim (attention output)][rows x hidden
+ * (gate/up input)][rows x intermediate (down input)]. proj_out may be NULL. */
+int32_t or_forward_taps(const or_model* m, or_kv* kv, const or_chunk* chunks,
+                        int32_t n_chunks, float* logits_out, float* hidden_out,
+                        float* proj_out);
+
+/* AWQ (src/awq.rs:128-217): channel statistics, the scales for one alpha,
+ * and the alpha search with the final quantization (see ferro_oracle.c). */
+void or_awq_stats(const float* cal, int32_t m, int32_t k, float* abs_mean, float* sq_mean);
+void or_awq_scales(const float* abs_mean, int32_t k, float alpha, float* s);
+int32_t or_awq_search(int32_t kind, int32_t rows, int32_t k, const float* w, int32_t m,
+                      const float* cal, float* scales_out, float* alpha_out, double* errs,
+                      uint8_t* q, float* s);
+
 /* Greedy generation with the reference engine's speculative loop for one
  * sequence (Engine::schedule/execute/propose, src/engine.rs:395-717,
  * greedy branches, ignore_eos). draft may be NULL (k = 0: plain decode).

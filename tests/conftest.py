@@ -38,6 +38,48 @@ def reference_prompts(n, seed):
     return out
 
 
+def reference_tokens(n, seed):
+    """tests/quant.rs:36-39 of the reference: n ids between(3, 511) from Rng(seed)."""
+    import ctypes
+    import oracle
+    rng = ctypes.c_uint64(oracle.lib().or_rng_new(seed))
+    return [3 + oracle.lib().or_rng_next(ctypes.byref(rng)) % 509 for _ in range(n)]
+
+
+def oracle_awq():
+    """The oracle's AWQ search and apply, in the shape ferrolm_amd.awq takes."""
+    import numpy as np
+    import oracle
+
+    def apply(kind, w, s, cal):
+        _, sq = oracle.awq_stats(cal)
+        ws = (np.ascontiguousarray(w, np.float32) * s[None, :]).astype(np.float32)
+        imp = (sq / (s * s) + np.float32(1e-8)).astype(np.float32)
+        return oracle.quantize(kind, ws, imp)
+
+    return oracle.awq_search, apply
+
+
+def plain_quantized(hm, kind, quantize):
+    """Model::quantize(kind, None) (src/model.rs:192-219) with the given
+    quantize(kind, w) -> Matrix."""
+    from dataclasses import replace
+    out = [replace(l, wqkv=quantize(kind, l.wqkv.to_f32()), wo=quantize(kind, l.wo.to_f32()),
+                   w_gate_up=quantize(kind, l.w_gate_up.to_f32()), w_down=quantize(kind, l.w_down.to_f32()))
+           for l in hm.layers]
+    return replace(hm, layers=out)
+
+
+def rel_error(a, b) -> float:
+    """tests/quant.rs:30-34: sqrt(sum (a - b)^2 / sum b^2), f64."""
+    import numpy as np
+    a = np.asarray(a, np.float32).ravel()
+    b = np.asarray(b, np.float32).ravel()
+    num = np.sum(np.square((a - b).astype(np.float64)))
+    den = np.sum(np.square(b.astype(np.float64)))
+    return float(np.sqrt(num / den))
+
+
 def exact_two_token_distribution(m, prompt, params):
     """tests/engine.rs:163-194 of the reference on the oracle model m: the
     probability of each two-token continuation of prompt under params =
