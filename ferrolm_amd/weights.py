@@ -221,7 +221,7 @@ def read_safetensors(path: Path) -> dict:
     header = json.loads(raw[8:8 + n])
     base = 8 + n
     out = {}
-    dt = {"BF16": np.uint16, "F32": np.float32, "F16": np.float16, "I64": np.int64}
+    dt = {"BF16": np.uint16, "F32": np.float32, "F16": np.float16, "I64": np.int64, "U8": np.uint8}
     for name, info in header.items():
         if name == "__metadata__":
             continue
@@ -276,3 +276,96 @@ def load_model(d: str | Path) -> HostModel:
         lm = _bf16(t["lm_head.weight"])
     return HostModel(cfg=cfg, embed=_bf16(t["model.embed_tokens.weight"]),
                      norm=_vec_f32(t["model.norm.weight"]), layers=layers, lm_head=lm)
+
+
+# ---------------------------------------------------------------------------
+# On-disk quantized models (the reference has none: it quantizes at load
+# time, README.md:373-376). One safetensors file holds a HostModel as the
+# device upload takes it: bf16 matrices as BF16 [rows, cols]; int8/int4
+# matrices as their QMatrix codes (U8, flat) and scales (F32, flat) in the
+# reference's layouts (src/quant.rs:64-76); norms, bias and embeddings as
+# they are. The header's __metadata__ holds the Config and each matrix's
+# format as JSON, so loading needs no config.json and repeats no search.
+# ---------------------------------------------------------------------------
+
+_MATS = ("wqkv", "wo", "w_gate_up", "w_down")
+_DTYPE = {np.dtype(np.uint16): "BF16", np.dtype(np.float32): "F32", np.dtype(np.uint8): "U8"}
+
+
+def write_safetensors(path: Path, tensors: dict, metadata: dict | None = None) -> None:
+    """Writes name -> (safetensors dtype, array) as one safetensors file
+    (8-byte little-endian header length, JSON header, data)."""
+    header, blobs, off = {}, [], 0
+    for name, (dtype, arr) in tensors.items():
+        b = np.ascontiguousarray(arr).tobytes()
+        header[name] = {"dtype": dtype, "shape": list(np.shape(arr)), "data_offsets": [off, off + len(b)]}
+        blobs.append(b)
+        off += len(b)
+    if metadata:
+        header["__metadata__"] = {k: str(v) for k, v in metadata.items()}
+    h = json.dumps(header, separators=(",", ":")).encode()
+    h += b" " * (-len(h) % 8)  # data starts 8-aligned
+    with open(path, "wb") as f:
+        f.write(struct.pack("<Q", len(h)))
+        f.write(h)
+        for b in blobs:
+            f.write(b)
+
+
+def save_quantized(hm: HostModel, path: str | Path) -> None:
+    """Saves a (quantized or bf16) HostModel to one safetensors file."""
+    t, formats = {}, {}
+    t["embed"] = ("BF16", hm.embed)
+    t["norm"] = ("F32", hm.norm)
+    if hm.lm_head is not None:
+        t["lm_head"] = ("BF16", hm.lm_head)
+    for i, l in enumerate(hm.layers):
+        p = f"layers.{i}"
+        t[f"{p}.attn_norm"] = ("F32", l.attn_norm)
+        t[f"{p}.mlp_norm"] = ("F32", l.mlp_norm)
+        if l.bqkv is not None:
+            t[f"{p}.bqkv"] = ("F32", l.bqkv)
+        for name in _MATS:
+            m = getattr(l, name)
+            formats[f"{p}.{name}"] = [m.kind, m.rows, m.cols]
+            if m.kind == BF16:
+                t[f"{p}.{name}"] = ("BF16", m.bf16)
+            else:
+                t[f"{p}.{name}.q"] = ("U8", m.q)
+                t[f"{p}.{name}.s"] = ("F32", m.s)
+    cfg = {k: (list(v) if isinstance(v, tuple) else v) for k, v in hm.cfg.__dict__.items()}
+    write_safetensors(Path(path), t, {"format": "ferrolm-quantized-1", "config": json.dumps(cfg),
+                                      "matrices": json.dumps(formats)})
+
+
+def load_quantized(path: str | Path) -> HostModel:
+    """Loads a model written by save_quantized."""
+    raw = Path(path).read_bytes()
+    (n,) = struct.unpack("<Q", raw[:8])
+    meta = json.loads(raw[8:8 + n]).get("__metadata__", {})
+    if meta.get("format") != "ferrolm-quantized-1":
+        raise ValueError(f"{path}: not a ferrolm quantized model")
+    c = json.loads(meta["config"])
+    c["eos"] = tuple(c.get("eos", ()))
+    cfg = Config(**c)
+    formats = json.loads(meta["matrices"])
+    t = read_safetensors(Path(path))
+
+    def arr(name, dtype):
+        return np.array(t[name][1], dtype=dtype, copy=True)
+
+    def mat(key):
+        kind, rows, cols = formats[key]
+        if kind == BF16:
+            return Matrix(BF16, rows, cols, bf16=arr(key, np.uint16).reshape(rows, cols))
+        return Matrix(kind, rows, cols, q=arr(key + ".q", np.uint8), s=arr(key + ".s", np.float32))
+
+    layers = []
+    for i in range(cfg.layers):
+        p = f"layers.{i}"
+        layers.append(Layer(attn_norm=arr(f"{p}.attn_norm", np.float32), wqkv=mat(f"{p}.wqkv"),
+                            bqkv=arr(f"{p}.bqkv", np.float32) if f"{p}.bqkv" in t else None,
+                            wo=mat(f"{p}.wo"), mlp_norm=arr(f"{p}.mlp_norm", np.float32),
+                            w_gate_up=mat(f"{p}.w_gate_up"), w_down=mat(f"{p}.w_down")))
+    return HostModel(cfg=cfg, embed=arr("embed", np.uint16), norm=arr("norm", np.float32), layers=layers,
+                     lm_head=arr("lm_head", np.uint16) if "lm_head" in t else None)

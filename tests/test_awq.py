@@ -124,3 +124,34 @@ def test_reference_awq_folds_scales_and_reduces_held_out_error():
     e_awq = rel_error(logits(oracle.Model(qm)), ref)
     print(f"held-out relative logit error: int4 {e_plain:.4f}, int4+AWQ {e_awq:.4f}")
     assert e_awq < e_plain
+
+
+@pytest.mark.parametrize("fixture", ["llama-gqa", "qwen2"])
+def test_quantized_model_round_trips_through_its_file(tmp_path, fixture):
+    """save_quantized / load_quantized: every array, the config and the
+    oracle's logits come back identical (AWQ int4 with the oracle's search;
+    qwen2 carries a q/k/v bias; a bf16 model round-trips too)."""
+    from ferrolm_amd.weights import load_quantized, save_quantized
+    hm = load_model(GOLDEN / fixture)
+    om = oracle.Model(hm)
+    acts = oracle.calibrate(om, [reference_tokens(48, 20 + i) for i in range(3)], 64)
+    qm, _ = awq.quantize_awq(hm, INT4, acts, *oracle_awq())
+    toks = reference_tokens(40, 5)
+    for model in (qm, hm):
+        path = tmp_path / "model.safetensors"
+        save_quantized(model, path)
+        back = load_quantized(path)
+        assert back.cfg == model.cfg
+        assert np.array_equal(back.embed, model.embed) and np.array_equal(back.norm, model.norm)
+        for a, b in zip(back.layers, model.layers):
+            for name in ("wqkv", "wo", "w_gate_up", "w_down"):
+                x, y = getattr(a, name), getattr(b, name)
+                assert (x.kind, x.rows, x.cols) == (y.kind, y.rows, y.cols)
+                for f in ("bf16", "q", "s"):
+                    assert (getattr(x, f) is None) == (getattr(y, f) is None)
+                    if getattr(x, f) is not None:
+                        assert np.array_equal(getattr(x, f), getattr(y, f))
+            assert np.array_equal(a.attn_norm, b.attn_norm) and np.array_equal(a.mlp_norm, b.mlp_norm)
+            assert (a.bqkv is None) == (b.bqkv is None)
+        lo = [oracle.Model(m).forward(oracle.Model(m).kv(3), [(toks, 0, [0, 1, 2], 2)]) for m in (back, model)]
+        assert np.array_equal(lo[0], lo[1])
