@@ -983,26 +983,40 @@ int fg_forward(fg_ctx* ctx, const fg_model* m, fg_kv* kv, const fg_chunk* chunks
     return 0;
 }
 
-// Distributions of `rows` rows carved from the context's sampling buffer
-// starting at row `first` (the buffer holds `total` rows).
-static SampleRows sample_rows(void* buf, int total, int first) {
-    const size_t cap = kSampleCap;
+// Distributions of rows carved from the context's sampling buffer starting at
+// row `first` (the buffer holds `total` rows of `cap` pairs): tok, pr, tok_id,
+// pr_id [total][cap], n [total]; with wide rows also dense [total][cap] and
+// the sort scratch [total][4 cap].
+static size_t sample_cap(bool wide, int vocab) { return wide ? (size_t)vocab : (size_t)kSampleCap; }
+static SampleRows sample_rows(void* buf, int total, int first, bool wide, int vocab) {
+    const size_t cap = sample_cap(wide, vocab), tc = (size_t)total * cap;
     uint8_t* b = (uint8_t*)buf;
     SampleRows r;
     r.tok = (uint32_t*)b + (size_t)first * cap;
-    r.pr = (float*)(b + (size_t)total * cap * 4) + (size_t)first * cap;
-    r.tok_id = (uint32_t*)(b + (size_t)total * cap * 8) + (size_t)first * cap;
-    r.pr_id = (float*)(b + (size_t)total * cap * 12) + (size_t)first * cap;
-    r.n = (int*)(b + (size_t)total * cap * 16) + first;
+    r.pr = (float*)(b + tc * 4) + (size_t)first * cap;
+    r.tok_id = (uint32_t*)(b + tc * 8) + (size_t)first * cap;
+    r.pr_id = (float*)(b + tc * 12) + (size_t)first * cap;
+    const size_t o_n = tc * 16, o_dense = o_n + ((size_t)total * 4 + 255) / 256 * 256;
+    r.n = (int*)(b + o_n) + first;
+    r.cap = (int)cap;
+    r.vocab = vocab;
+    r.dense = wide ? (float*)(b + o_dense) + (size_t)first * cap : nullptr;
+    r.scratch = wide ? (uint32_t*)(b + o_dense + tc * 4) + (size_t)first * cap * 4 : nullptr;
     return r;
 }
-static size_t sample_bytes(int total) { return (size_t)total * kSampleCap * 16 + (size_t)total * 4; }
+static size_t sample_bytes(int total, bool wide, int vocab) {
+    const size_t tc = (size_t)total * sample_cap(wide, vocab);
+    return tc * 16 + ((size_t)total * 4 + 255) / 256 * 256 + (wide ? tc * 20 : 0);
+}
 static_assert(sizeof(SampleParams) == sizeof(fg_sampling), "fg_sampling is copied to the device as SampleParams");
 
-static int check_sampling(const fg_sampling* p, int n) {
-    for (int i = 0; i < n; i++)
-        if (p[i].temperature > 0.0f && (p[i].top_k < 1 || p[i].top_k > kSampleCap))
-            return fail(FG_E_ARG, "device sampling needs 1 <= top_k <= 1024 (0, no limit, is not supported)");
+// Sets *wide when a sampled row has top_k 0 (no limit) or above kSampleCap.
+static int check_sampling(const fg_sampling* p, int n, bool* wide) {
+    *wide = false;
+    for (int i = 0; i < n; i++) {
+        if (p[i].temperature > 0.0f && p[i].top_k < 0) return fail(FG_E_ARG, "top_k must be 0 (no limit) or positive");
+        *wide |= sample_wide(*(const SampleParams*)&p[i]);
+    }
     return 0;
 }
 
@@ -1013,6 +1027,10 @@ static int spec_step(fg_ctx* ctx, const fg_model* target, fg_kv* tkv, const fg_m
         !out_accepted || (params && !rng))
         return fail(FG_E_ARG, "bad argument");
     const bool sampling = params != nullptr;
+    bool wide = false;  // a sampled sequence with top_k 0 or above kSampleCap
+    for (int i = 0; sampling && i < n_seqs; i++) wide |= sample_wide(*(const SampleParams*)&params[i]);
+    if (wide && draft->cfg.vocab != target->cfg.vocab)
+        return fail(FG_E_SHAPE, "draft and target must share a vocabulary");
     if (draft->cfg.vocab != target->cfg.vocab) return fail(FG_E_SHAPE, "draft and target must share a vocabulary");
     int rc;
     if ((rc = check_model_kv(target, tkv)) || (rc = check_model_kv(draft, dkv))) return rc;
@@ -1083,7 +1101,9 @@ static int spec_step(fg_ctx* ctx, const fg_model* target, fg_kv* tkv, const fg_m
     if ((rc = ensure(&ctx->ws, &ctx->ws_cap, need, ctx->stream, false))) return rc;
     // sampling rows: the target's n_seqs*(k+1) verify rows, then k draft rounds of n_seqs
     const int srows = n_seqs * K1 + k * n_seqs;
-    if (sampling && (rc = ensure(&ctx->sbuf, &ctx->sbuf_cap, sample_bytes(srows), ctx->stream, false))) return rc;
+    const int vocab = target->cfg.vocab;
+    if (sampling && (rc = ensure(&ctx->sbuf, &ctx->sbuf_cap, sample_bytes(srows, wide, vocab), ctx->stream, false)))
+        return rc;
     int32_t* dm = (int32_t*)ctx->dmeta;
     uint32_t* vtok = (uint32_t*)(dm + o_vtok);
     const SampleParams* dprm = (const SampleParams*)(dm + o_prm);
@@ -1101,7 +1121,7 @@ static int spec_step(fg_ctx* ctx, const fg_model* target, fg_kv* tkv, const fg_m
                                 (uint32_t*)(dm + o_am), vtok, K1, r + 1, nullptr);
             if (e) return e;
             if (sampling) {
-                SampleRows q = sample_rows(ctx->sbuf, srows, n_seqs * K1 + r * n_seqs);
+                SampleRows q = sample_rows(ctx->sbuf, srows, n_seqs * K1 + r * n_seqs, wide, vocab);
                 launch_dist(ctx->stream, w.logits, n_seqs, draft->cfg.vocab, 1, dprm, q);
                 launch_draw(ctx->stream, n_seqs, dprm, q, drng, vtok, K1, r + 1);
             }
@@ -1114,9 +1134,9 @@ static int spec_step(fg_ctx* ctx, const fg_model* target, fg_kv* tkv, const fg_m
                             (uint32_t*)(dm + o_am), nullptr, 0, 0, nullptr);
         if (e) return e;
         if (sampling) {
-            SampleRows p = sample_rows(ctx->sbuf, srows, 0);
+            SampleRows p = sample_rows(ctx->sbuf, srows, 0, wide, vocab);
             launch_dist(ctx->stream, w.logits, n_seqs * K1, target->cfg.vocab, K1, dprm, p);
-            SampleRows q = sample_rows(ctx->sbuf, srows, n_seqs * K1);
+            SampleRows q = sample_rows(ctx->sbuf, srows, n_seqs * K1, wide, vocab);
             launch_accept_sampled(ctx->stream, n_seqs, k, dprm, vtok, (const uint32_t*)(dm + o_am), p, q, drng,
                                   (uint32_t*)(dm + o_out), dm + o_cnt, dm + o_acc);
         } else {
@@ -1133,7 +1153,8 @@ static int spec_step(fg_ctx* ctx, const fg_model* target, fg_kv* tkv, const fg_m
         std::vector<int64_t> sig = {n_seqs, k, (int64_t)target->serial, (int64_t)draft->serial,
                                     (int64_t)tkv->serial, (int64_t)dkv->serial, (int64_t)(uintptr_t)ctx->ws,
                                     (int64_t)ctx->ws_cap, (int64_t)(uintptr_t)ctx->dmeta, (int64_t)ctx->dmeta_cap,
-                                    (int64_t)sampling, (int64_t)(uintptr_t)ctx->sbuf, (int64_t)ctx->sbuf_cap};
+                                    (int64_t)sampling, (int64_t)wide, (int64_t)(uintptr_t)ctx->sbuf,
+                                    (int64_t)ctx->sbuf_cap};
         for (int r = 0; r <= k; r++) {
             const Plan& P = plans[r];
             for (int64_t v : {(int64_t)P.t, (int64_t)P.S, (int64_t)P.Wc, (int64_t)P.words, (int64_t)P.ns})
@@ -1223,7 +1244,8 @@ int fg_forward_sampled(fg_ctx* ctx, const fg_model* m, fg_kv* kv, const fg_chunk
     if (rows_out) *rows_out = P.S;
     if (P.t == 0) return 0;
     if (P.S > 0 && (!params || !rng)) return fail(FG_E_ARG, "sampling parameters and generator states required");
-    if (P.S > 0 && (rc = check_sampling(params, P.S))) return rc;
+    bool wide = false;
+    if (P.S > 0 && (rc = check_sampling(params, P.S, &wide))) return rc;
     // the plan, then the selected rows' parameters and generator states
     const size_t o_prm = P.words, o_rng = o_prm + (size_t)P.S * 4 + 64, words = o_rng + (size_t)P.S * 2 + 64;
     if ((rc = ensure(&ctx->hmeta, &ctx->hmeta_cap, words * 4, ctx->stream, true))) return rc;
@@ -1238,7 +1260,9 @@ int fg_forward_sampled(fg_ctx* ctx, const fg_model* m, fg_kv* kv, const fg_chunk
     Work w{};
     const size_t need = layout_work(m, P, w, nullptr);
     if ((rc = ensure(&ctx->ws, &ctx->ws_cap, need, ctx->stream, false))) return rc;
-    if (P.S > 0 && (rc = ensure(&ctx->sbuf, &ctx->sbuf_cap, sample_bytes(P.S), ctx->stream, false))) return rc;
+    if (P.S > 0 &&
+        (rc = ensure(&ctx->sbuf, &ctx->sbuf_cap, sample_bytes(P.S, wide, m->cfg.vocab), ctx->stream, false)))
+        return rc;
     layout_work(m, P, w, ctx->ws);
     int32_t* dm = (int32_t*)ctx->dmeta;
     rc = run_forward(ctx, m, kv, P, dm, (const uint32_t*)(dm + P.o_tok), 1, w, w.logits, nullptr, nullptr, 0, 0,
@@ -1246,7 +1270,7 @@ int fg_forward_sampled(fg_ctx* ctx, const fg_model* m, fg_kv* kv, const fg_chunk
     if (rc) return rc;
     if (P.S > 0) {
         // greedy rows keep the argmax in w.am; sampled rows are drawn over it
-        SampleRows d = sample_rows(ctx->sbuf, P.S, 0);
+        SampleRows d = sample_rows(ctx->sbuf, P.S, 0, wide, m->cfg.vocab);
         const SampleParams* dprm = (const SampleParams*)(dm + o_prm);
         launch_dist(ctx->stream, w.logits, P.S, m->cfg.vocab, 1, dprm, d);
         launch_draw(ctx->stream, P.S, dprm, d, (uint64_t*)(dm + o_rng), w.am, 1, 0);
@@ -1270,7 +1294,8 @@ int fg_spec_step_sampled(fg_ctx* ctx, const fg_model* target, fg_kv* tkv, const 
                          const fg_spec_seq* seqs, int32_t n_seqs, int32_t k, const fg_sampling* params, uint64_t* rng,
                          uint32_t* out_tokens, int32_t* out_count, int32_t* out_accepted) {
     if (!params || !rng || n_seqs <= 0) return fail(FG_E_ARG, "sampling parameters and generator states required");
-    int rc = check_sampling(params, n_seqs);
+    bool wide = false;
+    int rc = check_sampling(params, n_seqs, &wide);
     if (rc) return rc;
     return spec_step(ctx, target, tkv, draft, dkv, seqs, n_seqs, k, params, rng, out_tokens, out_count,
                      out_accepted);

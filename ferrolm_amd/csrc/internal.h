@@ -175,9 +175,10 @@ int attn_qmax(int hd);
 constexpr int kAttnMfmaQueries = 16;
 
 // ---------------------------------------------------------------------------
-// Sampling (sampling.hip). A row's distribution holds at most kSampleCap
-// pairs (top_k 1..kSampleCap), stored in the reference's order (tok, pr) and
-// in token order (tok_id, pr_id), each [row][kSampleCap], with n[row] pairs.
+// Sampling (sampling.hip). A row's distribution is stored in the reference's
+// order (tok, pr) and, for top_k 1..kSampleCap, in token order (tok_id, pr_id),
+// each [row][cap], with n[row] pairs; wide rows (top_k 0 or above kSampleCap)
+// keep a dense by-token copy instead of the token-ordered pairs.
 // ---------------------------------------------------------------------------
 constexpr int kSampleCap = 1024;
 
@@ -192,7 +193,15 @@ struct SampleRows {
     uint32_t* tok_id;
     float* pr_id;
     int* n;
+    int cap;    // pairs per row: kSampleCap, or the vocabulary when any row is wide
+    int vocab;
+    float* dense;        // wide rows: probability by token [row][cap] (null: no wide rows)
+    uint32_t* scratch;   // wide rows: the sort's ping-pong keys and values [row][4 * cap]
 };
+// A row is wide when it samples with top_k 0 (no limit) or above kSampleCap.
+__host__ __device__ inline bool sample_wide(const SampleParams& p) {
+    return p.temperature > 0.0f && (p.top_k == 0 || p.top_k > kSampleCap);
+}
 
 // distributions of `rows` logits rows (row r uses prm[r / rows_per_seq])
 void launch_dist(hipStream_t st, const float* logits, int rows, int vocab, int rows_per_seq, const SampleParams* prm,

@@ -158,7 +158,7 @@ class Params:
 
     temperature: float = 0.0  # 0: greedy
     top_p: float = 1.0
-    top_k: int = 0  # the device draws with top_k 1..1024
+    top_k: int = 0  # 0: no limit
     seed: int = 0
     max_tokens: int = 64
     stop_ids: tuple = ()
@@ -260,8 +260,8 @@ class Engine:
         bad = next((t for t in req.prompt if t >= self.model.cfg.vocab), None)
         if bad is not None:
             return self._reject(req, f"token {bad} is outside the vocabulary")
-        if not req.params.greedy and not 1 <= req.params.top_k <= 1024:
-            return self._reject(req, "device sampling needs top_k in 1..1024")
+        if not req.params.greedy and req.params.top_k < 0:
+            return self._reject(req, "top_k must be 0 (no limit) or positive")
         self.stats.prompt_tokens += n
         self.waiting.append(_Seq(req))
         return req

@@ -70,8 +70,8 @@ class FgAwqChoice(C.Structure):
 @dataclass
 class SamplingParams:
     """The sampling fields of the reference's SamplingParams
-    (src/sampler.rs:8-19): temperature <= 0 is greedy; the device supports
-    top_k 1..1024. `seed` seeds the request's Rng (src/engine.rs:292-299)."""
+    (src/sampler.rs:8-19): temperature <= 0 is greedy; top_k 0 is no limit.
+    `seed` seeds the request's Rng (src/engine.rs:292-299)."""
     temperature: float = 0.0
     top_p: float = 1.0
     top_k: int = 0

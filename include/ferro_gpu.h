@@ -108,10 +108,9 @@ typedef struct {
 
 /* The sampling fields of SamplingParams (src/sampler.rs:8-19, :34-38):
  * temperature <= 0 is greedy; otherwise logits are divided by
- * max(temperature, 1e-5), cut to the top_k largest (1..1024 on the device:
- * the reference's 0, no limit, needs a whole-vocabulary sort and is
- * refused with FG_E_ARG) and to the shortest prefix whose probability
- * reaches top_p (1 keeps all). */
+ * max(temperature, 1e-5), cut to the top_k largest (0: no limit, the whole
+ * vocabulary; negative values are refused with FG_E_ARG) and to the
+ * shortest prefix whose probability reaches top_p (1 keeps all). */
 typedef struct {
     float temperature;
     float top_p;

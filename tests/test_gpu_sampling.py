@@ -24,7 +24,9 @@ from conftest import GOLDEN, chi_square, exact_two_token_distribution, reference
 pytestmark = pytest.mark.gpu
 
 PARAMS = [SamplingParams(1.0, 1.0, 4), SamplingParams(0.7, 0.9, 50), SamplingParams(1.3, 0.5, 1024),
-          SamplingParams(2.0, 1.0, 1), SamplingParams(0.8, 0.95, 300), SamplingParams(0.0, 1.0, 0)]
+          SamplingParams(2.0, 1.0, 1), SamplingParams(0.8, 0.95, 300), SamplingParams(0.0, 1.0, 0),
+          # wide rows: no top-k limit (the reference's default), and a limit above 1024
+          SamplingParams(1.0, 1.0, 0), SamplingParams(0.9, 0.9, 0), SamplingParams(1.1, 0.97, 3000)]
 
 
 def _tied_model():
@@ -42,7 +44,7 @@ def _tied_model():
 def test_forward_sampled_matches_the_oracle_on_device_logits(ctx):
     """Each selected row's token and the advanced generator state equal
     oracle.sample on the device's own logits of that row, over temperatures,
-    top-k 1..1024, top-p cuts, ties, several seeds, one row and several rows
+    top-k 1..1024, 0 (no limit) and above 1024, top-p cuts, ties, several seeds, one row and several rows
     in one call (each row its own parameters and generator)."""
     hm = _tied_model()
     m = gpu.Model(ctx, hm)
@@ -76,18 +78,19 @@ def test_forward_sampled_matches_the_oracle_on_device_logits(ctx):
             assert int(st[j]) == r.state
 
 
-def test_device_rejects_unbounded_top_k(ctx):
+def test_device_rejects_negative_top_k(ctx):
     hm = _tied_model()
     m = gpu.Model(ctx, hm)
     kv = gpu.KvCache(ctx, hm.cfg, 8)
     st = np.array([gpu.rng_init(1)], np.uint64)
     with pytest.raises(gpu.FgError, match="top_k"):
         gpu.forward_sampled(ctx, m, kv, [([5, 6, 7], 0, list(range(8)), gpu.LOGITS_LAST)],
-                            [SamplingParams(1.0, 0.9, 0)], st)
+                            [SamplingParams(1.0, 0.9, -1)], st)
 
 
-@pytest.mark.parametrize("params", [SamplingParams(1.0, 1.0, 4), SamplingParams(0.8, 0.9, 64)],
-                         ids=["t1-k4", "t0.8-p0.9-k64"])
+@pytest.mark.parametrize("params", [SamplingParams(1.0, 1.0, 4), SamplingParams(0.8, 0.9, 64),
+                                    SamplingParams(1.0, 1.0, 0), SamplingParams(0.9, 0.85, 0)],
+                         ids=["t1-k4", "t0.8-p0.9-k64", "t1-nolimit", "t0.9-p0.85-nolimit"])
 def test_spec_sampling_matches_the_oracle_engine(ctx, params):
     """Sampled speculative generation (one-layer draft, k=3) emits the
     oracle engine's tokens for the same seeds: the same draft draws,
@@ -151,3 +154,29 @@ def test_device_speculative_sampling_keeps_the_target_distribution(ctx):
     assert 0 < accepted < proposed
     assert c_plain < 37.7, c_plain
     assert c_spec < 37.7, c_spec
+
+
+def test_no_limit_sampling_at_the_full_vocabulary(ctx):
+    """top_k 0 over a 49152-token vocabulary (the SmolLM2 one): the sort, the
+    sequential sums and the top-p prefix of the whole distribution give the
+    oracle's tokens and generator states, several rows in one call."""
+    from ferrolm_amd.synth import random_model
+    from ferrolm_amd.weights import Config
+    cfg = Config(vocab=49152, hidden=64, intermediate=128, layers=1, heads=2, kv_heads=1, head_dim=32,
+                 rms_eps=1e-5, max_position=256, tie_embeddings=True)
+    hm = random_model(cfg, seed=3, std=0.3)
+    m = gpu.Model(ctx, hm)
+    rng = np.random.default_rng(5)
+    prompts = [[int(x) for x in rng.integers(3, 49000, n)] for n in (9, 21, 4)]
+    tables = [list(range(2 * i, 2 * i + 2)) for i in range(3)]
+    chunks = [(p, 0, t, gpu.LOGITS_LAST) for p, t in zip(prompts, tables)]
+    lg = gpu.forward(ctx, m, gpu.KvCache(ctx, cfg, 6), chunks).logits
+    ps = [SamplingParams(1.0, 1.0, 0), SamplingParams(0.7, 0.9, 0), SamplingParams(1.2, 0.5, 5000)]
+    for seed in (1, 2):
+        st = np.array([gpu.rng_init(seed * 10 + j) for j in range(3)], np.uint64)
+        tok = gpu.forward_sampled(ctx, m, gpu.KvCache(ctx, cfg, 6), chunks, ps, st)
+        for j in range(3):
+            r = oracle.Rng(seed * 10 + j)
+            p = ps[j]
+            assert int(tok[j]) == oracle.sample(lg[j], (p.temperature, p.top_p, p.top_k), r), (seed, j)
+            assert int(st[j]) == r.state
