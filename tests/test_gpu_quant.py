@@ -97,3 +97,18 @@ def test_reference_awq_test_on_the_device(ctx):
     print(f"device held-out relative logit error: int4 {e_plain:.4f}, int4+AWQ {e_awq:.4f}")
     assert all(x.error_awq <= x.error_plain for x in choices)
     assert e_awq < e_plain
+
+
+def test_device_awq_search_rejects_bad_arguments(ctx):
+    w = np.zeros((64, 64), np.float32)
+    with pytest.raises(gpu.FgError, match="calibration rows"):
+        gpu.awq_search(ctx, INT4, w, np.zeros((0, 64), np.float32))
+    with pytest.raises(gpu.FgError, match="input width"):
+        gpu.awq_search(ctx, INT4, w, np.zeros((4, 32), np.float32))
+    with pytest.raises(gpu.FgError, match="multiples of 32"):
+        gpu.awq_search(ctx, INT8, np.zeros((48, 64), np.float32), np.zeros((4, 64), np.float32))
+    # an all-zero matrix quantizes to zero codes and scales at every alpha, error 0
+    s, alpha, ep, ea, m = gpu.awq_search(ctx, INT4, w, np.random.default_rng(0).standard_normal((8, 64)).astype(
+        np.float32))
+    assert (alpha, ep, ea) == (0.0, 0.0, 0.0)
+    assert not m.s.any() and np.all(m.q == 0x88)
