@@ -524,8 +524,10 @@ static int kind_of(const DMat& m) { return m.kind; }
 // narrower than kGemmMinHidden keeps the GEMV at any row count: its small
 // projections finish sooner on the GEMV (measured: the 135M shape's at 8 to
 // 64 rows), while the lm_head, a large product either way, switches at
-// kGemvRows for every model.
-static constexpr int kGemvRows = 16;
+// kGemvRows for every model. At exactly 16 rows a 2048-wide bf16 model is
+// faster on the GEMM (measured: cfg4's 1B draft rounds of 16 sequences, 7.15
+// against 6.85 ms per step), so 16-row steps take the GEMM.
+static constexpr int kGemvRows = 15;
 static constexpr int kGemmMinHidden = 1024;
 
 // n-tiles per workgroup of a bf16 projection with fewer than 256 tiles: one, so
@@ -615,7 +617,7 @@ static int run_forward(fg_ctx* ctx, const fg_model* m, fg_kv* kv, const Plan& P,
     if (t == 0) return 0;
     const int passes = w.passes;
     int cur = 0;  // pieces buffer the next GEMV reads
-    // more than 16 rows (of a wide enough model): every projection runs as a GEMM on MM pieces
+    // 16 rows or more (of a wide enough model): every projection runs as a GEMM on MM pieces
     const bool mm = t > kGemvRows && H >= kGemmMinHidden;
     auto ck = [&](const DMat& d) { return mm ? (int)MM : kind_of(d); };
 

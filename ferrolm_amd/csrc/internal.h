@@ -35,7 +35,7 @@ namespace fg {
 // ---------------------------------------------------------------------------
 enum { BF16 = 0, INT8 = 1, INT4 = 2 };
 // Activation operand formats ("pieces", below): BF16 and INT8 for the GEMV
-// consumers, MM for the GEMM consumers (more than 16 rows).
+// consumers, MM for the GEMM consumers (16 rows or more).
 enum { MM = 3 };
 
 struct DMat {
