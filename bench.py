@@ -166,6 +166,8 @@ def main() -> int:
                     "bytes_per_launch": round(dom["bytes"] / dom["launches"]),
                     "us_per_launch": round(dom["us"] / dom["launches"], 3), "launches": dom["launches"]}
 
+    prefill = measure_prefill(ctx, target, draft, prompt, first[0])
+
     cpu = None
     parity = None
     if snap is not None:
@@ -218,10 +220,47 @@ def main() -> int:
                    "target_layers": cfg.layers, "hidden": cfg.hidden, "k": k, "batch": wl.batch,
                    "prompt": wl.prompt_len, "context_at_timed_start": ctx_start},
         "verify_step_us": round(verify_us, 2), "draft_us": round(draft_us, 2), "acceptance": round(acceptance, 4),
-        "roofline": roofline, "cpu_baseline": cpu, "parity": parity,
+        "roofline": roofline, "cpu_baseline": cpu, "parity": parity, "prefill": prefill,
     }
     print(json.dumps(line), flush=True)
     return 0
+
+
+def measure_prefill(ctx, target, draft, prompt, first_token, reps=5):
+    """Time to first token of the prompt: one forward of the whole prompt
+    through each model (the target's gives the first token; the draft's runs in
+    the first speculative step), warm, into caches of their own so the
+    speculative state is untouched. Wall time per forward, host planning and
+    launches included. `tflops` is the target's algorithmic rate: 2 flops per
+    weight per token, the lm_head for the last row only, and causal attention
+    (QK and PV, 4·hd flops per query head and visible position)."""
+    from ferrolm_amd import gpu
+    n = len(prompt)
+    nb = (n + 15) // 16
+    ch = [(prompt, 0, list(range(nb)), gpu.LOGITS_LAST)]
+    out = {"tokens": n, "reps": reps}
+    for name, m in (("target", target), ("draft", draft)):
+        kv = gpu.KvCache(ctx, m.cfg, nb)
+        o = gpu.forward(ctx, m, kv, ch, logits=False)
+        if name == "target" and int(o.argmax[0]) != first_token:
+            raise RuntimeError("a second prefill of the prompt gave another first token")
+        ctx.sync()
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            gpu.forward(ctx, m, kv, ch, logits=False)
+        ctx.sync()
+        out[f"{name}_ms"] = round((time.perf_counter() - t0) / reps * 1e3, 3)
+        del kv
+    c = target.cfg
+    qd, kvd = c.heads * c.head_dim, c.kv_heads * c.head_dim
+    layer_params = c.hidden * (qd + 2 * kvd) + qd * c.hidden + 3 * c.intermediate * c.hidden
+    flops = (2.0 * n * layer_params * c.layers + 2.0 * c.vocab * c.hidden
+             + 4.0 * c.head_dim * c.heads * (n * (n + 1) / 2) * c.layers)
+    out["target_tok_per_s"] = round(n / out["target_ms"] * 1e3, 1)
+    out["target_tflops"] = round(flops / (out["target_ms"] * 1e-3) / 1e12, 1)
+    log(f"prefill of {n} tokens (warm, {reps} reps): target {out['target_ms']:.2f} ms "
+        f"({out['target_tok_per_s']:.0f} tok/s, {out['target_tflops']:.0f} TFLOP/s), draft {out['draft_ms']:.2f} ms")
+    return out
 
 
 def run_batched(a, wl, ctx, target, draft) -> int:

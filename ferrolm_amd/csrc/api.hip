@@ -521,14 +521,19 @@ static int kind_of(const DMat& m) { return m.kind; }
 
 // Steps with more rows than this run their projections as GEMMs (k_gemm on
 // MM pieces); up to this many rows, as GEMVs on BF16/INT8 pieces. A model
-// narrower than kGemmMinHidden keeps the GEMV at any row count: its small
-// projections finish sooner on the GEMV (measured: the 135M shape's at 8 to
-// 64 rows), while the lm_head, a large product either way, switches at
-// kGemvRows for every model. At exactly 16 rows a 2048-wide bf16 model is
-// faster on the GEMM (measured: cfg4's 1B draft rounds of 16 sequences, 7.15
-// against 6.85 ms per step), so 16-row steps take the GEMM.
+// narrower than kGemmMinHidden keeps the GEMV below kNarrowGemmRows rows:
+// its small projections finish sooner on the GEMV (measured on the 135M
+// shape, one forward: 16 rows 1.18 against 1.39 ms, 128 rows 1.71 against
+// 1.98), while from 256 rows the GEMM wins (2.07 against 2.20 ms; a
+// 1024-token prompt 4.51 against 6.11). The lm_head, a large product either
+// way, switches at kGemvRows for every model. At exactly 16 rows a
+// 2048-wide bf16 model is faster on the GEMM (measured: cfg4's 1B draft
+// rounds of 16 sequences, 7.15 against 6.85 ms per step), so 16-row steps
+// take the GEMM.
 static constexpr int kGemvRows = 15;
 static constexpr int kGemmMinHidden = 1024;
+static constexpr int kNarrowGemmRows = 256;
+static bool step_gemm(int t, int H) { return t > kGemvRows && (H >= kGemmMinHidden || t >= kNarrowGemmRows); }
 
 // n-tiles per workgroup of a bf16 projection with fewer than 256 tiles: one, so
 // that it spreads over twice the CUs (a CU streams only about 22 GB/s), unless
@@ -572,7 +577,7 @@ static size_t layout_work(const fg_model* m, const Plan& P, Work& w, void* base)
     w.best = cv.take<float2>((size_t)(c.vocab / 32) * S);
     w.am = cv.take<uint32_t>(S);
     // the split rule keeps splits x rows x N within 64 x 256 x 64 floats
-    w.kpart_cap = (t > kGemvRows && H >= kGemmMinHidden) || S > kGemvRows ? (size_t)1 << 20 : 0;
+    w.kpart_cap = step_gemm(t, H) || S > kGemvRows ? (size_t)1 << 20 : 0;
     w.kpart = w.kpart_cap ? cv.take<float>(w.kpart_cap) : nullptr;
     return cv.off + 256;
 }
@@ -618,7 +623,7 @@ static int run_forward(fg_ctx* ctx, const fg_model* m, fg_kv* kv, const Plan& P,
     const int passes = w.passes;
     int cur = 0;  // pieces buffer the next GEMV reads
     // 16 rows or more (of a wide enough model): every projection runs as a GEMM on MM pieces
-    const bool mm = t > kGemvRows && H >= kGemmMinHidden;
+    const bool mm = step_gemm(t, H);
     auto ck = [&](const DMat& d) { return mm ? (int)MM : kind_of(d); };
 
     if (L > 0) {

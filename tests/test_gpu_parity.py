@@ -366,3 +366,42 @@ def test_long_gqa_prefill_runs_multi_span_attention(ctx, hd, heads, kv_heads, n)
         ok, ov = okv.layer(li)
         assert np.abs(gk - ok).max() <= 1e-4 * np.abs(ok).max()
         assert np.abs(gv - ov).max() <= 1e-4 * np.abs(ov).max()
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("kind", [BF16, INT8, INT4], ids=["bf16", "int8", "int4"])
+def test_narrow_model_long_prefill_takes_the_gemm(ctx, kind):
+    """A model narrower than 1024 (the 135M draft's 576: 18 k-blocks, padded
+    to 20 on the device) runs a prefill of 256 rows or more on the GEMM.
+    All logits, the hidden states and the cache slots against the oracle,
+    and the profiler's records show every projection on the GEMM path."""
+    from ferrolm_amd.synth import quantize_model, random_model
+    from ferrolm_amd.weights import Config
+    cfg = Config(vocab=512, hidden=576, intermediate=1536, layers=2, heads=9, kv_heads=3, head_dim=64,
+                 rms_eps=1e-5, rope_theta=100000.0, max_position=2048)
+    hm = quantize_model(random_model(cfg, seed=61, std=0.05), kind)
+    n = 300
+    prompt = [int(x) for x in np.random.default_rng(62).integers(3, 500, n)]
+    table, blocks = scattered_table(n)
+    m = gpu.Model(ctx, hm)
+    kv = gpu.KvCache(ctx, hm.cfg, blocks)
+    gpu.profile(ctx, True)
+    gpu.profile_read(ctx, reset=True)
+    try:
+        out = gpu.forward(ctx, m, kv, [(prompt, 0, table, gpu.LOGITS_ALL)], hidden=True)
+        recs = gpu.profile_read(ctx, reset=True)
+    finally:
+        gpu.profile(ctx, False)
+    assert sum(r["launches"] for r in recs if r["gemm"]) >= 1 + 4 * cfg.layers, recs
+    assert not any(r["launches"] for r in recs if not r["gemm"]), recs
+    om = oracle.Model(hm)
+    okv = om.kv(blocks)
+    ol, oh = om.forward(okv, [(prompt, 0, table, 2)], hidden=True)
+    assert np.abs(out.logits - ol).max() < 1e-4 * np.abs(ol).max()
+    rel = np.linalg.norm(out.hidden - oh, axis=-1) / np.linalg.norm(oh, axis=-1)
+    assert rel.max() < 1e-4, rel.max()
+    for li in range(cfg.layers):
+        gk, gv = kv.layer(li)
+        ok, ov = okv.layer(li)
+        assert np.abs(gk - ok).max() <= 1e-4 * np.abs(ok).max()
+        assert np.abs(gv - ov).max() <= 1e-4 * np.abs(ov).max()
