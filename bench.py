@@ -64,6 +64,8 @@ def main() -> int:
                     help="serve 32 requests with a shared prefix through the engine (continuous batching) instead")
     ap.add_argument("--awq", action="store_true",
                     help="time the AWQ alpha search (fg_awq_search) of one 1.7B-shape layer instead")
+    ap.add_argument("--prefill", action="store_true",
+                    help="only time the warm prefill of the config's prompt through the target and the draft")
     ap.add_argument("--copy-calib", type=int, default=0, metavar="MIB",
                     help="only run a plain device copy of MIB MiB and exit (calibrates rocprofv3 FETCH_SIZE/WRITE_SIZE)")
     a = ap.parse_args()
@@ -101,6 +103,10 @@ def main() -> int:
         return run_batched(a, wl, ctx, target, draft)
     cfg = wl.target.cfg
     prompt = synth.prompt_ids(wl.prompt_len, cfg.vocab, a.seed)
+    if a.prefill:
+        print(json.dumps({"workload": wl.name, "prefill": measure_prefill(ctx, target, draft, prompt, None)}),
+              flush=True)
+        return 0
     k = wl.k
     total_steps = a.warmup + 2 * a.steps
     kv_blocks = (wl.prompt_len + total_steps * (k + 1) + 64) // 16 + 1
@@ -230,7 +236,8 @@ def measure_prefill(ctx, target, draft, prompt, first_token, reps=5):
     """Time to first token of the prompt: one forward of the whole prompt
     through each model (the target's gives the first token; the draft's runs in
     the first speculative step), warm, into caches of their own so the
-    speculative state is untouched. Wall time per forward, host planning and
+    speculative state is untouched (first_token, when given, is checked against
+    the target's). Wall time per forward, host planning and
     launches included. `tflops` is the target's algorithmic rate: 2 flops per
     weight per token, the lm_head for the last row only, and causal attention
     (QK and PV, 4·hd flops per query head and visible position)."""
@@ -242,7 +249,7 @@ def measure_prefill(ctx, target, draft, prompt, first_token, reps=5):
     for name, m in (("target", target), ("draft", draft)):
         kv = gpu.KvCache(ctx, m.cfg, nb)
         o = gpu.forward(ctx, m, kv, ch, logits=False)
-        if name == "target" and int(o.argmax[0]) != first_token:
+        if name == "target" and first_token is not None and int(o.argmax[0]) != first_token:
             raise RuntimeError("a second prefill of the prompt gave another first token")
         ctx.sync()
         t0 = time.perf_counter()

@@ -338,7 +338,8 @@ def test_output_projection_merge_matches_separate_merge(ctx, shape, monkeypatch)
         pos += len(toks)
 
 
-@pytest.mark.parametrize("hd,heads,kv_heads,n", [(64, 16, 4, 1100), (128, 8, 2, 700)], ids=["hd64", "hd128"])
+@pytest.mark.parametrize("hd,heads,kv_heads,n", [(64, 16, 4, 1100), (128, 8, 2, 700), (64, 16, 16, 520)],
+                         ids=["hd64", "hd128", "mha-hd64"])
 def test_long_gqa_prefill_runs_multi_span_attention(ctx, hd, heads, kv_heads, n):
     """A prefill of n tokens whose row groups hold 32 queries (8 rows x GQA 4)
     launches more than 1024 attention work items of one span, so each item
