@@ -152,6 +152,12 @@ struct AttnArgs {
     int n_wi, nh, nkv, hd, bs;
     int ns;  // sub-spans of attn_span(hd) positions per work item (1, 2 or 4; at most 128 positions)
     float scale;
+    // Long chunks at hd 64: the records are parts of items of up to 2 * (32 / G)
+    // rows (p0, p1 the part's positions, word 6 the offset of the chunk's block
+    // table in btab, words 7 and 8 the partial slots of the two row halves);
+    // n_wi counts the partial slots, two per part.
+    int flash;
+    const int32_t* btab;
 };
 // Attention over the paged cache (RoPE, K/V write of the new rows), then the
 // split merge straight into the output projection's pieces (consumer_kind < 0:

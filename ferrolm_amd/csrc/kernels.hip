@@ -1705,6 +1705,210 @@ __global__ __launch_bounds__(256, 2) void k_attn(AttnArgs a) {
     }
 }
 
+// Long-chunk attention (prefill at hd 64): one workgroup per (kv head, item),
+// an item being up to 2 * (32 / G) consecutive rows of one chunk (at most 64
+// queries, G query heads per kv head). The workgroup walks every position the
+// item's last row sees (or a part of them) in blocks of 64: keys (rotated when new) and values go
+// through LDS, shared by the four waves; each wave owns 16 queries and keeps
+// their online softmax (running max and sum, weighted values) in registers,
+// scores and weighted values on f32 MFMA. The next block's loads are issued
+// before the current one is scored. The item's two row halves write their
+// partials (max score, sum of exponentials, weighted values) to the work-item
+// slots their record names: the layout the span merge reads, one span per part.
+template <int HD>
+__global__ __launch_bounds__(256, 2) void k_attn_flash(AttnArgs a) {
+    constexpr int P = 64, HALF = HD / 2, QM = 32, NTD = HD / 16;
+    __shared__ __align__(16) float ks[P][HD + 4];
+    __shared__ __align__(16) float vs[P][HD + 4];
+    __shared__ __align__(16) float qs[64][HD + 4];
+    __shared__ __align__(16) float pw[4][16][P + 4];
+    __shared__ int lim[64];
+
+    const int h = blockIdx.x, fi = blockIdx.y;
+    const int4* rec = (const int4*)(a.wrec + (size_t)fi * 16);
+    const int4 r0 = rec[0], r1 = rec[1], r2 = rec[2];
+    const int row0 = r0.x, nrows = r0.y, crow0 = r0.z, cpos0 = r0.w;
+    // the part's positions [p0, L), the chunk's block table, the partial slots of the two row halves
+    const int p0 = r1.x, L = r1.y, boff = r1.z, slot0 = r1.w, slot1 = r2.x;
+    if (nrows == 0) return;  // an unused slot of the launch's capacity
+    const int G = a.nh / a.nkv, Q = nrows * G, RQ = QM / G;
+    const int qd = a.nh * HD;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int kk = lane >> 4, c16 = lane & 15;
+    const int32_t* bt = a.btab + boff;
+    const int pos_of_row0 = cpos0 + row0 - crow0;
+    for (int q = tid; q < 64; q += 256) lim[q] = q < Q ? pos_of_row0 + q / G : -1;
+
+    // position p's key (col 0) or value (col HD * nkv): the cache, or this chunk's q/k/v rows
+    auto src_of = [&](int p, int col) -> const float* {
+        return p < cpos0 ? (col ? a.vc : a.kc) + (((size_t)(uint32_t)bt[p >> 4] * a.nkv + h) * 16 + (p & 15)) * HD
+                         : a.qkv + (size_t)(crow0 + p - cpos0) * a.ld + qd + col + h * HD;
+    };
+    constexpr int KIT = P * (HALF / 4) / 256, VIT = P * (HD / 4) / 256;
+    static_assert(KIT * 256 == P * (HALF / 4) && VIT * 256 == P * (HD / 4), "whole iterations");
+    float4 ku[KIT], kw[KIT], kcs[KIT], ksn[KIT], vv[VIT];
+    auto load_blk = [&](int b0) {
+#pragma unroll
+        for (int it = 0; it < KIT; it++) {
+            const int i = tid + it * 256, d = (i % (HALF / 4)) * 4, p = min(b0 + i / (HALF / 4), L - 1);
+            const float* kp = src_of(p, 0);
+            ku[it] = ld_nt_f4(kp + d);
+            kw[it] = ld_nt_f4(kp + d + HALF);
+            const int pr = max(p, cpos0);
+            kcs[it] = *(const float4*)(a.cos_t + (size_t)pr * HALF + d);
+            ksn[it] = *(const float4*)(a.sin_t + (size_t)pr * HALF + d);
+        }
+#pragma unroll
+        for (int it = 0; it < VIT; it++) {
+            const int i = tid + it * 256, d = (i % (HD / 4)) * 4, p = min(b0 + i / (HD / 4), L - 1);
+            vv[it] = ld_nt_f4(src_of(p, a.nkv * HD) + d);
+        }
+    };
+    load_blk(p0);
+    // the queries, rotated; rows past Q are zero
+    for (int i = tid; i < 64 * (HALF / 4); i += 256) {
+        const int q = i / (HALF / 4), d = (i % (HALF / 4)) * 4;
+        float r1v[4] = {0, 0, 0, 0}, r2v[4] = {0, 0, 0, 0};
+        if (q < Q) {
+            const int r = q / G, j = q % G, pos = pos_of_row0 + r;
+            const float* src = a.qkv + (size_t)(row0 + r) * a.ld + (size_t)(h * G + j) * HD;
+            const float4 x1 = *(const float4*)(src + d), x2 = *(const float4*)(src + d + HALF);
+            const float4 c = *(const float4*)(a.cos_t + (size_t)pos * HALF + d);
+            const float4 sn = *(const float4*)(a.sin_t + (size_t)pos * HALF + d);
+            const float a1[4] = {x1.x, x1.y, x1.z, x1.w}, a2[4] = {x2.x, x2.y, x2.z, x2.w};
+            const float cc[4] = {c.x, c.y, c.z, c.w}, ss[4] = {sn.x, sn.y, sn.z, sn.w};
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                r1v[e] = __fadd_rn(__fmul_rn(a1[e], cc[e]), __fmul_rn(-a2[e], ss[e]));
+                r2v[e] = __fadd_rn(__fmul_rn(a2[e], cc[e]), __fmul_rn(a1[e], ss[e]));
+            }
+        }
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            qs[q][d + e] = r1v[e];
+            qs[q][d + HALF + e] = r2v[e];
+        }
+    }
+
+    float mrow[4], lrow[4];
+    f32x4 oc[NTD];
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+        mrow[r] = -INFINITY;
+        lrow[r] = 0.0f;
+    }
+#pragma unroll
+    for (int j = 0; j < NTD; j++) oc[j] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
+    const int nblk = (L - p0 + P - 1) / P;
+    const int q0 = wave * 16;
+    for (int b = 0; b < nblk; b++) {
+        const int b0 = p0 + b * P;
+        if (b > 0) __syncthreads();  // the previous block's readers of ks, vs and pw are done
+#pragma unroll
+        for (int it = 0; it < KIT; it++) {
+            const int i = tid + it * 256, o = i / (HALF / 4), d = (i % (HALF / 4)) * 4, p = b0 + o;
+            const float a1[4] = {ku[it].x, ku[it].y, ku[it].z, ku[it].w};
+            const float a2[4] = {kw[it].x, kw[it].y, kw[it].z, kw[it].w};
+            const float cc[4] = {kcs[it].x, kcs[it].y, kcs[it].z, kcs[it].w};
+            const float ss[4] = {ksn[it].x, ksn[it].y, ksn[it].z, ksn[it].w};
+            const bool live = p < L, rot = live && p >= cpos0;
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const float x1 = rot ? __fadd_rn(__fmul_rn(a1[e], cc[e]), __fmul_rn(-a2[e], ss[e])) : a1[e];
+                const float x2 = rot ? __fadd_rn(__fmul_rn(a2[e], cc[e]), __fmul_rn(a1[e], ss[e])) : a2[e];
+                ks[o][d + e] = live ? x1 : 0.0f;
+                ks[o][d + HALF + e] = live ? x2 : 0.0f;
+            }
+        }
+#pragma unroll
+        for (int it = 0; it < VIT; it++) {
+            const int i = tid + it * 256, o = i / (HD / 4), d = (i % (HD / 4)) * 4;
+            const bool live = b0 + o < L;
+            *(float4*)&vs[o][d] = make_float4(live ? vv[it].x : 0.0f, live ? vv[it].y : 0.0f,
+                                              live ? vv[it].z : 0.0f, live ? vv[it].w : 0.0f);
+        }
+        __syncthreads();
+        if (b + 1 < nblk) load_blk(b0 + P);
+        // this item's new rows in the block go to the cache
+        {
+            const int n0 = max(b0, pos_of_row0), n1 = min(b0 + P, pos_of_row0 + nrows);
+            for (int i = tid; i < (n1 - n0) * HD; i += 256) {
+                const int p = n0 + i / HD, d = i % HD, o = p - b0;
+                const size_t at = (((size_t)(uint32_t)bt[p >> 4] * a.nkv + h) * 16 + (p & 15)) * HD + d;
+                a.kc[at] = ks[o][d];
+                a.vc[at] = vs[o][d];
+            }
+        }
+        // the wave's 16 x 64 scores (v_mfma_f32_16x16x4f32: A[i][k] in lane i + 16k,
+        // B[k][j] in lane j + 16k, D[4(l/16) + r][l%16] in register r of lane l)
+        f32x4 sc[P / 16];
+#pragma unroll
+        for (int nt = 0; nt < P / 16; nt++) {
+            const float* qa = &qs[q0 + c16][kk];
+            const float* kb = &ks[nt * 16 + c16][kk];
+            f32x4 c = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int d0 = 0; d0 < HD; d0 += 4) c = __builtin_amdgcn_mfma_f32_16x16x4f32(qa[d0], kb[d0], c, 0, 0, 0);
+            sc[nt] = c;
+        }
+        // online softmax of each of the lane's four query rows; a row's 64 scores
+        // sit in the 16 lanes of its lane group, four per lane
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const int lq = lim[q0 + 4 * kk + r];
+            float mx = -INFINITY;
+#pragma unroll
+            for (int nt = 0; nt < P / 16; nt++) {
+                const float v = b0 + nt * 16 + c16 <= lq ? sc[nt][r] * a.scale : -INFINITY;
+                sc[nt][r] = v;
+                mx = fmaxf(mx, v);
+            }
+#pragma unroll
+            for (int off = 8; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 16));
+            const float mn = fmaxf(mrow[r], mx);
+            const float f = mrow[r] == -INFINITY ? 0.0f : dev_exp(mrow[r] - mn);
+            float sum = 0.0f;
+#pragma unroll
+            for (int nt = 0; nt < P / 16; nt++) {
+                const float e = sc[nt][r] == -INFINITY ? 0.0f : dev_exp(sc[nt][r] - mn);
+                pw[wave][4 * kk + r][nt * 16 + c16] = e;
+                sum += e;
+            }
+#pragma unroll
+            for (int off = 8; off > 0; off >>= 1) sum += __shfl_xor(sum, off, 16);
+            lrow[r] = fmaf(lrow[r], f, sum);
+            mrow[r] = mn;
+#pragma unroll
+            for (int j = 0; j < NTD; j++) oc[j][r] *= f;
+        }
+        __syncthreads();  // pw rows are read across the wave's lanes
+        // weighted values: O += P V over the block's 64 positions
+#pragma unroll
+        for (int j = 0; j < NTD; j++) {
+            const float* pa = &pw[wave][c16][kk];
+            const float* vb = &vs[kk][j * 16 + c16];
+#pragma unroll
+            for (int k0 = 0; k0 < P; k0 += 4)
+                oc[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(pa[k0], vb[k0 * (HD + 4)], oc[j], 0, 0, 0);
+        }
+    }
+    // the partials of the item's two row halves
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+        const int q = q0 + 4 * kk + r;
+        if (q < Q) {
+            const int half = q / G >= RQ ? 1 : 0;
+            float* pq = a.part + (((size_t)(half ? slot1 : slot0) * a.nkv + h) * QM + (q - half * RQ * G)) * (HD + 4);
+            if (c16 == 0) {
+                pq[0] = mrow[r];
+                pq[1] = lrow[r];
+            }
+#pragma unroll
+            for (int j = 0; j < NTD; j++) pq[4 + j * 16 + c16] = oc[j][r];
+        }
+    }
+}
+
 // Merge of the spans of each (row, head) into the attention output, written
 // as the output projection's pieces. One wave per (k-block, pass); the four
 // lanes of a (row, 8 dims) pair (one per piece) share the spans.
@@ -1722,12 +1926,19 @@ __global__ __launch_bounds__(64) void k_merge_pieces(AttnArgs a, int m, void* __
 
 template <int HD, int P, int QM>
 static void attention_hd(hipStream_t st, const AttnArgs& a, int m, int ck, Pieces& out) {
+    if constexpr (HD == 64 && QM == 32) {
+        if (a.flash) {
+            hipLaunchKernelGGL(k_attn_flash<HD>, dim3(a.nkv, a.n_wi / 2), dim3(256), 0, st, a);
+            goto merge;
+        }
+    }
     if (a.ns >= 4 && 4 * P <= 128)
         hipLaunchKernelGGL((k_attn<HD, P, QM, (4 * P <= 128 ? 4 : 1)>), dim3(a.nkv, a.n_wi), dim3(256), 0, st, a);
     else if (a.ns >= 2 && 2 * P <= 128)
         hipLaunchKernelGGL((k_attn<HD, P, QM, (2 * P <= 128 ? 2 : 1)>), dim3(a.nkv, a.n_wi), dim3(256), 0, st, a);
     else
         hipLaunchKernelGGL((k_attn<HD, P, QM, 1>), dim3(a.nkv, a.n_wi), dim3(256), 0, st, a);
+merge:
     if (ck < 0) return;  // the consumer merges the spans itself
     if (ck == BF16)
         hipLaunchKernelGGL((k_merge_pieces<HD, QM, BF16>), dim3(out.kb, out.passes), dim3(64), 0, st, a, m, out.a,

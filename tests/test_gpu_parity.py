@@ -406,3 +406,43 @@ def test_narrow_model_long_prefill_takes_the_gemm(ctx, kind):
         ok, ov = okv.layer(li)
         assert np.abs(gk - ok).max() <= 1e-4 * np.abs(ok).max()
         assert np.abs(gv - ov).max() <= 1e-4 * np.abs(ov).max()
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("heads,kv_heads", [(32, 32), (27, 9)], ids=["mha", "gqa3"])
+def test_flash_prefill_attention_across_chunks_and_sequences(ctx, heads, kv_heads):
+    """Long hd-64 chunks run the flash attention items (64 rows of an MHA
+    model, 20 of a GQA-3 one, each walking the positions it sees in blocks of
+    64, split into parts of at most four blocks merged as spans). Two forwards:
+    the first 520 tokens of one sequence; then its remaining 580 tokens (the
+    items read the cached 520 positions) beside a fresh 300-token sequence.
+    All logits, the hidden states and both sequences' cache slots against the
+    oracle running the same chunks."""
+    from ferrolm_amd.synth import random_model
+    from ferrolm_amd.weights import Config
+    cfg = Config(vocab=512, hidden=heads * 64, intermediate=512, layers=2, heads=heads, kv_heads=kv_heads,
+                 head_dim=64, rms_eps=1e-5, rope_theta=10000.0, max_position=2048)
+    hm = random_model(cfg, seed=71, std=0.03)
+    rng = np.random.default_rng(72)
+    a = [int(x) for x in rng.integers(3, 500, 1100)]
+    b = [int(x) for x in rng.integers(3, 500, 300)]
+    ta, na = scattered_table(1100)
+    tb, nb = scattered_table(300)
+    tb = [x + na for x in tb]
+    m = gpu.Model(ctx, hm)
+    kv = gpu.KvCache(ctx, hm.cfg, na + nb)
+    om = oracle.Model(hm)
+    okv = om.kv(na + nb)
+    steps = [[(a[:520], 0, ta, gpu.LOGITS_ALL)],
+             [(a[520:], 520, ta, gpu.LOGITS_ALL), (b, 0, tb, gpu.LOGITS_ALL)]]
+    for chunks in steps:
+        out = gpu.forward(ctx, m, kv, chunks, hidden=True)
+        ol, oh = om.forward(okv, [(t, p, tab, 2) for t, p, tab, _ in chunks], hidden=True)
+        assert np.abs(out.logits - ol).max() < 1e-4 * np.abs(ol).max()
+        rel = np.linalg.norm(out.hidden - oh, axis=-1) / np.linalg.norm(oh, axis=-1)
+        assert rel.max() < 1e-4, rel.max()
+    for li in range(cfg.layers):
+        gk, gv = kv.layer(li)
+        ok, ov = okv.layer(li)
+        assert np.abs(gk - ok).max() <= 1e-4 * np.abs(ok).max()
+        assert np.abs(gv - ov).max() <= 1e-4 * np.abs(ov).max()
