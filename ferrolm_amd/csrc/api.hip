@@ -415,9 +415,6 @@ struct Plan {
     size_t o_wrec, o_mrec, o_sel, o_tok, o_btab, words;
 };
 
-// Flash attention parts: at most this many blocks of 64 positions (measured on
-// the 1.7B shape's 1024-token prefill: 15.7 ms unsplit, 15.5 at 8, 15.3 at 4).
-static constexpr int kFlashBlocks = 4;
 
 static int build_plan(const fg_config& c, const fg_kv& kv, int max_pos, const ChunkIn* ch, int nch, Plan& P) {
     const int bs = kv.block_size;
@@ -448,13 +445,15 @@ static int build_plan(const fg_config& c, const fg_kv& kv, int max_pos, const Ch
         }
     P.ns = w1 * c.kv_heads > 1024 && maxq >= kAttnMfmaQueries ? 128 / span1 : 1;
     const int span = span1 * P.ns;
-    // Long chunks at hd 64 take the flash items (rf rows each, split into parts
-    // of at most kFlashBlocks blocks of 64 positions) when there are at least 256
-    // rows and enough parts to spread over the CUs.
+    // Long chunks at hd 64 and 128 take the flash items (rf rows each, split into
+    // parts of at most kFlashPart positions: on the 1.7B shape's 1024-token
+    // prefill 15.7 ms unsplit, 15.5 at 512, 15.3 at 256) when there are at least
+    // 256 rows and enough parts to spread over the CUs.
     const int rf = 2 * (attn_qmax(c.head_dim) / group);
-    auto flash_parts = [](int L) {
-        const int nb = (L + 63) / 64;
-        return (nb + kFlashBlocks - 1) / kFlashBlocks;
+    const int fblk = kFlashBlock(c.head_dim);
+    auto flash_parts = [&](int L) {
+        const int nb = (L + fblk - 1) / fblk, per = kFlashPart / fblk;
+        return (nb + per - 1) / per;
     };
     {
         int64_t parts = 0, rows = 0;
@@ -465,7 +464,7 @@ static int build_plan(const fg_config& c, const fg_kv& kv, int max_pos, const Ch
                     for (int r0 = 0; r0 < ch[ci].n; r0 += rf)
                         parts += flash_parts(ch[ci].pos + r0 + std::min(rf, ch[ci].n - r0));
             }
-        P.flash = c.head_dim == 64 && rf >= 2 && rows >= 256 && parts * c.kv_heads >= 256;
+        P.flash = (c.head_dim == 64 || c.head_dim == 128) && rf >= 2 && rows >= 256 && parts * c.kv_heads >= 256;
         if (P.flash) P.ns = 1;
     }
     for (int ci = 0; ci < nch; ci++) {
@@ -495,11 +494,11 @@ static int build_plan(const fg_config& c, const fg_kv& kv, int max_pos, const Ch
                 // an item whose rows see more than kFlashBlocks blocks of 64 positions
                 // is split into parts of even length, each writing its own partials
                 // (the merge combines them as spans)
-                const int nr = std::min(rf, k.n - r0), L = k.pos + r0 + nr, nb = (L + 63) / 64;
+                const int nr = std::min(rf, k.n - r0), L = k.pos + r0 + nr, nb = (L + fblk - 1) / fblk;
                 const int parts = flash_parts(L), per = (nb + parts - 1) / parts;
                 const int base = P.W;
                 for (int sp = 0; sp < parts; sp++) {
-                    const int p0 = sp * per * 64, p1 = std::min(L, (sp + 1) * per * 64);
+                    const int p0 = sp * per * fblk, p1 = std::min(L, (sp + 1) * per * fblk);
                     const int32_t rec[16] = {row_base + r0, nr,   row_base, k.pos, p0, p1, boff, base + sp,
                                              base + parts + sp, 0, 0, 0, 0, 0, 0, 0};
                     P.wrec.insert(P.wrec.end(), rec, rec + 16);

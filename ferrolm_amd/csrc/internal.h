@@ -152,7 +152,7 @@ struct AttnArgs {
     int n_wi, nh, nkv, hd, bs;
     int ns;  // sub-spans of attn_span(hd) positions per work item (1, 2 or 4; at most 128 positions)
     float scale;
-    // Long chunks at hd 64: the records are parts of items of up to 2 * (32 / G)
+    // Long chunks at hd 64 and 128: the records are parts of items of up to 2 * (32 / G)
     // rows (p0, p1 the part's positions, word 6 the offset of the chunk's block
     // table in btab, words 7 and 8 the partial slots of the two row halves);
     // n_wi counts the partial slots, two per part.
@@ -179,6 +179,9 @@ int attn_qmax(int hd);
 // several sub-spans when the launch is large (k_attn's NS): the loads of the
 // next sub-span then overlap MFMA work worth hiding them behind.
 constexpr int kAttnMfmaQueries = 16;
+// Positions per block of the flash attention items, and per part of an item.
+constexpr int kFlashBlock(int hd) { return hd >= 128 ? 32 : 64; }
+constexpr int kFlashPart = 256;
 
 // ---------------------------------------------------------------------------
 // Sampling (sampling.hip). A row's distribution is stored in the reference's

@@ -1705,19 +1705,21 @@ __global__ __launch_bounds__(256, 2) void k_attn(AttnArgs a) {
     }
 }
 
-// Long-chunk attention (prefill at hd 64): one workgroup per (kv head, item),
+// Long-chunk attention (prefill at hd 64 and 128): one workgroup per (kv head, item),
 // an item being up to 2 * (32 / G) consecutive rows of one chunk (at most 64
 // queries, G query heads per kv head). The workgroup walks every position the
-// item's last row sees (or a part of them) in blocks of 64: keys (rotated when new) and values go
+// item's last row sees (or a part of them) in blocks of P (64 at hd 64, 32 at
+// hd 128, so that two workgroups fit a CU's LDS): keys (rotated when new) and values go
 // through LDS, shared by the four waves; each wave owns 16 queries and keeps
 // their online softmax (running max and sum, weighted values) in registers,
 // scores and weighted values on f32 MFMA. The next block's loads are issued
 // before the current one is scored. The item's two row halves write their
 // partials (max score, sum of exponentials, weighted values) to the work-item
 // slots their record names: the layout the span merge reads, one span per part.
-template <int HD>
+template <int HD, int P>
 __global__ __launch_bounds__(256, 2) void k_attn_flash(AttnArgs a) {
-    constexpr int P = 64, HALF = HD / 2, QM = 32, NTD = HD / 16;
+    constexpr int HALF = HD / 2, QM = 32, NTD = HD / 16;
+    static_assert(P % 16 == 0 && 64 % P == 0, "blocks of whole 16-position MFMA tiles");
     __shared__ __align__(16) float ks[P][HD + 4];
     __shared__ __align__(16) float vs[P][HD + 4];
     __shared__ __align__(16) float qs[64][HD + 4];
@@ -1926,9 +1928,9 @@ __global__ __launch_bounds__(64) void k_merge_pieces(AttnArgs a, int m, void* __
 
 template <int HD, int P, int QM>
 static void attention_hd(hipStream_t st, const AttnArgs& a, int m, int ck, Pieces& out) {
-    if constexpr (HD == 64 && QM == 32) {
+    if constexpr ((HD == 64 || HD == 128) && QM == 32) {
         if (a.flash) {
-            hipLaunchKernelGGL(k_attn_flash<HD>, dim3(a.nkv, a.n_wi / 2), dim3(256), 0, st, a);
+            hipLaunchKernelGGL((k_attn_flash<HD, kFlashBlock(HD)>), dim3(a.nkv, a.n_wi / 2), dim3(256), 0, st, a);
             goto merge;
         }
     }

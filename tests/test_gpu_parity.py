@@ -409,19 +409,21 @@ def test_narrow_model_long_prefill_takes_the_gemm(ctx, kind):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("heads,kv_heads", [(32, 32), (27, 9)], ids=["mha", "gqa3"])
-def test_flash_prefill_attention_across_chunks_and_sequences(ctx, heads, kv_heads):
-    """Long hd-64 chunks run the flash attention items (64 rows of an MHA
-    model, 20 of a GQA-3 one, each walking the positions it sees in blocks of
-    64, split into parts of at most four blocks merged as spans). Two forwards:
+@pytest.mark.parametrize("heads,kv_heads,hd", [(32, 32, 64), (27, 9, 64), (32, 8, 128)],
+                         ids=["mha-hd64", "gqa3-hd64", "gqa4-hd128"])
+def test_flash_prefill_attention_across_chunks_and_sequences(ctx, heads, kv_heads, hd):
+    """Long chunks at hd 64 and 128 run the flash attention items (64 rows of
+    an MHA model, 20 of a GQA-3 one, 16 of a GQA-4 one, each walking the
+    positions it sees in blocks of 64 or 32, split into parts of at most 256
+    positions merged as spans). Two forwards:
     the first 520 tokens of one sequence; then its remaining 580 tokens (the
     items read the cached 520 positions) beside a fresh 300-token sequence.
     All logits, the hidden states and both sequences' cache slots against the
     oracle running the same chunks."""
     from ferrolm_amd.synth import random_model
     from ferrolm_amd.weights import Config
-    cfg = Config(vocab=512, hidden=heads * 64, intermediate=512, layers=2, heads=heads, kv_heads=kv_heads,
-                 head_dim=64, rms_eps=1e-5, rope_theta=10000.0, max_position=2048)
+    cfg = Config(vocab=512, hidden=heads * hd, intermediate=512, layers=2, heads=heads, kv_heads=kv_heads,
+                 head_dim=hd, rms_eps=1e-5, rope_theta=10000.0, max_position=2048)
     hm = random_model(cfg, seed=71, std=0.03)
     rng = np.random.default_rng(72)
     a = [int(x) for x in rng.integers(3, 500, 1100)]
