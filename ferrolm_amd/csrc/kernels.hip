@@ -942,6 +942,8 @@ __device__ void gemm_epilogue(const GemvArgs& a, float* yt, float* part, float* 
     constexpr int YS = 68;
     static_assert(MR * 4 <= NTHR, "four lanes per row");
     const int tid = threadIdx.x;
+    // the tile's place among the output's 64-column tiles (col0 is a multiple of 64)
+    const int tile = col0 / 64, ntiles = (a.N + 63) / 64;
     __syncthreads();
     // 1/rms of each row from the producers' sums of squares: four lanes per row
     if (NEED_R && tid < MR * 4) {
@@ -988,7 +990,7 @@ __device__ void gemm_epilogue(const GemvArgs& a, float* yt, float* part, float* 
                         bv = yr[cc];
                         bi = cc;
                     }
-                a.best[((size_t)blockIdx.x * 2 + j) * a.m + row] = make_float2(bv, __int_as_float(col0 + j * 32 + bi));
+                a.best[((size_t)tile * 2 + j) * a.m + row] = make_float2(bv, __int_as_float(col0 + j * 32 + bi));
             }
         }
         return;
@@ -1025,7 +1027,7 @@ __device__ void gemm_epilogue(const GemvArgs& a, float* yt, float* part, float* 
             ssq = fmaf(x, x, ssq);
         }
         ssq = group_reduce<4, false>(ssq);
-        if (q4 == 0 && rr < rows) a.ss_out[(size_t)blockIdx.x * a.ss_m + row] = ssq;
+        if (q4 == 0 && rr < rows) a.ss_out[(size_t)tile * a.ss_m + row] = ssq;
     }
     if (a.pa) {
         // slot (k-block, row tile, piece h, lane q8 * 16 + row % 16) holds 8 values
@@ -1034,7 +1036,7 @@ __device__ void gemm_epilogue(const GemvArgs& a, float* yt, float* part, float* 
         for (int idx = tid; idx < MR * Q8 * 2; idx += NTHR) {
             const int h = idx & 1, q8 = (idx >> 1) % Q8, rr = (idx >> 1) / Q8, row = row0 + rr;
             if (rr >= rows) continue;
-            const int kb = (EPI == EPI_RESID ? kb0 : (int)blockIdx.x) + q8 / 4;
+            const int kb = (EPI == EPI_RESID ? kb0 : tile) + q8 / 4;
             const float* vr = &vt[rr * YS + q8 * 8];
             u16x8 o;
 #pragma unroll
@@ -1042,8 +1044,8 @@ __device__ void gemm_epilogue(const GemvArgs& a, float* yt, float* part, float* 
             ((u16x8*)a.pa)[(((size_t)kb * prt + (row >> 4)) * 2 + h) * 64 + (q8 & 3) * 16 + (row & 15)] = o;
         }
         // the consumer's zero padding past the last k-block
-        if (blockIdx.x == gridDim.x - 1) {
-            const int covered = EPI == EPI_RESID ? (a.N + 31) / 32 : (int)gridDim.x;
+        if (tile == ntiles - 1) {
+            const int covered = EPI == EPI_RESID ? (a.N + 31) / 32 : ntiles;
             const u16x8 z = {0, 0, 0, 0, 0, 0, 0, 0};
             for (int idx = tid; idx < (a.pa_kb - covered) * MR * 8; idx += NTHR) {
                 const int kb = covered + idx / (MR * 8), rem = idx % (MR * 8), h = rem & 1, q8 = (rem >> 1) & 3,
@@ -1055,9 +1057,13 @@ __device__ void gemm_epilogue(const GemvArgs& a, float* yt, float* part, float* 
     }
 }
 
-template <int KIND, int EPI, int RTW>
+// CS 2 (steps of 256 rows or more): the eight waves form two sets of four, one
+// per 64-column half of a 128-column tile, each set splitting K in quarters, so
+// that a workgroup reads its activation rows once for twice the columns.
+template <int KIND, int EPI, int RTW, int CS = 1>
 __global__ __launch_bounds__(512) void k_gemm(const GemvArgs a) {
-    constexpr int NW = 8, NTHR = 64 * NW;
+    constexpr int NW = 8, NTHR = 64 * NW, NKW = NW / CS;
+    static_assert(CS == 1 || CS == 2, "one or two column sets");
     constexpr bool Q = KIND != BF16;
     constexpr bool WNT = Q || EPI == EPI_ARGMAX;  // weights read once per step: non-temporal
     constexpr bool NEED_R = EPI == EPI_QKV || EPI == EPI_SILU || EPI == EPI_ARGMAX;
@@ -1070,8 +1076,9 @@ __global__ __launch_bounds__(512) void k_gemm(const GemvArgs a) {
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: scalar registers, no divergence
     const int RT = (a.p_total + 3) >> 2;                         // row tiles of the activation buffer
-    const int rtb = blockIdx.y * RTW, tb = blockIdx.x * 4;
-    const int row0 = rtb * 16, col0 = tb * 16;
+    const int cs = CS == 1 ? 0 : wave / NKW, kw = wave % NKW;  // column set, K share
+    const int rtb = blockIdx.y * RTW, tb = blockIdx.x * 4 * CS + cs * 4;
+    const int row0 = rtb * 16, col0 = blockIdx.x * 64 * CS;
     const int rows = min(16 * RTW, a.m - row0);  // rows of this tile that exist (others are discarded)
     const int ntl = a.N >> 4, KB = a.KB, KC = KB >> 2;
     // row tiles / n-tiles past the end re-read the last one (their results are discarded)
@@ -1084,7 +1091,7 @@ __global__ __launch_bounds__(512) void k_gemm(const GemvArgs a) {
     // eighth of it per wave
     const int NP = KB >> 1, ks = gridDim.z;
     const int g0 = blockIdx.z * NP / ks, g1 = (blockIdx.z + 1) * NP / ks;
-    const int p0 = g0 + wave * (g1 - g0) / NW, p1 = g0 + (wave + 1) * (g1 - g0) / NW;
+    const int p0 = g0 + kw * (g1 - g0) / NKW, p1 = g0 + (kw + 1) * (g1 - g0) / NKW;
 
     f32x4 acc[RTW][4];
 #pragma unroll
@@ -1173,18 +1180,24 @@ __global__ __launch_bounds__(512) void k_gemm(const GemvArgs a) {
 #pragma unroll
             for (int t = 0; t < 4; t++) acc[i][t] += *(const f32x4*)&part[((slot * RTW * 4 + i * 4 + t) * 64 + lane) * 4];
     };
-    if (wave >= 4) put(wave - 4);
+    if constexpr (CS == 1) {
+        if (wave >= 4) put(wave - 4);
+        __syncthreads();
+        if (wave < 4) take(wave);
+        __syncthreads();
+    }
+    // (CS 2: each set's four partial tiles, in the same order, in slots 2 cs and 2 cs + 1)
+    if (kw == 2 || kw == 3) put(cs * 2 + kw - 2);
     __syncthreads();
-    if (wave < 4) take(wave);
+    if (kw < 2) take(cs * 2 + kw);
     __syncthreads();
-    if (wave == 2 || wave == 3) put(wave - 2);
+    if (kw == 1) put(cs * 2);
     __syncthreads();
-    if (wave < 2) take(wave);
-    __syncthreads();
-    if (wave == 1) put(0);
-    __syncthreads();
-    if (wave == 0) {
-        take(0);
+    if (kw == 0) take(cs * 2);
+    for (int c = 0; c < CS; c++) {
+    if (c > 0) __syncthreads();  // the previous column set's epilogue is done with yt
+    const int colc = col0 + c * 64;
+    if (wave == c * NKW) {
         if (ks > 1) {
             // split K: this workgroup's partial tile goes to kpart[z][row][col]; k_gemm_finish sums
             // the splits in order and runs the epilogue
@@ -1195,11 +1208,10 @@ __global__ __launch_bounds__(512) void k_gemm(const GemvArgs a) {
 #pragma unroll
                     for (int r = 0; r < 4; r++) {
                         const int rr = i * 16 + 4 * (lane >> 4) + r, cc = t * 16 + (lane & 15);
-                        if (rr < rows && col0 + cc < a.N)
-                            a.kpart[((size_t)blockIdx.z * a.m + row0 + rr) * a.N + col0 + cc] = acc[i][t][r];
+                        if (rr < rows && colc + cc < a.N)
+                            a.kpart[((size_t)blockIdx.z * a.m + row0 + rr) * a.N + colc + cc] = acc[i][t][r];
                     }
-            return;
-        }
+        } else {
         // D of a 16 x 16 tile has row 4 (l / 16) + r, column l % 16 in lane l
 #pragma unroll
         for (int i = 0; i < RTW; i++)
@@ -1207,9 +1219,10 @@ __global__ __launch_bounds__(512) void k_gemm(const GemvArgs a) {
             for (int t = 0; t < 4; t++)
 #pragma unroll
                 for (int r = 0; r < 4; r++) yt[(i * 16 + 4 * (lane >> 4) + r) * YS + t * 16 + (lane & 15)] = acc[i][t][r];
+        }
     }
-    if (ks > 1) return;
-    gemm_epilogue<EPI, NTHR, 16 * RTW>(a, yt, part, rs, row0, rows, col0);
+    if (ks == 1 && colc < a.N) gemm_epilogue<EPI, NTHR, 16 * RTW>(a, yt, part, rs, row0, rows, colc);
+    }
 }
 
 // The split-K sum (splits in order, so the result does not depend on which
@@ -1253,14 +1266,14 @@ __global__ __launch_bounds__(256) void k_gemm_finish(const GemvArgs a) {
     gemm_epilogue<EPI, 256, 16 * RTW>(a, yt, vt, rs, row0, rows, col0);
 }
 
-template <int KIND, int RTW>
+template <int KIND, int RTW, int CS>
 static void gemm_rtw(hipStream_t st, int epi, const DMat& w, const GemvArgs& a0, int groups, hipEvent_t e0,
                      hipEvent_t e1) {
     // Split K across workgroups when the tiles alone leave most CUs idle: up
     // to 256 workgroups, at least one k-block pair per wave and split, and the
     // partial tiles within the workspace's kpart buffer.
     GemvArgs a = a0;
-    const int cg = (w.n_tiles + 3) / 4, np = w.kb / 2;
+    const int cg = (w.n_tiles + 4 * CS - 1) / (4 * CS), cg64 = (w.n_tiles + 3) / 4, np = w.kb / 2;
     int ks = 1;
     if (a.kpart)
         while (ks < 8 && cg * groups * ks * 2 <= 256 && np / (ks * 2) >= 8 &&
@@ -1274,32 +1287,35 @@ static void gemm_rtw(hipStream_t st, int epi, const DMat& w, const GemvArgs& a0,
             launch_timed(kern, grid, dim3(512), st, a, e0, e1);
         } else {
             launch_timed(kern, grid, dim3(512), st, a, e0, nullptr);
-            launch_timed(fin, dim3(cg, (a.m + 15) / 16), dim3(256), st, a, nullptr, e1);
+            launch_timed(fin, dim3(cg64, (a.m + 15) / 16), dim3(256), st, a, nullptr, e1);
         }
     };
     switch (epi) {
-        case EPI_STORE: run(k_gemm<KIND, EPI_STORE, RTW>, k_gemm_finish<EPI_STORE, 1>); break;
-        case EPI_QKV: run(k_gemm<KIND, EPI_QKV, RTW>, k_gemm_finish<EPI_QKV, 1>); break;
-        case EPI_RESID: run(k_gemm<KIND, EPI_RESID, RTW>, k_gemm_finish<EPI_RESID, 1>); break;
-        case EPI_SILU: run(k_gemm<KIND, EPI_SILU, RTW>, k_gemm_finish<EPI_SILU, 1>); break;
-        case EPI_ARGMAX: run(k_gemm<KIND, EPI_ARGMAX, RTW>, k_gemm_finish<EPI_ARGMAX, 1>); break;
+        case EPI_STORE: run(k_gemm<KIND, EPI_STORE, RTW, CS>, k_gemm_finish<EPI_STORE, 1>); break;
+        case EPI_QKV: run(k_gemm<KIND, EPI_QKV, RTW, CS>, k_gemm_finish<EPI_QKV, 1>); break;
+        case EPI_RESID: run(k_gemm<KIND, EPI_RESID, RTW, CS>, k_gemm_finish<EPI_RESID, 1>); break;
+        case EPI_SILU: run(k_gemm<KIND, EPI_SILU, RTW, CS>, k_gemm_finish<EPI_SILU, 1>); break;
+        case EPI_ARGMAX: run(k_gemm<KIND, EPI_ARGMAX, RTW, CS>, k_gemm_finish<EPI_ARGMAX, 1>); break;
     }
 }
 
-// Row tiles per workgroup: as few groups of at most five as cover the rows
-// (each group reads every weight tile once), each as small as that allows
-// (rows past m cost loads and MFMAs).
 template <int KIND>
 static void gemm_kind(hipStream_t st, int epi, const DMat& w, const GemvArgs& a, hipEvent_t e0, hipEvent_t e1) {
     const int rt = (a.p_total + 3) / 4, groups = (rt + 4) / 5, rtw = (rt + groups - 1) / groups;
-    if (rtw <= 2)
-        gemm_rtw<KIND, 2>(st, epi, w, a, (rt + 1) / 2, e0, e1);
+    // 128-column tiles (CS 2) for steps of 256 rows or more when they still make
+    // 512 workgroups (measured on the 1.7B int4 prefill of 1024 tokens: 14.45
+    // against 15.3 ms; with fewer workgroups, the 135M draft's prefill and the
+    // 160-row verify steps ran slower: 4.54 against 4.0 ms, 7.42 against 6.80 ms)
+    if (rt >= 16 && (w.n_tiles + 7) / 8 * groups >= 512)
+        gemm_rtw<KIND, 5, 2>(st, epi, w, a, groups, e0, e1);
+    else if (rtw <= 2)
+        gemm_rtw<KIND, 2, 1>(st, epi, w, a, (rt + 1) / 2, e0, e1);
     else if (rtw == 3)
-        gemm_rtw<KIND, 3>(st, epi, w, a, (rt + 2) / 3, e0, e1);
+        gemm_rtw<KIND, 3, 1>(st, epi, w, a, (rt + 2) / 3, e0, e1);
     else if (rtw == 4)
-        gemm_rtw<KIND, 4>(st, epi, w, a, (rt + 3) / 4, e0, e1);
+        gemm_rtw<KIND, 4, 1>(st, epi, w, a, (rt + 3) / 4, e0, e1);
     else
-        gemm_rtw<KIND, 5>(st, epi, w, a, groups, e0, e1);
+        gemm_rtw<KIND, 5, 1>(st, epi, w, a, groups, e0, e1);
 }
 
 template <int KIND, int NT, int EPI>
