@@ -44,3 +44,15 @@ def test_product_code_never_imports_the_oracle():
         if p.suffix in (".py", ".hip", ".cpp", ".h"):
             t = p.read_text()
             assert "import oracle" not in t and "from oracle" not in t and "ferro_oracle" not in t, p
+
+
+def test_bench_refuses_more_than_one_gpu():
+    """bench.py measures one GPU: --gpus above 1 exits with status 2 and says
+    why, before touching the device."""
+    import subprocess
+    import sys
+    root = Path(__file__).resolve().parents[1]
+    r = subprocess.run([sys.executable, str(root / "bench.py"), "--gpus", "2"], cwd=root, capture_output=True,
+                       text=True, timeout=120)
+    assert r.returncode == 2
+    assert "one GPU" in r.stderr and not r.stdout.strip()
