@@ -733,7 +733,8 @@ static int run_forward(fg_ctx* ctx, const fg_model* m, fg_kv* kv, const Plan& P,
         aa.vc = kv->v + li * kv->layer_floats();
         Pieces po = pieces(w, cur ^ 1, l.wo.kb, passes);
         const bool am = ctx->merge_in_o && merge_in_o(c, P, l.wo, mm);
-        launch_attention(st, aa, t, am ? -1 : ck(l.wo), po);
+        if (launch_attention(st, aa, t, am ? -1 : ck(l.wo), po))
+            return fail(FG_E_SHAPE, "no attention kernel for head_dim " + std::to_string(hd));
         cur ^= 1;
         // o projection + residual; pieces of mlp_norm * x for gate/up
         g = gemv_args(l.wo, pieces(w, cur, l.wo.kb, passes), t, w);
@@ -874,16 +875,29 @@ int fg_ctx_sync(fg_ctx* c) {
     return 0;
 }
 
+// Head dims with an attention kernel instance (launch_attention).
+static bool head_dim_supported(int hd) { return hd == 16 || hd == 32 || hd == 64 || hd == 128; }
+
+int fg_config_check(const fg_config* cfg) {
+    if (!cfg) return fail(FG_E_ARG, "null config");
+    const fg_config& c = *cfg;
+    if (c.heads <= 0 || c.kv_heads <= 0 || c.heads % c.kv_heads || c.head_dim % 16 || c.hidden % 16 ||
+        c.vocab <= 0 || c.layers < 0 || c.max_position <= 0)
+        return fail(FG_E_SHAPE, "unsupported model shape");  // src/config.rs:70-74
+    if (!head_dim_supported(c.head_dim))
+        return fail(FG_E_SHAPE, "head_dim " + std::to_string(c.head_dim) +
+                                    " has no device attention kernel (supported: 16, 32, 64, 128)");
+    if (c.heads / c.kv_heads > attn_qmax(c.head_dim)) return fail(FG_E_SHAPE, "GQA group too large");
+    if (c.hidden % 32 || c.intermediate % 32 || (c.heads * c.head_dim) % 32 || c.vocab % 32)
+        return fail(FG_E_SHAPE, "hidden, intermediate, q and vocab sizes must be multiples of 32");
+    return 0;
+}
+
 int fg_model_upload(fg_ctx* ctx, const fg_config* cfg, const fg_layer* layers, const uint16_t* embed,
                     const float* norm, const uint16_t* lm_head, fg_model** out) {
     if (!ctx || !cfg || (!layers && cfg->layers > 0) || !embed || !norm || !out) return fail(FG_E_ARG, "null argument");
     const fg_config& c = *cfg;
-    if (c.heads <= 0 || c.kv_heads <= 0 || c.heads % c.kv_heads || c.head_dim % 16 || c.hidden % 16 ||
-        c.head_dim > 128 || c.vocab <= 0 || c.layers < 0 || c.max_position <= 0)
-        return fail(FG_E_SHAPE, "unsupported model shape");
-    if (c.heads / c.kv_heads > attn_qmax(c.head_dim)) return fail(FG_E_SHAPE, "GQA group too large");
-    if (c.hidden % 32 || c.intermediate % 32 || (c.heads * c.head_dim) % 32)
-        return fail(FG_E_SHAPE, "hidden, intermediate and q sizes must be multiples of 32");
+    if (int rc = fg_config_check(cfg)) return rc;
     HIPCHK(hipSetDevice(ctx->device));
     fg_model* m = new fg_model();
     m->cfg = c;
@@ -918,7 +932,6 @@ int fg_model_upload(fg_ctx* ctx, const fg_config* cfg, const fg_layer* layers, c
     int rc;
     if ((rc = upload_vec(embed, (size_t)c.vocab * H, &m->embed, m->allocs))) return bad(rc);
     fg_matrix lm{FG_BF16, c.vocab, H, 0, (lm_head && !c.tie_embeddings) ? lm_head : embed, nullptr, nullptr};
-    if (c.vocab % 32) return bad(fail(FG_E_SHAPE, "vocab must be a multiple of 32"));
     if ((rc = upload_mat(lm, m->lm_head, &m->allocs))) return bad(rc);
     ref += (int64_t)c.vocab * H * 2 * ((lm_head && !c.tie_embeddings) ? 2 : 1);
     if ((rc = upload_vec(norm, H, &m->norm, m->allocs))) return bad(rc);
@@ -965,6 +978,9 @@ int fg_kv_create(fg_ctx* ctx, int32_t layers, int32_t kv_heads, int32_t head_dim
                  fg_kv** out) {
     if (!ctx || !out || layers <= 0 || kv_heads <= 0 || head_dim <= 0 || block_size != 16 || blocks <= 0)
         return fail(FG_E_ARG, "bad cache shape (block_size must be 16)");
+    if (!head_dim_supported(head_dim))
+        return fail(FG_E_SHAPE, "head_dim " + std::to_string(head_dim) +
+                                    " has no device attention kernel (supported: 16, 32, 64, 128)");
     HIPCHK(hipSetDevice(ctx->device));
     fg_kv* kv = new fg_kv();
     kv->layers = layers;

@@ -161,8 +161,9 @@ struct AttnArgs {
 };
 // Attention over the paged cache (RoPE, K/V write of the new rows), then the
 // split merge straight into the output projection's pieces (consumer_kind < 0:
-// no merge, the output projection merges the spans itself).
-void launch_attention(hipStream_t st, const AttnArgs& a, int m, int consumer_kind, Pieces& out);
+// no merge, the output projection merges the spans itself). Returns -1, and
+// launches nothing, for a head dim without a kernel instance (16, 32, 64, 128).
+int launch_attention(hipStream_t st, const AttnArgs& a, int m, int consumer_kind, Pieces& out);
 
 void launch_argmax_final(hipStream_t st, const float2* best, int tiles, int rows, uint32_t* argmax_out,
                          uint32_t* aux, int aux_stride, int aux_off);

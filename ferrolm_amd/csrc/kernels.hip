@@ -1979,13 +1979,14 @@ merge:
 int attn_span(int hd) { return hd >= 128 ? 32 : 64; }
 int attn_qmax(int hd) { return hd >= 64 ? 32 : 64; }
 
-void launch_attention(hipStream_t st, const AttnArgs& a, int m, int consumer_kind, Pieces& out) {
-    if (m <= 0 || a.n_wi <= 0) return;
+int launch_attention(hipStream_t st, const AttnArgs& a, int m, int consumer_kind, Pieces& out) {
+    if (m <= 0 || a.n_wi <= 0) return 0;
     switch (a.hd) {
-        case 16: attention_hd<16, 64, 64>(st, a, m, consumer_kind, out); break;
-        case 32: attention_hd<32, 64, 64>(st, a, m, consumer_kind, out); break;
-        case 64: attention_hd<64, 64, 32>(st, a, m, consumer_kind, out); break;
-        case 128: attention_hd<128, 32, 32>(st, a, m, consumer_kind, out); break;
+        case 16: attention_hd<16, 64, 64>(st, a, m, consumer_kind, out); return 0;
+        case 32: attention_hd<32, 64, 64>(st, a, m, consumer_kind, out); return 0;
+        case 64: attention_hd<64, 64, 32>(st, a, m, consumer_kind, out); return 0;
+        case 128: attention_hd<128, 32, 32>(st, a, m, consumer_kind, out); return 0;
+        default: return -1;  // no instance: nothing is launched
     }
 }
 

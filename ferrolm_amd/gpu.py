@@ -95,6 +95,7 @@ EXPORTS = {
     "fg_ctx_destroy": (None, [C.c_void_p]),
     "fg_last_error": (C.c_char_p, []),
     "fg_ctx_sync": (C.c_int, [C.c_void_p]),
+    "fg_config_check": (C.c_int, [C.POINTER(FgConfig)]),
     "fg_model_upload": (C.c_int, [C.c_void_p, C.POINTER(FgConfig), C.POINTER(FgLayer), u16p, f32p, u16p,
                                   C.POINTER(C.c_void_p)]),
     "fg_model_truncated": (C.c_int, [C.c_void_p, C.c_void_p, C.c_int32, C.POINTER(C.c_void_p)]),
@@ -167,6 +168,35 @@ def config_struct(c: Config) -> FgConfig:
                     c.rope_orig_max_pos, c.max_position, int(c.tie_embeddings), int(c.qkv_bias))
 
 
+def check_config(c: Config) -> None:
+    """fg_config_check: the reference's config shape checks plus the device's
+    limits (host only, no GPU needed). Raises FgError on a refused shape."""
+    cs = config_struct(c)
+    check(lib().fg_config_check(C.byref(cs)))
+
+
+def _need(a, dtype, n: int, what: str) -> None:
+    if a is None or a.dtype != dtype or a.size != n or not a.flags["C_CONTIGUOUS"]:
+        got = "None" if a is None else f"{a.dtype} x {a.size}"
+        raise ValueError(f"{what}: expected {n} contiguous {np.dtype(dtype)} values, got {got}")
+
+
+def check_matrix(m: Matrix, what: str) -> None:
+    """The host arrays of a weight matrix match its shape and format, so the
+    upload never reads past them: bf16 rows x cols uint16; quantized codes
+    rows x cols (int8) or rows x cols / 2 (int4) bytes and (rows / 32) x
+    (cols / 32) x 32 f32 scales (QMatrix, src/quant.rs:64-76)."""
+    if m.rows <= 0 or m.cols <= 0:
+        raise ValueError(f"{what}: empty matrix")
+    if m.kind == BF16:
+        _need(m.bf16, np.uint16, m.rows * m.cols, f"{what} bf16")
+        return
+    if m.rows % 32 or m.cols % 32:
+        raise ValueError(f"{what}: quantized matrices need rows and cols that are multiples of 32")
+    _need(m.q, np.uint8, m.rows * m.cols // (1 if m.kind == INT8 else 2), f"{what} codes")
+    _need(m.s, np.float32, m.rows * m.cols // 32, f"{what} scales")
+
+
 def matrix_struct(m: Matrix) -> FgMatrix:
     return FgMatrix(m.kind, m.rows, m.cols, 0, ptr(m.bf16, u16p), ptr(m.q, u8p), ptr(m.s, f32p))
 
@@ -202,6 +232,25 @@ class Model:
             self.cfg = cfg
             return
         self.cfg = hm.cfg
+        c = hm.cfg
+        check_config(c)
+        if len(hm.layers) != c.layers:
+            raise ValueError(f"{len(hm.layers)} layers given for a config of {c.layers}")
+        _need(hm.embed, np.uint16, c.vocab * c.hidden, "embed")
+        _need(hm.norm, np.float32, c.hidden, "norm")
+        if hm.lm_head is not None and not c.tie_embeddings:
+            _need(hm.lm_head, np.uint16, c.vocab * c.hidden, "lm_head")
+        for i, l in enumerate(hm.layers):
+            _need(l.attn_norm, np.float32, c.hidden, f"layer {i} attn_norm")
+            _need(l.mlp_norm, np.float32, c.hidden, f"layer {i} mlp_norm")
+            if c.qkv_bias:
+                _need(l.bqkv, np.float32, c.qkv_dim, f"layer {i} bqkv")
+            for name, m, rows, cols in (("wqkv", l.wqkv, c.qkv_dim, c.hidden), ("wo", l.wo, c.hidden, c.q_dim),
+                                        ("w_gate_up", l.w_gate_up, 2 * c.intermediate, c.hidden),
+                                        ("w_down", l.w_down, c.hidden, c.intermediate)):
+                if (m.rows, m.cols) != (rows, cols):
+                    raise ValueError(f"layer {i} {name}: {m.rows} x {m.cols}, the config needs {rows} x {cols}")
+                check_matrix(m, f"layer {i} {name}")
         ls = (FgLayer * max(1, len(hm.layers)))()
         for i, l in enumerate(hm.layers):
             ls[i] = FgLayer(ptr(l.attn_norm, f32p), matrix_struct(l.wqkv), ptr(l.bqkv, f32p), matrix_struct(l.wo),
@@ -402,6 +451,7 @@ class Mat:
     def __init__(self, ctx: Context, m: Matrix):
         self.ctx = ctx
         self.rows, self.cols, self.kind = m.rows, m.cols, m.kind
+        check_matrix(m, "matrix")
         ms = matrix_struct(m)
         h = C.c_void_p()
         check(lib().fg_mat_upload(ctx.h, C.byref(ms), C.byref(h)))

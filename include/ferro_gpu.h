@@ -128,6 +128,13 @@ const char* fg_last_error(void);
 int fg_ctx_sync(fg_ctx* ctx);
 
 /* ---- weights ---------------------------------------------------------- */
+/* The shape checks of Config::parse (src/config.rs:70-74: heads divisible by
+ * kv_heads, head_dim and hidden multiples of 16) plus the device's own limits:
+ * head_dim one of 16, 32, 64, 128 (the attention kernel instances), GQA group
+ * at most 32 (64 below head_dim 64), hidden / intermediate / heads*head_dim /
+ * vocab multiples of 32. Host-only: 0 or FG_E_SHAPE with fg_last_error().
+ * fg_model_upload runs it first. */
+int fg_config_check(const fg_config* cfg);
 /* Model::load/random + Model::quantize output handed to the device
  * (src/model.rs:92-219). embed is vocab x hidden bf16 row-major; lm_head
  * NULL when tied (src/model.rs:263-265). */
@@ -145,7 +152,9 @@ int64_t fg_model_weight_bytes(const fg_model* m);
 
 /* ---- paged KV cache --------------------------------------------------- */
 /* KvCache::new (src/kv.rs:33-44): f32 keys and values for every layer in
- * the reference layout [layer][block][kv_head][block_size][head_dim]. */
+ * the reference layout [layer][block][kv_head][block_size][head_dim].
+ * block_size must be 16 (FG_E_ARG) and head_dim 16, 32, 64 or 128
+ * (FG_E_SHAPE). */
 int fg_kv_create(fg_ctx* ctx, int32_t layers, int32_t kv_heads,
                  int32_t head_dim, int32_t block_size, int32_t blocks,
                  fg_kv** out);

@@ -102,3 +102,35 @@ def chi_square(counts: dict, exact, n: int) -> float:
     """Pearson's statistic of observed continuation counts against exact."""
     assert set(counts) <= {s for s, _ in exact}, "impossible continuation sampled"
     return sum((counts.get(s, 0) - p * n) ** 2 / (p * n) for s, p in exact)
+
+
+# Near-tie rule for greedy tokens. The device's logits agree with the oracle's
+# to LOGIT_TOL x the row's largest |logit| (the fixture and config tests hold
+# them to that), so the device may pick a different token only where the
+# oracle's top two are within twice that of each other. Such a row is a
+# documented near-tie; any other difference fails.
+LOGIT_TOL = 1e-4
+NEAR_TIE = 2 * LOGIT_TOL
+
+
+def assert_argmax_parity(dev_argmax, ref_logits, tol: float = NEAR_TIE, max_ties: int | None = None) -> int:
+    """Per-row greedy token of the device against sampler::argmax of the
+    reference logits (first index of the maximum, src/sampler.rs:42-51).
+    A row may differ only at a near-tie: the reference logit of the device's
+    token is within tol x max|logit| of the row's maximum. Returns the number
+    of excused rows (at most max_ties, default 1% of the rows + 1)."""
+    import numpy as np
+    dev = np.asarray(dev_argmax).astype(np.int64).ravel()
+    ref = np.asarray(ref_logits, np.float32).reshape(len(dev), -1)
+    want = ref.argmax(axis=1)
+    ties = 0
+    for r in np.nonzero(dev != want)[0]:
+        gap = float(ref[r, want[r]]) - float(ref[r, dev[r]])
+        scale = float(np.abs(ref[r]).max())
+        assert 0.0 <= gap <= tol * scale, (
+            f"row {r}: device token {dev[r]} vs {want[r]}, logit gap {gap:.3e} above the near-tie bar "
+            f"{tol * scale:.3e}")
+        ties += 1
+    limit = max_ties if max_ties is not None else len(dev) // 100 + 1
+    assert ties <= limit, f"{ties} near-tie rows of {len(dev)}"
+    return ties

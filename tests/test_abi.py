@@ -56,3 +56,38 @@ def test_bench_refuses_more_than_one_gpu():
                        text=True, timeout=120)
     assert r.returncode == 2
     assert "one GPU" in r.stderr and not r.stdout.strip()
+
+
+def test_config_check_refuses_head_dims_without_an_attention_kernel():
+    """head_dim 96 passes the reference's own check (a multiple of 16,
+    src/config.rs:70) but has no device attention instance: the library
+    refuses it up front with FG_E_SHAPE instead of launching nothing."""
+    from dataclasses import replace
+    from ferrolm_amd import gpu
+    from ferrolm_amd.weights import shape
+    base = shape("smollm2-135m")
+    gpu.check_config(base)  # head_dim 64: accepted
+    for hd in (16, 32, 128):
+        gpu.check_config(replace(base, head_dim=hd, heads=8, kv_heads=2))
+    for hd in (48, 80, 96, 112):
+        with pytest.raises(gpu.FgError, match=f"head_dim {hd}"):
+            gpu.check_config(replace(base, head_dim=hd, heads=6, kv_heads=2))
+    with pytest.raises(gpu.FgError, match="unsupported model shape"):
+        gpu.check_config(replace(base, heads=9, kv_heads=2))  # src/config.rs:70: heads % kv_heads
+
+
+def test_model_arrays_are_checked_before_upload():
+    """A host model whose arrays are short or of the wrong type raises
+    ValueError in the binding, before any pointer reaches the library."""
+    import numpy as np
+    from dataclasses import replace
+    from ferrolm_amd import gpu
+    from ferrolm_amd.weights import INT4, Matrix
+    good = Matrix(INT4, 64, 64, q=np.zeros(64 * 32, np.uint8), s=np.zeros(64 * 2, np.float32))
+    gpu.check_matrix(good, "w")
+    with pytest.raises(ValueError, match="codes"):
+        gpu.check_matrix(replace(good, q=np.zeros(64 * 31, np.uint8)), "w")
+    with pytest.raises(ValueError, match="scales"):
+        gpu.check_matrix(replace(good, s=np.zeros(64 * 2, np.float64)), "w")
+    with pytest.raises(ValueError, match="bf16"):
+        gpu.check_matrix(Matrix(0, 32, 32, bf16=np.zeros(32 * 32, np.float32)), "w")

@@ -18,7 +18,7 @@ from ferrolm_amd import gpu
 from ferrolm_amd.spec import Batch, generate
 from ferrolm_amd.weights import BF16, INT4, INT8, Matrix, bf16_to_f32, f32_to_bf16, load_model
 
-from conftest import FIXTURES, GOLDEN
+from conftest import FIXTURES, GOLDEN, assert_argmax_parity
 
 pytestmark = pytest.mark.gpu
 
@@ -89,8 +89,8 @@ def test_fixture_forward_matches_transformers_and_oracle(ctx, name):
     ol, oh = om.forward(okv, [(prompt, 0, table, 2)], hidden=True)
     assert np.abs(out.logits - ol).max() < 1e-4 * np.abs(ol).max()
     rel = np.linalg.norm(out.hidden - oh, axis=-1) / np.linalg.norm(oh, axis=-1)
-    assert rel.max() < 2e-2 and rel.max() < 1e-4, rel.max()
-    assert np.array_equal(out.argmax, ol.argmax(axis=1)) or True  # ties handled below
+    assert rel.max() < 1e-4, rel.max()  # the north star's bar is 2e-2
+    assert_argmax_parity(out.argmax, ol)  # every row's greedy token, near-ties excused
     # KV slots: every written position holds the oracle's keys/values
     for li in range(hm.cfg.layers):
         gk, gv = kv.layer(li)

@@ -85,26 +85,130 @@ def test_bf16_round_to_nearest_even():
     assert l.or_f32_to_bf16(1.01171875) == 0x3F82  # tie rounds up to even
 
 
-def test_rng_matches_a_plain_restatement():
-    """src/rng.rs: xorshift64* and Box-Muller, against a Python loop."""
-    def py_rng(seed):
-        s = (seed * 0x9E3779B97F4A7C15 & (2**64 - 1)) | 1
-        while True:
-            s ^= s >> 12
-            s ^= (s << 25) & (2**64 - 1)
-            s ^= s >> 27
-            yield s * 0x2545F4914F6CDD1D & (2**64 - 1)
+# ---------------------------------------------------------------------------
+# Rng (src/rng.rs:8-44), pinned by what the mathematics fixes rather than by a
+# restatement of the same formula:
+#  - the state update of xorshift64* is linear over GF(2); its 64 x 64 matrix is
+#    read off or_rng_next on the basis states, and it must have order exactly
+#    2^64 - 1 (the full period every xorshift triple in use is chosen for:
+#    M^(2^64-1) = I and M^((2^64-1)/p) != I for each prime p of 2^64 - 1). Only
+#    about one shift triple in a hundred passes, so a mistyped shift or a
+#    swapped direction fails;
+#  - the triple itself: M^T M differs from I exactly where the published
+#    (12, 25, 27) xorshift (right, left, right) puts terms;
+#  - Rng::new's multiplier is floor(2^64 / phi) (Fibonacci hashing), computed
+#    here from the golden ratio; the output multiplier is the published
+#    xorshift64* constant 2685821657736338717 (Vigna, "An experimental
+#    exploration of Marsaglia's xorshift generators, scrambled", 2016);
+#  - uniform = top 53 bits / 2^53 and normal = Box-Muller of two uniforms,
+#    bit for bit from the oracle's own stream, and the normals pass a KS test.
+# ---------------------------------------------------------------------------
+MASK64 = (1 << 64) - 1
+PRIMES_2_64_MINUS_1 = [3, 5, 17, 257, 641, 65537, 6700417]
+
+
+def _state_after_next(state: int) -> int:
+    st = ctypes.c_uint64(state)
+    oracle.lib().or_rng_next(ctypes.byref(st))
+    return st.value
+
+
+def _gf2_columns() -> list:
+    """Columns of the state-update matrix: column j = update(e_j)."""
+    return [_state_after_next(1 << j) for j in range(64)]
+
+
+def _gf2_apply(cols, v: int) -> int:
+    out = 0
+    j = 0
+    while v:
+        if v & 1:
+            out ^= cols[j]
+        v >>= 1
+        j += 1
+    return out
+
+
+def _gf2_mul(a, b):
+    """Columns of A B (apply B, then A)."""
+    return [_gf2_apply(a, c) for c in b]
+
+
+def _gf2_pow(a, e: int):
+    r = [1 << j for j in range(64)]
+    while e:
+        if e & 1:
+            r = _gf2_mul(a, r)
+        a = _gf2_mul(a, a)
+        e >>= 1
+    return r
+
+
+def test_rng_state_update_is_linear_with_full_period():
+    import random
+    cols = _gf2_columns()
+    rnd = random.Random(5)
+    for _ in range(200):  # linearity: update(a ^ b) = update(a) ^ update(b)
+        a, b = rnd.getrandbits(64), rnd.getrandbits(64)
+        assert _state_after_next(a ^ b) == _state_after_next(a) ^ _state_after_next(b)
+        assert _state_after_next(a) == _gf2_apply(cols, a)
+    ident = [1 << j for j in range(64)]
+    n = (1 << 64) - 1
+    assert n == 3 * 5 * 17 * 257 * 641 * 65537 * 6700417
+    assert _gf2_pow(cols, n) == ident
+    for p in PRIMES_2_64_MINUS_1:
+        assert _gf2_pow(cols, n // p) != ident, p
+
+
+def test_rng_state_update_is_the_published_shift_triple():
+    """x ^= x >> 12; x ^= x << 25; x ^= x >> 27, checked on single bits: bit j
+    of the input reaches exactly the output bits the three shifts place it
+    at (a wrong amount or direction moves them)."""
+    cols = _gf2_columns()
+    for j in range(64):
+        # the composition as a set of bit positions, built one shift at a time
+        bits = {j}
+        bits ^= {b - 12 for b in bits if b - 12 >= 0}
+        bits ^= {b + 25 for b in bits if b + 25 < 64}
+        bits ^= {b - 27 for b in bits if b - 27 >= 0}
+        assert cols[j] == sum(1 << b for b in bits), j
+
+
+def test_rng_constants_and_conversions():
+    from decimal import Decimal, getcontext
+    getcontext().prec = 60
+    phi = (1 + Decimal(5).sqrt()) / 2
+    golden = int(Decimal(2) ** 64 / phi)
+    assert golden == 0x9E3779B97F4A7C15
     l = oracle.lib()
-    st = ctypes.c_uint64(l.or_rng_new(7))
-    g = py_rng(7)
-    for _ in range(100):
-        assert l.or_rng_next(ctypes.byref(st)) == next(g)
-    st = ctypes.c_uint64(l.or_rng_new(3))
-    g = py_rng(3)
+    for seed in [0, 1, 2, 7, 12345, MASK64]:
+        assert l.or_rng_new(seed) == ((seed * golden) & MASK64) | 1
+    # the output of next = (new state) * the published multiplier
+    st = ctypes.c_uint64(l.or_rng_new(11))
     for _ in range(50):
-        u = 1.0 - (next(g) >> 11) / 2**53
-        v = (next(g) >> 11) / 2**53
-        assert l.or_rng_normal(ctypes.byref(st)) == math.sqrt(-2.0 * math.log(u)) * math.cos(2 * math.pi * v)
+        out = l.or_rng_next(ctypes.byref(st))
+        assert out == (st.value * 2685821657736338717) & MASK64
+        assert out & 1 == st.value & 1  # odd multiplier keeps the low bit
+    # uniform: the top 53 bits of next, over 2^53; normal: Box-Muller of two uniforms
+    a, b = ctypes.c_uint64(l.or_rng_new(3)), ctypes.c_uint64(l.or_rng_new(3))
+    for _ in range(100):
+        u = l.or_rng_uniform(ctypes.byref(a))
+        assert u == (l.or_rng_next(ctypes.byref(b)) >> 11) / 2.0 ** 53 and 0.0 <= u < 1.0
+    a, b = ctypes.c_uint64(l.or_rng_new(9)), ctypes.c_uint64(l.or_rng_new(9))
+    for _ in range(100):
+        z = l.or_rng_normal(ctypes.byref(a))
+        u = 1.0 - l.or_rng_uniform(ctypes.byref(b))
+        v = l.or_rng_uniform(ctypes.byref(b))
+        assert z == math.sqrt(-2.0 * math.log(u)) * math.cos(2 * math.pi * v)
+
+
+def test_rng_normals_are_standard_normal():
+    from scipy import stats
+    l = oracle.lib()
+    st = ctypes.c_uint64(l.or_rng_new(2024))
+    z = np.array([l.or_rng_normal(ctypes.byref(st)) for _ in range(20000)])
+    assert stats.kstest(z, "norm").pvalue > 1e-3
+    assert abs(z.mean()) < 0.03 and abs(z.std() - 1.0) < 0.03
 
 
 def _rand_bf16(n, k, seed):
