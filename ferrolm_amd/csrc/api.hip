@@ -5,6 +5,7 @@
 #include "ferro_gpu.h"
 #include "ferro_host.h"
 #include "internal.h"
+#include "pdraft.h"
 
 #include <algorithm>
 #include <atomic>
@@ -87,6 +88,23 @@ struct fg_ctx {
     hipEvent_t ev[3] = {nullptr, nullptr, nullptr};
     float last_us[3] = {0, 0, 0};
     bool merge_in_o = true;  // small bf16 output projections merge the attention spans themselves
+    // split-K GEMV meeting counters (GemvArgs::gcnt): zeroed once here, left at
+    // zero by every launch's last workgroups
+    unsigned* gcnt = nullptr;
+    // the persistent draft forward (pdraft.hip, FERRO_PDRAFT=1): its tagged exchange words and
+    // control words (epoch, finished workgroups, abort), and a pinned word the
+    // abort flag is read back into after a step
+    bool pdraft = true;
+    uint64_t* pd_ll = nullptr;
+    size_t pd_ll_cap = 0;  // words
+    unsigned* pd_ctl = nullptr;
+    unsigned* pd_abort = nullptr;
+    // launches since the words were last cleared: a tag holds 24 bits of the
+    // launch epoch, so the words are cleared and the epoch restarted well
+    // before it wraps
+    uint64_t pd_launches = 0;
+    int pd_groups = 0;  // workgroups of a launch (all resident at once)
+    int pd_spin = kPdSpin;  // polls a wait may take (FERRO_PDRAFT_SPIN: the time-out path's test)
     // GEMV launch profiling (fg_profile)
     bool prof = false;
     std::vector<hipEvent_t> pev;
@@ -182,6 +200,8 @@ static std::atomic<uint64_t> g_serial{1};
 
 struct fg_model {
     uint64_t serial = g_serial++;
+    // device layer records of the persistent draft forward (made on first use)
+    PdLayer* pd_layers = nullptr;
     fg_config cfg{};
     std::vector<DLayer> layers;
     uint16_t* embed = nullptr;
@@ -568,6 +588,7 @@ struct Work {
     float *x, *ss, *qkv, *apart, *logits;
     float* kpart;  // GEMM split-K partial tiles (steps of more than kGemvRows rows)
     size_t kpart_cap;
+    float* gpart;  // GEMV split-K partial tiles (decode steps of one pass)
     void* pa[2];   // activation pieces, ping-pong: each kernel reads one and writes the other
     float* pxs[2];
     float2* best;
@@ -589,6 +610,7 @@ static int kind_of(const DMat& m) { return m.kind; }
 // rounds of 16 sequences, 7.15 against 6.85 ms per step), so 16-row steps
 // take the GEMM.
 static constexpr int kGemvRows = 15;
+static constexpr int kGemvSplitGroups = 1024;  // output groups a split-K GEMV may have (counters per context)
 static constexpr int kGemmMinHidden = 1024;
 static constexpr int kNarrowGemmRows = 256;
 static bool step_gemm(int t, int H) { return t > kGemvRows && (H >= kGemmMinHidden || t >= kNarrowGemmRows); }
@@ -600,6 +622,26 @@ static bool step_gemm(int t, int H) { return t > kGemvRows && (H >= kGemmMinHidd
 // streams faster per CU).
 static int narrow_nt(const DMat& w, bool int8_pieces) {
     return w.kind == BF16 && w.n_tiles < 256 && !int8_pieces ? 1 : 2;
+}
+
+// Split K of a residual projection (o, down) in a decode step: a quantized
+// projection whose output groups (two n-tiles, the 32 columns of an int8
+// k-block of its consumer) cannot fill the CUs splits K among up to
+// kGemvSplitMax workgroups per group, to at most 256 workgroups, while each
+// share keeps at least 16 chunks of four k-blocks. A CU streams only about
+// 20 GB/s of weights, so 64 busy CUs cap a projection near 1.3 TB/s; the
+// last workgroup of a group to finish sums the partials (k_gemv), which
+// costs about 1.5 us. Measured on the 1.7B shape (graph, cold weights):
+// down (64 groups, 64 chunks) 10.2 us unsplit, 7.1 us in four; o (16
+// chunks) 5.3 us unsplit, 5.6 to 6.1 us split, so it stays whole.
+static constexpr int kGemvSplitMax = 8;
+static int gemv_split(const DMat& d, int nt, int passes, bool mm) {
+    if (mm || passes != 1 || d.kind == BF16) return 1;
+    const int groups = d.n_tiles / nt, kc = d.kb / 4;
+    if (groups > kGemvSplitGroups) return 1;
+    int s = 1;
+    while (s < kGemvSplitMax && groups * s * 2 <= 256 && kc >= s * 2 * 16) s *= 2;
+    return s;
 }
 static int qkv_dim(const fg_config& c) { return (c.heads + 2 * c.kv_heads) * c.head_dim; }
 
@@ -637,6 +679,8 @@ static size_t layout_work(const fg_model* m, const Plan& P, Work& w, void* base)
     // the split rule keeps splits x rows x N within 64 x 256 x 64 floats
     w.kpart_cap = step_gemm(t, H) || S > kGemvRows ? (size_t)1 << 20 : 0;
     w.kpart = w.kpart_cap ? cv.take<float>(w.kpart_cap) : nullptr;
+    // GEMV split K: [group][split][16 rows][group columns] over the hidden columns
+    w.gpart = w.passes == 1 ? cv.take<float>((size_t)kGemvSplitMax * 16 * H) : nullptr;
     return cv.off + 256;
 }
 
@@ -759,6 +803,11 @@ static int run_forward(fg_ctx* ctx, const fg_model* m, fg_kv* kv, const Plan& P,
         g.pa_kb = l.w_gate_up.kb;
         g.nt = narrow_nt(l.wo, g.pa_kind == INT8 || g.pa_kind == INT4);
         g.mm = mm;
+        if (!am) {
+            g.gsplit = gemv_split(l.wo, g.nt, passes, mm);
+            g.gpart = w.gpart;
+            g.gcnt = ctx->gcnt;
+        }
         ss_cols = mm ? 64 : 16 * g.nt;
         gemv(ctx, EPI_RESID, l.wo, g);
         cur ^= 1;
@@ -795,6 +844,9 @@ static int run_forward(fg_ctx* ctx, const fg_model* m, fg_kv* kv, const Plan& P,
         }
         g.nt = narrow_nt(l.w_down, g.pa && (g.pa_kind == INT8 || g.pa_kind == INT4));
         g.mm = mm;
+        g.gsplit = gemv_split(l.w_down, g.nt, passes, mm);
+        g.gpart = w.gpart;
+        g.gcnt = ctx->gcnt;
         ss_cols = mm ? 64 : 16 * g.nt;
         gemv(ctx, EPI_RESID, l.w_down, g);
         cur ^= 1;
@@ -845,6 +897,23 @@ int fg_ctx_create(int device, fg_ctx** out) {
         return fail(FG_E_DEVICE, "stream creation failed");
     }
     for (auto& e : c->ev) HIPCHK(hipEventCreate(&e));
+    if (hipMalloc((void**)&c->gcnt, kGemvSplitGroups * 32 * sizeof(unsigned)) != hipSuccess) {
+        fg_ctx_destroy(c);
+        return fail(FG_E_NOMEM, "counter allocation failed");
+    }
+    HIPCHK(hipMemset(c->gcnt, 0, kGemvSplitGroups * 32 * sizeof(unsigned)));
+    // the persistent draft forward is opt-in (FERRO_PDRAFT=1): on MI355X its
+    // in-kernel cross-XCD handoffs cost about what graph kernel boundaries do
+    const char* npd = std::getenv("FERRO_PDRAFT");
+    c->pdraft = npd && npd[0] == '1';
+    if (c->pdraft) {
+        // every workgroup of the persistent draft must be resident at once: at
+        // the largest LDS operand the eligibility rule admits (1536 columns)
+        c->pd_groups = pdraft_init() == hipSuccess ? pdraft_groups(kPdMaxKb) : 0;
+        if (c->pd_groups < 64) c->pdraft = false;
+        const char* sp = std::getenv("FERRO_PDRAFT_SPIN");
+        if (sp && std::atoi(sp) > 0) c->pd_spin = std::atoi(sp);
+    }
     const char* ng = std::getenv("FERRO_NO_GRAPH");
     c->graphs = !(ng && ng[0] == '1');
     const char* sm = std::getenv("FERRO_SEPARATE_MERGE");
@@ -862,6 +931,10 @@ void fg_ctx_destroy(fg_ctx* c) {
     if (c->sbuf) (void)hipFree(c->sbuf);
     if (c->dmeta) (void)hipFree(c->dmeta);
     if (c->hmeta) (void)hipHostFree(c->hmeta);
+    if (c->gcnt) (void)hipFree(c->gcnt);
+    if (c->pd_ll) (void)hipFree(c->pd_ll);
+    if (c->pd_ctl) (void)hipFree(c->pd_ctl);
+    if (c->pd_abort) (void)hipHostFree(c->pd_abort);
     for (auto& e : c->ev)
         if (e) (void)hipEventDestroy(e);
     for (auto& e : c->pev) (void)hipEventDestroy(e);
@@ -967,6 +1040,7 @@ int fg_model_truncated(fg_ctx* ctx, const fg_model* base, int32_t layers, fg_mod
 
 void fg_model_destroy(fg_model* m) {
     if (!m) return;
+    if (m->pd_layers) (void)hipFree(m->pd_layers);
     if (m->owns)
         for (void* p : m->allocs) (void)hipFree(p);
     delete m;
@@ -1103,6 +1177,147 @@ static int check_sampling(const fg_sampling* p, int n, bool* wide) {
     return 0;
 }
 
+// Whether a draft round runs as one persistent launch (pdraft.hip): greedy,
+// one sequence of at most kPdMaxRows new rows, a bf16 model with head_dim 64,
+// at most kPdMaxGqa query heads per kv head, sizes the kernel's fetch slots
+// cover (hidden, intermediate and q sizes up to 1536), a vocabulary of whole
+// 64-row lm_head groups and a hidden tile per workgroup.
+static bool pdraft_eligible(const fg_ctx* ctx, const fg_model* d, int n_seqs, bool sampling, const Plan& P) {
+    if (!ctx->pdraft || n_seqs != 1 || sampling || P.t < 1 || P.t > kPdMaxRows || P.S != 1) return false;
+    const fg_config& c = d->cfg;
+    const int L = (int)d->layers.size();
+    if (c.head_dim != 64 || c.heads % c.kv_heads || c.heads / c.kv_heads > kPdMaxGqa || L < 1 || 6 * L + 2 > 255)
+        return false;
+    const int qd = c.heads * 64, kvd = c.kv_heads * 64;
+    if (c.hidden > 1536 || c.intermediate > 1536 || qd > 1536 || c.hidden % 16 || c.intermediate % 16 ||
+        (qd + 2 * kvd) % 16 || c.vocab % 64 || c.hidden / 16 > ctx->pd_groups || d->lm_head.kind != BF16)
+        return false;
+    for (const DLayer& l : d->layers)
+        if (l.wqkv.kind != BF16 || l.wo.kind != BF16 || l.w_gate_up.kind != BF16 || l.w_down.kind != BF16 ||
+            l.w_gate_up.il != 16)
+            return false;
+    return true;
+}
+
+// Clears the persistent draft's exchange words and restarts its epoch at 1
+// (no launch of it may be in flight).
+static int pdraft_reset(fg_ctx* ctx) {
+    HIPCHK(hipMemset(ctx->pd_ctl, 0, kPdCtlWords * sizeof(unsigned)));
+    const unsigned one = 1;
+    HIPCHK(hipMemcpy(ctx->pd_ctl + kPdCtlEpoch, &one, sizeof(one), hipMemcpyHostToDevice));
+    if (ctx->pd_ll) HIPCHK(hipMemset(ctx->pd_ll, 0, ctx->pd_ll_cap * sizeof(uint64_t)));
+    HIPCHK(hipDeviceSynchronize());
+    ctx->pd_launches = 0;
+    return 0;
+}
+
+// Buffers of the persistent draft forward for model d, which is about to be
+// launched `rounds` times: the context's exchange and control words (zeroed,
+// epoch 1) and the model's layer records. Runs before any capture.
+static int pdraft_setup(fg_ctx* ctx, fg_model* d, int rounds) {
+    const fg_config& c = d->cfg;
+    const int qd = c.heads * 64, kvd = c.kv_heads * 64, spans = (d->max_pos + 63) / 64;
+    const size_t need = pdraft_sizes(c.hidden, c.intermediate, qd, kvd, c.heads, c.kv_heads, spans).total();
+    int rc;
+    bool fresh = false;
+    if (!ctx->pd_ctl) {
+        HIPCHK(hipMalloc((void**)&ctx->pd_ctl, kPdCtlWords * sizeof(unsigned)));
+        HIPCHK(hipHostMalloc((void**)&ctx->pd_abort, sizeof(unsigned), hipHostMallocDefault));
+        *ctx->pd_abort = 0;
+        fresh = true;
+    }
+    if (need > ctx->pd_ll_cap) {
+        HIPCHK(hipStreamSynchronize(ctx->stream));
+        if (ctx->pd_ll) HIPCHK(hipFree(ctx->pd_ll));
+        ctx->pd_ll = nullptr;
+        ctx->pd_ll_cap = 0;
+        HIPCHK(hipMalloc((void**)&ctx->pd_ll, need * sizeof(uint64_t)));
+        ctx->pd_ll_cap = need;
+        fresh = true;
+    }
+    if (!fresh && ctx->pd_launches + rounds >= (1u << 24) - 256) {
+        HIPCHK(hipStreamSynchronize(ctx->stream));
+        fresh = true;
+    }
+    if (fresh && (rc = pdraft_reset(ctx))) return rc;
+    ctx->pd_launches += rounds;
+    if (!d->pd_layers) {
+        std::vector<PdLayer> h(d->layers.size());
+        for (size_t i = 0; i < d->layers.size(); i++) {
+            const DLayer& l = d->layers[i];
+            h[i] = PdLayer{l.wqkv.w, l.wo.w, l.w_gate_up.w, l.w_down.w, l.wqkv.kb, l.wo.kb, l.w_gate_up.kb,
+                           l.w_down.kb, l.attn_norm, l.mlp_norm, l.bqkv};
+        }
+        HIPCHK(hipMalloc((void**)&d->pd_layers, h.size() * sizeof(PdLayer)));
+        HIPCHK(hipMemcpy(d->pd_layers, h.data(), h.size() * sizeof(PdLayer), hipMemcpyHostToDevice));
+    }
+    return 0;
+}
+
+// The persistent draft round r over plan P (pdraft_eligible): rows at the
+// positions from device word *pos0 on, tokens at tok[row * tok_stride], the
+// argmax into am and aux[aux_off] (stride aux_stride).
+static void pdraft_round(fg_ctx* ctx, const fg_model* d, fg_kv* kv, const Plan& P, const int32_t* pos0,
+                         const int32_t* blocks,
+                         const uint32_t* tok, int tok_stride, uint32_t* am, uint32_t* aux, int aux_stride,
+                         int aux_off) {
+    const fg_config& c = d->cfg;
+    PdArgs a{};
+    a.layers = d->pd_layers;
+    a.kc = kv->k;
+    a.vc = kv->v;
+    a.layer_floats = kv->layer_floats();
+    a.L = (int)d->layers.size();
+    a.H = c.hidden;
+    a.I = c.intermediate;
+    a.nh = c.heads;
+    a.nkv = c.kv_heads;
+    a.qd = c.heads * 64;
+    a.kvd = c.kv_heads * 64;
+    a.V = c.vocab;
+    a.eps = c.rms_eps;
+    a.scale = 1.0f / sqrtf(64.0f);
+    a.embed = d->embed;
+    a.lm = d->lm_head.w;
+    a.lm_kb = d->lm_head.kb;
+    a.norm = d->norm;
+    a.cos_t = d->cos_t;
+    a.sin_t = d->sin_t;
+    a.t = P.t;
+    a.pos0 = pos0;
+    a.tok = tok;
+    a.tok_stride = tok_stride;
+    a.blocks = blocks;
+    a.logits_rows = 1;
+    int kbmax = d->lm_head.kb;
+    for (const DLayer& l : d->layers)
+        for (const DMat* m : {&l.wqkv, &l.wo, &l.w_gate_up, &l.w_down}) kbmax = std::max(kbmax, m->kb);
+    a.ap_kb = kbmax;
+    const int qd = a.qd, kvd = a.kvd, spans = (d->max_pos + 63) / 64;
+    const PdSizes z = pdraft_sizes(c.hidden, c.intermediate, qd, kvd, c.heads, c.kv_heads, spans);
+    uint64_t* p = ctx->pd_ll;
+    a.xa = p;
+    p += z.xa;
+    a.xb = p;
+    p += z.xb;
+    a.qkv = p;
+    p += z.qkv;
+    a.att = p;
+    p += z.att;
+    a.act = p;
+    p += z.act;
+    a.part = p;
+    p += z.part;
+    a.lmp = p;
+    a.ctl = ctx->pd_ctl;
+    a.spin = ctx->pd_spin;
+    a.am = am;
+    a.aux = aux;
+    a.aux_stride = aux_stride;
+    a.aux_off = aux_off;
+    launch_pdraft(ctx->stream, ctx->pd_groups, a);
+}
+
 static int spec_step(fg_ctx* ctx, const fg_model* target, fg_kv* tkv, const fg_model* draft, fg_kv* dkv,
                      const fg_spec_seq* seqs, int32_t n_seqs, int32_t k, const fg_sampling* params, uint64_t* rng,
                      uint32_t* out_tokens, int32_t* out_count, int32_t* out_accepted) {
@@ -1148,6 +1363,14 @@ static int spec_step(fg_ctx* ctx, const fg_model* target, fg_kv* tkv, const fg_m
     }
     const size_t o_vtok = words;
     words += (size_t)n_seqs * K1 + 64;
+    // the persistent draft rounds' first positions (k words), then the block
+    // table (one sequence; room rounded up to 64 blocks, so the layout and a
+    // step graph keyed on it change only every 1024 positions)
+    std::vector<bool> pd(k, false);
+    bool any_pd = false;
+    for (int r = 0; r < k; r++) any_pd |= (pd[r] = pdraft_eligible(ctx, draft, n_seqs, sampling, plans[r]));
+    const size_t o_dbt = words;
+    if (any_pd) words += (size_t)k + ((size_t)seqs[0].n_draft_blocks + 63) / 64 * 64 + 64;
     // sampling: parameters and generator states (uploaded with the plans; the
     // states come back with the outputs)
     words = (words + 15) / 16 * 16;  // 64-byte aligned parameters and states
@@ -1167,6 +1390,12 @@ static int spec_step(fg_ctx* ctx, const fg_model* target, fg_kv* tkv, const fg_m
     if ((rc = ensure(&ctx->dmeta, &ctx->dmeta_cap, words * 4, ctx->stream, false))) return rc;
     int32_t* h = (int32_t*)ctx->hmeta;
     for (int r = 0; r <= k; r++) pack_plan(plans[r], h + base[r]);
+    if (any_pd) {
+        if ((rc = pdraft_setup(ctx, const_cast<fg_model*>(draft), (int)std::count(pd.begin(), pd.end(), true))))
+            return rc;
+        for (int r = 0; r < k; r++) h[o_dbt + r] = r == 0 ? seqs[0].draft_pos : seqs[0].pos + r;
+        for (int b = 0; b < seqs[0].n_draft_blocks; b++) h[o_dbt + k + b] = (int32_t)seqs[0].draft_blocks[b];
+    }
     uint32_t* hv = (uint32_t*)(h + o_vtok);
     for (int s = 0; s < n_seqs; s++) {
         hv[s * K1] = seqs[s].tail[seqs[s].n_tail - 1];
@@ -1200,6 +1429,11 @@ static int spec_step(fg_ctx* ctx, const fg_model* target, fg_kv* tkv, const fg_m
             const int stride = r == 0 ? 1 : K1;
             // the draft's proposal d_{r+1} goes to verify row s, column r+1: the
             // greedy argmax, replaced by a draw for sampled sequences
+            if (pd[r]) {
+                pdraft_round(ctx, draft, dkv, plans[r], dm + o_dbt + r, dm + o_dbt + k, tok, stride,
+                             (uint32_t*)(dm + o_am), vtok, K1, r + 1);
+                continue;
+            }
             int e = run_forward(ctx, draft, dkv, plans[r], meta, tok, stride, w, sampling ? w.logits : nullptr,
                                 (uint32_t*)(dm + o_am), vtok, K1, r + 1, nullptr);
             if (e) return e;
@@ -1237,7 +1471,9 @@ static int spec_step(fg_ctx* ctx, const fg_model* target, fg_kv* tkv, const fg_m
                                     (int64_t)tkv->serial, (int64_t)dkv->serial, (int64_t)(uintptr_t)ctx->ws,
                                     (int64_t)ctx->ws_cap, (int64_t)(uintptr_t)ctx->dmeta, (int64_t)ctx->dmeta_cap,
                                     (int64_t)sampling, (int64_t)wide, (int64_t)(uintptr_t)ctx->sbuf,
-                                    (int64_t)ctx->sbuf_cap};
+                                    (int64_t)ctx->sbuf_cap, (int64_t)(uintptr_t)ctx->pd_ll, (int64_t)ctx->pd_ll_cap,
+                                    (int64_t)o_out};
+        for (int r = 0; r < k; r++) sig.push_back((int64_t)pd[r]);
         for (int r = 0; r <= k; r++) {
             const Plan& P = plans[r];
             for (int64_t v : {(int64_t)P.t, (int64_t)P.S, (int64_t)P.Wc, (int64_t)P.words, (int64_t)P.ns,
@@ -1296,7 +1532,17 @@ static int spec_step(fg_ctx* ctx, const fg_model* target, fg_kv* tkv, const fg_m
     HIPCHK(hipGetLastError());
     HIPCHK(hipEventRecord(ctx->ev[2], ctx->stream));
     HIPCHK(hipMemcpyAsync(h + o_rng, dm + o_rng, (words - o_rng) * 4, hipMemcpyDeviceToHost, ctx->stream));
+    if (any_pd)
+        HIPCHK(hipMemcpyAsync(ctx->pd_abort, ctx->pd_ctl + kPdCtlAbort, sizeof(unsigned), hipMemcpyDeviceToHost,
+                              ctx->stream));
     HIPCHK(hipStreamSynchronize(ctx->stream));
+    if (any_pd && *ctx->pd_abort) {
+        // a wait of the persistent draft timed out: its outputs are not valid; the
+        // words start over (every workgroup has finished)
+        *ctx->pd_abort = 0;
+        if ((rc = pdraft_reset(ctx))) return rc;
+        return fail(FG_E_DEVICE, "the persistent draft forward timed out waiting for its inputs");
+    }
     if (sampling) memcpy(rng, h + o_rng, (size_t)n_seqs * 8);
     memcpy(out_tokens, h + o_out, (size_t)n_seqs * K1 * 4);
     memcpy(out_count, h + o_cnt, (size_t)n_seqs * 4);

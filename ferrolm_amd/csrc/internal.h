@@ -114,6 +114,14 @@ struct GemvArgs {
     // ARGMAX
     float* logits = nullptr;
     float2* best = nullptr;
+    // GEMV split K (decode steps of one pass): gsplit workgroups share each
+    // output group's inputs; each stores its partial tile in gpart
+    // [group][split][16 rows][16 * nt] and bumps the group's counter gcnt[32 *
+    // group] (zero between launches); the last to arrive sums the partials in
+    // split order and runs the epilogue.
+    int gsplit = 1;
+    float* gpart = nullptr;
+    unsigned* gcnt = nullptr;
     // RESID with am: the input is the attention output, merged in the workgroup
     // from the span partials (AttnArgs::part / mrec) instead of read as pieces
     bool am = false;

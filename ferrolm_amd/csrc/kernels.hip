@@ -18,7 +18,7 @@
 //                                                             src/kernels.rs:703-756
 //   k_merge_pieces  the softmax normalisation of attend       src/kernels.rs:722-732
 //   k_accept        Engine::execute greedy accept             src/engine.rs:563-616
-#include "internal.h"
+#include "devutil.h"
 
 #include <hip/hip_ext.h>
 #include <math.h>
@@ -27,152 +27,6 @@
 #include <type_traits>
 
 namespace fg {
-
-typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
-typedef float f32x4 __attribute__((ext_vector_type(4)));
-typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-typedef uint16_t u16x8 __attribute__((ext_vector_type(8)));
-typedef int8_t i8x8 __attribute__((ext_vector_type(8)));
-typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
-typedef float f32x2 __attribute__((ext_vector_type(2)));
-
-// A load marked non-temporal (NT) or plain. Data read once per step (quantized
-// weights and their scales, the lm_heads, the KV cache) is loaded
-// non-temporally: such lines are not kept in the 256 MB memory-side cache,
-// which then holds what a step reads again (a bf16 draft's layer weights,
-// 212 MB at 135M, read by every draft round). Measured: a 200 MB buffer stays
-// resident across a 1.2 GB non-temporal stream and is evicted by a plain one.
-template <bool NT, typename T>
-__device__ __forceinline__ T ld_nt(const T* p) {
-    if constexpr (NT)
-        return __builtin_nontemporal_load(p);
-    else
-        return *p;
-}
-__device__ __forceinline__ float4 ld_nt_f4(const float* p) {
-    const f32x4 v = __builtin_nontemporal_load((const f32x4*)p);
-    return make_float4(v[0], v[1], v[2], v[3]);
-}
-
-__device__ __forceinline__ float bf16_bits_to_f32(uint32_t h) { return __uint_as_float(h << 16); }
-
-// round to nearest even (v_cvt_pk_bf16_f32)
-__device__ __forceinline__ uint32_t f32_to_bf16_bits(float x) { return __builtin_bit_cast(uint16_t, (__bf16)x); }
-
-// exp(x) by range reduction and the Cephes expf polynomial, the same
-// sequence of operations as the reference's kernels::exp (src/kernels.rs:609-637).
-__device__ __forceinline__ float dev_exp(float x) {
-    x = fminf(fmaxf(x, -87.0f), 88.0f);
-    const float n = rintf(x * 1.44269504088896341f);
-    const float r = fmaf(n, 2.1219444e-4f, fmaf(n, -0.6933594f, x));
-    float p = 1.9875691e-4f;
-    p = fmaf(p, r, 1.3982e-3f);
-    p = fmaf(p, r, 8.333452e-3f);
-    p = fmaf(p, r, 4.1665796e-2f);
-    p = fmaf(p, r, 0.16666665f);
-    p = fmaf(p, r, 0.5f);
-    const float y = fmaf(p, r * r, r) + 1.0f;
-    return y * __int_as_float(((int)n + 127) << 23);
-}
-
-// ---------------------------------------------------------------------------
-// Activation pieces (see Pieces in internal.h). Called by a whole wave: lane
-// l holds v[0..7] = inputs 8*(l/16)..+7 of k-block kb for (row, piece) =
-// (4*pass + (l%16)/4, l%4). The four lanes of a (row, inputs) pair must hold
-// bit-identical v: each writes its own piece, and for int8 each derives the
-// block scale itself. Producers that combine values across lanes therefore
-// sum rounded values in a symmetric order (the library is built without
-// floating-point contraction, so a shuffle sum is never fused with a product).
-// ---------------------------------------------------------------------------
-// Cross-lane reductions without the LDS crossbar (ds_bpermute). Within rows
-// of 16 lanes: DPP quad swaps (partners l^1, l^2) and the row mirrors; across
-// rows: the gfx950 row swaps, whose two results hold the even and the odd
-// 16-lane rows (or 32-lane halves), so both lanes of a pair combine the same
-// operands in the same order and end with the same bits. Every lane of the
-// group must be active.
-template <int CTRL>
-__device__ __forceinline__ float dpp_f(float v) {
-    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
-}
-__device__ __forceinline__ float lane_xor1(float v) { return dpp_f<0xB1>(v); }  // quad_perm [1,0,3,2]
-__device__ __forceinline__ float lane_xor2(float v) { return dpp_f<0x4E>(v); }  // quad_perm [2,3,0,1]
-template <bool MAX>
-__device__ __forceinline__ float red_op(float x, float y) { return MAX ? fmaxf(x, y) : x + y; }
-// over lanes l, l^16 (and l^32 when WIDE)
-template <bool MAX, bool WIDE>
-__device__ __forceinline__ float reduce_rows(float v) {
-    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-    v = red_op<MAX>(__uint_as_float(r[0]), __uint_as_float(r[1]));
-    if (WIDE) {
-        const auto h = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-        v = red_op<MAX>(__uint_as_float(h[0]), __uint_as_float(h[1]));
-    }
-    return v;
-}
-// out[j] = v of lane (l % 16) + 16 j, for every lane l.
-__device__ __forceinline__ void gather_rows(float v, float (&out)[4]) {
-    const uint32_t x = __float_as_uint(v);
-    const auto a = __builtin_amdgcn_permlane16_swap(x, x, false, false);  // rows (2r, 2r+1) of each half
-    const auto e = __builtin_amdgcn_permlane32_swap(a[0], a[0], false, false);
-    const auto o = __builtin_amdgcn_permlane32_swap(a[1], a[1], false, false);
-    out[0] = __uint_as_float(e[0]);
-    out[1] = __uint_as_float(o[0]);
-    out[2] = __uint_as_float(e[1]);
-    out[3] = __uint_as_float(o[1]);
-}
-// Max / sum over aligned groups of N lanes (4, 8, 16, 32 or 64).
-template <int N, bool MAX>
-__device__ __forceinline__ float group_reduce(float v) {
-    static_assert(N == 4 || N == 8 || N == 16 || N == 32 || N == 64, "4, 8, 16, 32 or 64 lanes");
-    v = red_op<MAX>(v, lane_xor1(v));
-    v = red_op<MAX>(v, lane_xor2(v));
-    if (N >= 8) v = red_op<MAX>(v, dpp_f<0x141>(v));  // row_half_mirror: the other quad of the 8
-    if (N >= 16) v = red_op<MAX>(v, dpp_f<0x140>(v));  // row_mirror: the other 8 of the row
-    if (N >= 32) v = reduce_rows<MAX, N == 64>(v);
-    return v;
-}
-
-// bf16 piece `piece` of x: four successive bf16 roundings of the remainder
-// (all four are formed and one is selected, without branches).
-__device__ __forceinline__ uint32_t bf16_piece(float x, int piece) {
-    uint32_t h = f32_to_bf16_bits(x), sel = h;
-#pragma unroll
-    for (int p = 1; p < 4; p++) {
-        x = x - bf16_bits_to_f32(h);
-        h = f32_to_bf16_bits(x);
-        sel = p == piece ? h : sel;
-    }
-    return sel;
-}
-
-// Exponent e of the int8 block scale 2^e shared by the four lanes of a row
-// (l, l^16, l^32, l^48 hold its 32 inputs; mx is this lane's max |input|):
-// the block maximum / 2^e lies in [64, 128) and never rounds past 127.
-__device__ __forceinline__ int int8_block_exp(float mx) {
-    mx = reduce_rows<true, true>(mx);
-    int e = 0;
-    if (mx > 0.0f) {
-        int fe;
-        frexpf(mx, &fe);
-        e = fe - 7;
-        if (ldexpf(mx, -e) > 127.0f) e++;
-    }
-    return e;
-}
-
-// int8 piece `piece` of x at block exponent e: x / 2^e = a0 + a1/128 + ...
-__device__ __forceinline__ int int8_piece(float x, int e, int piece) {
-    float r = ldexpf(x, -e);  // exact
-    float a = rintf(r), sel = a;
-#pragma unroll
-    for (int p = 1; p < 4; p++) {
-        r = (r - a) * 128.0f;  // both exact
-        a = rintf(r);
-        sel = p == piece ? a : sel;
-    }
-    return (int)sel;
-}
 
 template <int CK>
 __device__ __forceinline__ void write_pieces(const float (&v)[8], int kb, int pass, int passes, int row, int piece,
@@ -512,7 +366,10 @@ __global__ __launch_bounds__(64 * WMAX) void k_gemv(const GemvArgs a) {
     }
     const int np = min(PG, a.p_total - pass0);
     const int KB = a.KB, KC = KB >> 2;
-    const int c0 = wave * KC / W, c1 = (wave + 1) * KC / W;
+    // split K (gridDim.y > 1): this workgroup's share of the chunks, split among its waves
+    const int ks = gridDim.y, split = blockIdx.y;
+    const int cs0 = split * KC / ks, cs1 = (split + 1) * KC / ks;
+    const int c0 = cs0 + wave * (cs1 - cs0) / W, c1 = cs0 + (wave + 1) * (cs1 - cs0) / W;
 
     // 1/rms of the input rows from the producers' sum-of-squares partials
     // ss_in[tile][row]: slot (row r, j) sums tiles j, j + 16, ... The fast path
@@ -735,6 +592,8 @@ __global__ __launch_bounds__(64 * WMAX) void k_gemv(const GemvArgs a) {
     } else {
         int c = c0;
         for (; c + U <= c1; c += U) chunks(c, std::integral_constant<int, U>{});
+        if constexpr (U > 2)
+            for (; c + 2 <= c1; c += 2) chunks(c, std::integral_constant<int, 2>{});
         if constexpr (U > 1)
             for (; c < c1; c++) chunks(c, std::integral_constant<int, 1>{});
     }
@@ -788,6 +647,44 @@ __global__ __launch_bounds__(64 * WMAX) void k_gemv(const GemvArgs a) {
         yt[(p * 4 + (l >> 4)) * YS + t * 16 + (l & 15)] = v;
     }
     __syncthreads();
+    if (EPI != EPI_ARGMAX && ks > 1) {
+        // The workgroups of the group meet: each stores its partial tile with
+        // agent-coherent (L2-bypassing) stores and, once they have completed,
+        // bumps the group's counter; the last to arrive reads every partial the
+        // same way and sums them in split order (the same bits whichever
+        // arrives last), then runs the epilogue. The counter is reset for the
+        // next launch by that last workgroup.
+        __shared__ int last;
+        float* gp = a.gpart + (size_t)blockIdx.x * ks * (16 * COLS);
+        for (int idx = threadIdx.x; idx < rows * COLS; idx += blockDim.x)
+            __hip_atomic_store(gp + (size_t)split * 16 * COLS + idx, yt[(idx / COLS) * YS + idx % COLS],
+                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            unsigned* cnt = a.gcnt + (size_t)blockIdx.x * 32;
+            const unsigned old = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            last = old == (unsigned)ks - 1;
+            if (last) __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        __syncthreads();
+        if (!last) return;
+        constexpr int KSMAX = 8;
+        for (int idx = threadIdx.x; idx < rows * COLS; idx += blockDim.x) {
+            float pv[KSMAX];
+#pragma unroll
+            for (int s = 0; s < KSMAX; s++)
+                pv[s] = s >= ks ? 0.0f
+                                : __hip_atomic_load(gp + (size_t)s * 16 * COLS + idx, __ATOMIC_RELAXED,
+                                                    __HIP_MEMORY_SCOPE_AGENT);
+            float v = pv[0];
+#pragma unroll
+            for (int s = 1; s < KSMAX; s++)
+                if (s < ks) v += pv[s];
+            yt[(idx / COLS) * YS + idx % COLS] = v;
+        }
+        __syncthreads();
+    }
 
     if (EPI == EPI_STORE || EPI == EPI_QKV) {
 #pragma unroll
@@ -1331,6 +1228,12 @@ static void gemv_pg(hipStream_t st, const DMat& w, const GemvArgs& a, hipEvent_t
     const int KC = w.kb / 4;
     const int maxw = 8;  // waves per group: launch bounds of k_gemv
     if (a.p_total == 1) {
+        if (a.gsplit > 1) {
+            // split K: up to 8 waves over each workgroup's share of the chunks
+            const int W = std::max(1, std::min(maxw, KC / a.gsplit));
+            launch_timed(k_gemv<KIND, NT, EPI, 1>, dim3(groups, a.gsplit, 1), dim3(64 * W), st, a, e0, e1);
+            return;
+        }
         if constexpr (KIND == INT4 && NT == 2) {
             if (KC >= 16) {
                 // 16 waves (4 per SIMD) cover each other's waits on the big int4 matrices
