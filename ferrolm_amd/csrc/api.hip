@@ -8,6 +8,7 @@
 #include "pdraft.h"
 
 #include <algorithm>
+#include <mutex>
 #include <atomic>
 #include <cstdlib>
 #include <functional>
@@ -77,6 +78,9 @@ struct Carver {
 struct fg_ctx {
     int device = 0;
     hipStream_t stream = nullptr;
+    // this device's copy of `scratch` (fg_matmul_device_noalloc), from
+    // hipGetSymbolAddress at creation; nullptr when that failed
+    uint8_t* scratch = nullptr;
     void* ws = nullptr;
     size_t ws_cap = 0;
     void* sbuf = nullptr;  // sampling: the distributions of a step's rows
@@ -884,6 +888,32 @@ extern "C" {
 
 const char* fg_last_error(void) { return g_err.c_str(); }
 
+// The device scratch of fg_matmul_device_noalloc: the activation pieces and
+// their block scales of one product. Each GPU holds its own copy for the
+// life of the process; host code uses only the address hipGetSymbolAddress
+// gives for the current device (kept per device below), never the array's
+// name. Calls that overlap on one GPU share it and race.
+static constexpr size_t kScratchBytes = (size_t)2 << 20;
+static __device__ __align__(256) uint8_t scratch[kScratchBytes];
+static constexpr int kMaxDevices = 64;
+static std::mutex g_scratch_mu;
+static uint8_t* g_scratch_at[kMaxDevices];
+
+// This device's scratch address (the device is current), looked up once.
+static uint8_t* scratch_address(int device) {
+    if (device < 0 || device >= kMaxDevices) return nullptr;
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_at[device]) {
+        void* ptr = nullptr;
+        if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)) != hipSuccess) {
+            (void)hipGetLastError();
+            return nullptr;
+        }
+        g_scratch_at[device] = (uint8_t*)ptr;
+    }
+    return g_scratch_at[device];
+}
+
 int fg_ctx_create(int device, fg_ctx** out) {
     if (!out) return fail(FG_E_ARG, "null out");
     int n = 0;
@@ -904,6 +934,7 @@ int fg_ctx_create(int device, fg_ctx** out) {
     HIPCHK(hipMemset(c->gcnt, 0, kGemvSplitGroups * 32 * sizeof(unsigned)));
     // the persistent draft forward is opt-in (FERRO_PDRAFT=1): on MI355X its
     // in-kernel cross-XCD handoffs cost about what graph kernel boundaries do
+    c->scratch = scratch_address(device);
     const char* npd = std::getenv("FERRO_PDRAFT");
     c->pdraft = npd && npd[0] == '1';
     if (c->pdraft) {
@@ -1758,6 +1789,32 @@ int fg_matmul_device(fg_ctx* ctx, const fg_mat* w, const float* x_dev, int32_t m
         return rc;
     layout_mat(d, m, p, &xb, &yb, &bb, wk, ctx->ws);
     matmul_launch(ctx, d, p, wk, x_dev, m, nullptr, y_dev);
+    HIPCHK(hipGetLastError());
+    return 0;
+}
+
+int fg_matmul_device_noalloc(fg_ctx* ctx, const fg_mat* w, const float* x_dev, int32_t m, float* y_dev) {
+    if (!ctx || !w || !x_dev || !y_dev || m <= 0) return fail(FG_E_ARG, "bad argument");
+    if (!ctx->scratch) return fail(FG_E_DEVICE, "no scratch address on this device");
+    if (m > kGemvRows) return fail(FG_E_SHAPE, "at most 15 rows without allocating (the GEMV path)");
+    const DMat& d = w->m;
+    // pieces, then their block scales, in the scratch (no byte of it is read
+    // before this call's k_pieces writes it: nothing to clear)
+    Pieces p;
+    p.kb = d.kb;
+    p.passes = (m + 3) / 4;
+    const size_t a_bytes = (size_t)d.kb * p.passes * 64 * 16;
+    const size_t xs_off = (a_bytes + 255) / 256 * 256;
+    if (xs_off + (size_t)d.kb * p.passes * 4 * sizeof(float) > kScratchBytes)
+        return fail(FG_E_SHAPE, "the product's pieces exceed the 2 MiB scratch (at most 504 k-blocks at 15 rows)");
+    p.a = ctx->scratch;
+    p.xs = (float*)(ctx->scratch + xs_off);
+    launch_pieces(ctx->stream, d.kind, x_dev, d.cols, m, d.cols, nullptr, nullptr, p);
+    Work wk{};
+    GemvArgs g = gemv_args(d, p, m, wk);
+    g.out = y_dev;
+    g.ldo = d.rows;
+    launch_gemv(ctx->stream, EPI_STORE, d, g);  // no timing events: nothing is created
     HIPCHK(hipGetLastError());
     return 0;
 }

@@ -123,6 +123,7 @@ EXPORTS = {
     "fg_mat_destroy": (None, [C.c_void_p]),
     "fg_matmul": (C.c_int, [C.c_void_p, C.c_void_p, f32p, C.c_int32, f32p, f32p]),
     "fg_matmul_device": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_int32, C.c_void_p]),
+    "fg_matmul_device_noalloc": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_int32, C.c_void_p]),
     "fg_quantize": (C.c_int, [C.c_void_p, C.c_int32, C.c_int32, C.c_int32, f32p, f32p, u8p, f32p]),
     "fg_awq_search": (C.c_int, [C.c_void_p, C.c_int32, C.c_int32, C.c_int32, f32p, C.c_int32, f32p, f32p,
                                 C.POINTER(FgAwqChoice), u8p, f32p]),

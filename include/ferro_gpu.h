@@ -255,6 +255,17 @@ int fg_matmul(fg_ctx* ctx, const fg_mat* w, const float* x, int32_t m,
  * time the GEMV kernels. */
 int fg_matmul_device(fg_ctx* ctx, const fg_mat* w, const float* x_dev,
                      int32_t m, float* y_dev);
+/* fg_matmul_device without allocating: no counterpart in the reference; for
+ * callers that cannot allocate device memory (HIP graph capture, tight
+ * serving loops). The same kernels, with the activation pieces in a static
+ * 2 MiB device array (one per GPU, kept until the process ends) instead of
+ * the context workspace. At most 15 rows (FG_E_SHAPE beyond), and the
+ * pieces of m rows must fit the array: ceil(m / 4) x k-blocks x 1040 bytes,
+ * k-blocks = ceil(cols / 32) rounded up to 4 (FG_E_SHAPE beyond). Calls
+ * that overlap on one GPU share the array and race. Queued on the context
+ * stream without synchronising. */
+int fg_matmul_device_noalloc(fg_ctx* ctx, const fg_mat* w, const float* x_dev,
+                             int32_t m, float* y_dev);
 
 /* ---- load-time quantization on the device ------------------------------ */
 /* QMatrix::quantize (src/quant.rs:78-143) on the device, bit for bit the
