@@ -20,7 +20,10 @@ class gives achieved = algorithmic bytes per launch / mean launch time.
 cpu_baseline: the C oracle (the reference's CPU algorithm restated) resumes
 from a copy of the GPU's KV state before the timed steps and runs as many
 spec steps as fit in --cpu-seconds on the host cores; its emitted tokens are
-compared with the GPU's from the same state.
+compared with the GPU's from the same state. It runs the oracle's fast path
+where the CPU has AVX-512: the reference's register tiles, eight-wide
+attention scores and spinning thread pool, bit-identical to the portable
+loops. The record names the CPU model, the path and the threads.
 """
 from __future__ import annotations
 
@@ -47,6 +50,19 @@ MEASURED_TRAFFIC = {"int4": 14_920_806}
 
 def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def cpu_model() -> str:
+    """The host CPU's model name (/proc/cpuinfo), or the platform's processor string."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    import platform
+    return platform.processor() or "unknown"
 
 
 def main() -> int:
@@ -181,6 +197,7 @@ def main() -> int:
         ncores = len(os.sched_getaffinity(0))
         threads = int(os.environ.get("OMP_NUM_THREADS", ncores))
         oracle.threads(threads)
+        fast = oracle.fast(True, threads)
         ot = oracle.Model(wl.target)
         od = oracle.Model(wl.draft) if wl.draft is not None else ot.truncated(wl.draft_layers)
         okv = ot.kv(kv_blocks)
@@ -207,10 +224,14 @@ def main() -> int:
             tokens.extend(int(x) for x in out)
         cpu_elapsed = time.perf_counter() - tc
         n_cpu = sum(len(e) for e in cpu_emitted)
+        oracle.fast(False)
+        path = ("the reference's AVX-512 register tiles and spinning pool" if fast
+                else "portable loops (no AVX-512 on this CPU)")
         cpu = {"value": round(n_cpu / cpu_elapsed, 3), "unit": "tok/s", "cores": threads, "kind": "port",
                "sample": f"{len(cpu_emitted)} spec steps of {wl.name} from the GPU's KV state at context "
-                         f"{ctx_start} ({n_cpu} tokens, {cpu_elapsed:.1f}s), C oracle, {threads} threads",
-               "ms_per_step": round(cpu_elapsed / len(cpu_emitted) * 1e3, 2)}
+                         f"{ctx_start} ({n_cpu} tokens, {cpu_elapsed:.1f}s), C oracle, {path}, {threads} threads",
+               "ms_per_step": round(cpu_elapsed / len(cpu_emitted) * 1e3, 2), "cpu_model": cpu_model(),
+               "path": "avx512" if fast else "portable"}
         gpu_first = emitted[:len(cpu_emitted)]
         same = sum(1 for x, y in zip(gpu_first, cpu_emitted) if x == y)
         parity = {"steps_compared": len(cpu_emitted), "steps_identical": same}

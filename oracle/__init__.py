@@ -88,6 +88,7 @@ def lib():
             "or_distribution": (C.c_int32, [f32p, C.c_int32, C.c_float, C.c_float, C.c_int32, u32p, f32p]),
             "or_draw": (C.c_uint32, [u32p, f32p, C.c_int32, C.POINTER(C.c_uint64)]),
             "or_set_threads": (None, [C.c_int32]),
+            "or_set_fast": (C.c_int32, [C.c_int32, C.c_int32]),
             "or_quantize": (C.c_int32, [C.c_int32, C.c_int32, C.c_int32, f32p, f32p, u8p, f32p]),
             "or_dequantize": (None, [C.c_int32, C.c_int32, C.c_int32, u8p, f32p, f32p]),
             "or_matmul": (C.c_int32, [C.POINTER(OrMatrix), f32p, C.c_int32, f32p, f32p]),
@@ -140,6 +141,13 @@ def matrix_struct(m: Matrix) -> OrMatrix:
 
 def threads(n: int) -> None:
     lib().or_set_threads(n)
+
+
+def fast(on: bool, threads: int = 0) -> bool:
+    """The CPU baseline's fast path (AVX-512 register tiles and a spinning
+    pool of `threads` threads, bit-identical to the portable loops) on or
+    off; False when this CPU cannot take it."""
+    return lib().or_set_fast(int(on), threads) == 0
 
 
 class Model:

@@ -22,8 +22,14 @@
 #include <float.h>
 #include <math.h>
 #include <omp.h>
+#include <pthread.h>
+#include <sched.h>
+#include <stdatomic.h>
 #include <stdlib.h>
 #include <string.h>
+#if defined(__x86_64__)
+#include <immintrin.h>
+#endif
 
 #define PANEL 32
 #define GROUP 32
@@ -481,17 +487,404 @@ HOT static void mm_q_panel(const float* x, int32_t m, int32_t K, const uint8_t* 
     (void)G;
 }
 
+/* ------------------------------------------------------------------ */
+/* The CPU baseline's fast path (or_set_fast): the reference's register */
+/* tiles (src/kernels.rs:279-289; AVX-512 tiles src/kernels.rs:378-430  */
+/* and src/quant.rs:306-374) dispatched in panel ranges on a spinning   */
+/* thread pool (src/pool.rs). Each output is the same chain of fused    */
+/* multiply-adds as in the portable loops above, in the same order, so  */
+/* the two agree bit for bit (tests/test_oracle.py holds them equal, as */
+/* the reference's ISA-invariance test does, src/quant.rs:471-506).     */
+/* ------------------------------------------------------------------ */
+static int g_fast = 0;
+static int32_t g_fast_threads = 0;
+
+/* Pool: src/pool.rs:40-152. run(n, f) calls f(0..n) on the workers and the
+ * calling thread; tasks are handed out from a shared counter, each writes a
+ * fixed part of the output. Workers spin between jobs (a decode step
+ * issues hundreds of small ones), then sleep on a condition variable. */
+#define POOL_SPINS (1 << 16)
+#define POOL_MAX 256
+typedef void (*task_fn)(void* arg, int32_t task);
+typedef struct {
+    int32_t workers;
+    pthread_t th[POOL_MAX];
+    _Atomic uint64_t generation;
+    task_fn fn;
+    void* arg;
+    _Atomic int32_t tasks, next, pending, shutdown;
+    pthread_mutex_t lock;
+    pthread_cond_t wake;
+} spool;
+static spool* g_pool = NULL;
+
+static inline void cpu_relax(void) {
+#if defined(__x86_64__)
+    _mm_pause();
+#endif
+}
+
+static void pool_drain(spool* s, task_fn fn, void* arg) {
+    int32_t n = atomic_load_explicit(&s->tasks, memory_order_relaxed);
+    for (;;) {
+        int32_t i = atomic_fetch_add_explicit(&s->next, 1, memory_order_relaxed);
+        if (i >= n) break;
+        fn(arg, i);
+    }
+}
+
+static void* pool_worker(void* p) {
+    spool* s = (spool*)p;
+    uint64_t seen = 0;
+    for (;;) {
+        int32_t spins = 0;
+        while (atomic_load_explicit(&s->generation, memory_order_acquire) == seen &&
+               !atomic_load_explicit(&s->shutdown, memory_order_relaxed)) {
+            if (++spins < POOL_SPINS) {
+                cpu_relax();
+                continue;
+            }
+            pthread_mutex_lock(&s->lock);
+            while (atomic_load_explicit(&s->generation, memory_order_acquire) == seen &&
+                   !atomic_load_explicit(&s->shutdown, memory_order_relaxed))
+                pthread_cond_wait(&s->wake, &s->lock);
+            pthread_mutex_unlock(&s->lock);
+        }
+        if (atomic_load_explicit(&s->shutdown, memory_order_relaxed)) return NULL;
+        seen = atomic_load_explicit(&s->generation, memory_order_acquire);
+        pool_drain(s, s->fn, s->arg);
+        atomic_fetch_sub_explicit(&s->pending, 1, memory_order_release);
+    }
+}
+
+static void pool_stop(void) {
+    if (!g_pool) return;
+    spool* s = g_pool;
+    atomic_store(&s->shutdown, 1);
+    pthread_mutex_lock(&s->lock);
+    pthread_cond_broadcast(&s->wake);
+    pthread_mutex_unlock(&s->lock);
+    for (int32_t i = 0; i < s->workers; i++) pthread_join(s->th[i], NULL);
+    pthread_mutex_destroy(&s->lock);
+    pthread_cond_destroy(&s->wake);
+    free(s);
+    g_pool = NULL;
+}
+
+/* A pool of `threads` threads in all, the caller included. */
+static int pool_start(int32_t threads) {
+    pool_stop();
+    spool* s = (spool*)calloc(1, sizeof(spool));
+    if (!s) return -1;
+    pthread_mutex_init(&s->lock, NULL);
+    pthread_cond_init(&s->wake, NULL);
+    int32_t want = threads - 1 < POOL_MAX ? threads - 1 : POOL_MAX;
+    for (int32_t i = 0; i < want; i++) {
+        if (pthread_create(&s->th[i], NULL, pool_worker, s)) break;
+        s->workers++;
+    }
+    g_pool = s;
+    return 0;
+}
+
+static void pool_run(int32_t tasks, task_fn fn, void* arg) {
+    if (tasks <= 0) return;
+    spool* s = g_pool;
+    if (tasks == 1 || !s || s->workers == 0) {
+        for (int32_t i = 0; i < tasks; i++) fn(arg, i);
+        return;
+    }
+    s->fn = fn;
+    s->arg = arg;
+    atomic_store_explicit(&s->tasks, tasks, memory_order_relaxed);
+    atomic_store_explicit(&s->next, 0, memory_order_relaxed);
+    atomic_store_explicit(&s->pending, s->workers, memory_order_relaxed);
+    atomic_fetch_add_explicit(&s->generation, 1, memory_order_release);
+    pthread_mutex_lock(&s->lock);
+    pthread_cond_broadcast(&s->wake);
+    pthread_mutex_unlock(&s->lock);
+    pool_drain(s, fn, arg);
+    int32_t spins = 0;
+    while (atomic_load_explicit(&s->pending, memory_order_acquire) != 0) {
+        if (++spins < POOL_SPINS)
+            cpu_relax();
+        else
+            sched_yield();
+    }
+}
+
+#if defined(__x86_64__)
+#define AVX512 __attribute__((target("avx512f,avx512bw")))
+#define AVX2 __attribute__((target("avx2,fma")))
+
+/* One register tile of `mr` rows x `np` panels over kc inner positions,
+ * starting from zero (init) or from the partial sums already in y. */
+typedef struct {
+    const float* x;
+    int32_t xs;
+    const uint16_t* w; /* bf16 panel data at (p0, k0) */
+    const uint8_t* q;  /* quantized codes at (p0, k0) */
+    const float* s;    /* group scales at (p0, k0 / GROUP) */
+    size_t ws, qs, ss; /* strides between panels */
+    int32_t kc, q4, init;
+    float* y;
+    int32_t ys;
+} mtile;
+
+/* bf16 tile: per output one chain over k from zero (src/kernels.rs:344-356). */
+#define DEF_BTILE(MR, NP)                                                                      \
+    AVX512 static void btile_##MR##_##NP(const mtile* t) {                                     \
+        __m512 acc[MR][NP][2];                                                                 \
+        for (int i = 0; i < MR; i++)                                                           \
+            for (int p = 0; p < NP; p++) {                                                     \
+                float* yy = t->y + (size_t)i * t->ys + p * PANEL;                              \
+                acc[i][p][0] = t->init ? _mm512_setzero_ps() : _mm512_loadu_ps(yy);            \
+                acc[i][p][1] = t->init ? _mm512_setzero_ps() : _mm512_loadu_ps(yy + 16);       \
+            }                                                                                  \
+        for (int32_t kk = 0; kk < t->kc; kk++) {                                               \
+            __m512 xb[MR];                                                                     \
+            for (int i = 0; i < MR; i++) xb[i] = _mm512_set1_ps(t->x[(size_t)i * t->xs + kk]); \
+            for (int p = 0; p < NP; p++) {                                                     \
+                const uint16_t* wp = t->w + p * t->ws + (size_t)kk * PANEL;                    \
+                __m512i lo = _mm512_cvtepu16_epi32(_mm256_loadu_si256((const __m256i*)wp));   \
+                __m512i hi = _mm512_cvtepu16_epi32(_mm256_loadu_si256((const __m256i*)(wp + 16))); \
+                __m512 w0 = _mm512_castsi512_ps(_mm512_slli_epi32(lo, 16));                    \
+                __m512 w1 = _mm512_castsi512_ps(_mm512_slli_epi32(hi, 16));                    \
+                for (int i = 0; i < MR; i++) {                                                 \
+                    acc[i][p][0] = _mm512_fmadd_ps(xb[i], w0, acc[i][p][0]);                   \
+                    acc[i][p][1] = _mm512_fmadd_ps(xb[i], w1, acc[i][p][1]);                   \
+                }                                                                              \
+            }                                                                                  \
+        }                                                                                      \
+        for (int i = 0; i < MR; i++)                                                           \
+            for (int p = 0; p < NP; p++) {                                                     \
+                float* yy = t->y + (size_t)i * t->ys + p * PANEL;                              \
+                _mm512_storeu_ps(yy, acc[i][p][0]);                                            \
+                _mm512_storeu_ps(yy + 16, acc[i][p][1]);                                       \
+            }                                                                                  \
+    }
+
+/* Columns 0-15 and 16-31 of one panel at one position, as f32: int8 codes,
+ * or int4 nibbles (low: columns 0-15, high: 16-31) minus 8. */
+AVX512 static inline void q_codes(const uint8_t* p, int32_t q4, __m512* w0, __m512* w1) {
+    if (q4) {
+        __m512i b = _mm512_cvtepu8_epi32(_mm_loadu_si128((const __m128i*)p));
+        __m512i eight = _mm512_set1_epi32(8);
+        *w0 = _mm512_cvtepi32_ps(_mm512_sub_epi32(_mm512_and_si512(b, _mm512_set1_epi32(0x0F)), eight));
+        *w1 = _mm512_cvtepi32_ps(_mm512_sub_epi32(_mm512_srli_epi32(b, 4), eight));
+    } else {
+        *w0 = _mm512_cvtepi32_ps(_mm512_cvtepi8_epi32(_mm_loadu_si128((const __m128i*)p)));
+        *w1 = _mm512_cvtepi32_ps(_mm512_cvtepi8_epi32(_mm_loadu_si128((const __m128i*)(p + 16))));
+    }
+}
+
+/* Quantized tile: per group a chain over its 32 positions from zero, then
+ * y = fma(group sum, scale, y) (src/quant.rs:318-370). */
+#define DEF_QTILE(MR, NP)                                                                      \
+    AVX512 static void qtile_##MR##_##NP(const mtile* t) {                                     \
+        const int32_t bpk = t->q4 ? PANEL / 2 : PANEL;                                         \
+        if (t->init)                                                                           \
+            for (int i = 0; i < MR; i++)                                                       \
+                for (int p = 0; p < NP; p++) {                                                 \
+                    float* yy = t->y + (size_t)i * t->ys + p * PANEL;                          \
+                    _mm512_storeu_ps(yy, _mm512_setzero_ps());                                 \
+                    _mm512_storeu_ps(yy + 16, _mm512_setzero_ps());                            \
+                }                                                                              \
+        for (int32_t g = 0; g < t->kc / GROUP; g++) {                                          \
+            __m512 gs[MR][NP][2];                                                              \
+            for (int i = 0; i < MR; i++)                                                       \
+                for (int p = 0; p < NP; p++) gs[i][p][0] = gs[i][p][1] = _mm512_setzero_ps();  \
+            for (int32_t kk = g * GROUP; kk < (g + 1) * GROUP; kk++) {                         \
+                __m512 xb[MR];                                                                 \
+                for (int i = 0; i < MR; i++) xb[i] = _mm512_set1_ps(t->x[(size_t)i * t->xs + kk]); \
+                for (int p = 0; p < NP; p++) {                                                 \
+                    __m512 w0, w1;                                                             \
+                    q_codes(t->q + p * t->qs + (size_t)kk * bpk, t->q4, &w0, &w1);             \
+                    for (int i = 0; i < MR; i++) {                                             \
+                        gs[i][p][0] = _mm512_fmadd_ps(xb[i], w0, gs[i][p][0]);                 \
+                        gs[i][p][1] = _mm512_fmadd_ps(xb[i], w1, gs[i][p][1]);                 \
+                    }                                                                          \
+                }                                                                              \
+            }                                                                                  \
+            for (int p = 0; p < NP; p++) {                                                     \
+                const float* sp = t->s + p * t->ss + (size_t)g * PANEL;                        \
+                __m512 s0 = _mm512_loadu_ps(sp), s1 = _mm512_loadu_ps(sp + 16);                \
+                for (int i = 0; i < MR; i++) {                                                 \
+                    float* yy = t->y + (size_t)i * t->ys + p * PANEL;                          \
+                    _mm512_storeu_ps(yy, _mm512_fmadd_ps(gs[i][p][0], s0, _mm512_loadu_ps(yy)));         \
+                    _mm512_storeu_ps(yy + 16, _mm512_fmadd_ps(gs[i][p][1], s1, _mm512_loadu_ps(yy + 16))); \
+                }                                                                              \
+            }                                                                                  \
+        }                                                                                      \
+    }
+
+DEF_BTILE(1, 1)
+DEF_BTILE(1, 2)
+DEF_BTILE(1, 3)
+DEF_BTILE(1, 4)
+DEF_BTILE(2, 1)
+DEF_BTILE(2, 2)
+DEF_BTILE(4, 1)
+DEF_BTILE(4, 2)
+DEF_BTILE(8, 1)
+DEF_QTILE(1, 1)
+DEF_QTILE(1, 2)
+DEF_QTILE(1, 3)
+DEF_QTILE(1, 4)
+DEF_QTILE(2, 1)
+DEF_QTILE(2, 2)
+DEF_QTILE(4, 1)
+DEF_QTILE(4, 2)
+DEF_QTILE(8, 1)
+
+static void run_tile(const mtile* t, int32_t bf, int32_t mr, int32_t np) {
+#define TCASE(MR, NP)                                   \
+    if (mr == MR && np == NP) {                         \
+        bf ? btile_##MR##_##NP(t) : qtile_##MR##_##NP(t); \
+        return;                                         \
+    }
+    TCASE(1, 1) TCASE(1, 2) TCASE(1, 3) TCASE(1, 4) TCASE(2, 1) TCASE(2, 2) TCASE(4, 1) TCASE(4, 2) TCASE(8, 1)
+#undef TCASE
+    abort();
+}
+
+/* The AVX-512 tile shapes by the rows left in a block (src/kernels.rs:281-289). */
+static void tile_shape(int32_t rows, int32_t* mr, int32_t* np) {
+    if (rows == 1) *mr = 1, *np = 4;
+    else if (rows <= 3) *mr = 2, *np = 2;
+    else if (rows <= 7) *mr = 4, *np = 2;
+    else *mr = 8, *np = 1;
+}
+
+/* Rows of x per cache block, inner positions per block (a multiple of GROUP). */
+#define MC 60
+#define KC 256
+
+typedef struct {
+    const omat* w;
+    const float* x;
+    float* y;
+    int32_t m, per_task, panels;
+} mm_job;
+
+/* Output panels of one task for every row (src/kernels.rs:293-322, src/quant.rs:180-217). */
+static void mm_task(void* arg, int32_t task) {
+    const mm_job* j = (const mm_job*)arg;
+    const omat* w = j->w;
+    int32_t n = w->rows, K = w->cols, bf = w->kind == OR_BF16, G = K / GROUP;
+    int32_t bpk = bf ? 0 : bytes_per_k(w->kind);
+    int32_t p0 = task * j->per_task, p1 = p0 + j->per_task < j->panels ? p0 + j->per_task : j->panels;
+    for (int32_t m0 = 0; m0 < j->m; m0 += MC) {
+        int32_t m1 = m0 + MC < j->m ? m0 + MC : j->m;
+        for (int32_t k0 = 0; k0 < K; k0 += KC) {
+            int32_t kc = KC < K - k0 ? KC : K - k0;
+            for (int32_t i = m0; i < m1;) {
+                int32_t mr, np;
+                tile_shape(m1 - i, &mr, &np);
+                for (int32_t p = p0; p < p1;) {
+                    int32_t npp = np < p1 - p ? np : p1 - p;
+                    mtile t;
+                    memset(&t, 0, sizeof(t));
+                    t.x = j->x + (size_t)i * K + k0;
+                    t.xs = K;
+                    if (bf) {
+                        t.w = w->packed + ((size_t)p * K + k0) * PANEL;
+                        t.ws = (size_t)K * PANEL;
+                    } else {
+                        t.q = w->q + ((size_t)p * K + k0) * bpk;
+                        t.qs = (size_t)K * bpk;
+                        t.s = w->s + ((size_t)p * G + k0 / GROUP) * PANEL;
+                        t.ss = (size_t)G * PANEL;
+                        t.q4 = w->kind == OR_INT4;
+                    }
+                    t.kc = kc;
+                    t.init = k0 == 0;
+                    t.y = j->y + (size_t)i * n + (size_t)p * PANEL;
+                    t.ys = n;
+                    run_tile(&t, bf, mr, npp);
+                    p += npp;
+                }
+                i += mr;
+            }
+        }
+    }
+}
+
+/* kernels::matmul's dispatch (src/kernels.rs:250-268): enough tasks to
+ * balance the threads, in whole panels. */
+static void fast_matmul(const omat* w, const float* x, int32_t m, float* y) {
+    int32_t panels = w->rows / PANEL, threads = g_pool ? g_pool->workers + 1 : 1;
+    int32_t per = panels / (threads * 6);
+    per = per < 1 ? 1 : per > 64 ? 64 : per;
+    mm_job j = {w, x, y, m, per, panels};
+    pool_run((panels + per - 1) / per, mm_task, &j);
+}
+
+/* dot's lane order (src/kernels.rs:193-214) on eight-wide vectors: lane l
+ * sums products l, l + 8, ..., then the fixed pairwise sum of the lanes. */
+AVX2 static float dot8(const float* a, const float* b, int32_t n) {
+    __m256 acc = _mm256_setzero_ps();
+    for (int32_t i = 0; i + 8 <= n; i += 8) acc = _mm256_fmadd_ps(_mm256_loadu_ps(a + i), _mm256_loadu_ps(b + i), acc);
+    float l[8];
+    _mm256_storeu_ps(l, acc);
+    return hsum8(l);
+}
+
+/* out[d] = fma(w, v[d], out[d]) for every d: the weighted values' in-order chain. */
+AVX512 static void axpy16(float* out, float w, const float* v, int32_t n) {
+    __m512 ww = _mm512_set1_ps(w);
+    int32_t d = 0;
+    for (; d + 16 <= n; d += 16)
+        _mm512_storeu_ps(out + d, _mm512_fmadd_ps(ww, _mm512_loadu_ps(v + d), _mm512_loadu_ps(out + d)));
+    for (; d < n; d++) out[d] = fmaf(w, v[d], out[d]);
+}
+#else
+static void fast_matmul(const omat* w, const float* x, int32_t m, float* y) {
+    (void)w, (void)x, (void)m, (void)y;
+    abort();
+}
+static float dot8(const float* a, const float* b, int32_t n) { return or_dot(a, b, n); }
+static void axpy16(float* out, float w, const float* v, int32_t n) {
+    for (int32_t d = 0; d < n; d++) out[d] = fmaf(w, v[d], out[d]);
+}
+#endif
+
+/* The fast path on (threads in all, caller included) when the CPU has
+ * AVX-512 F/BW; 0 when it is on, -1 when this CPU cannot take it. */
+int32_t or_set_fast(int32_t on, int32_t threads) {
+    pool_stop();
+    g_fast = 0;
+    if (!on) return 0;
+#if defined(__x86_64__)
+    __builtin_cpu_init();
+    if (!__builtin_cpu_supports("avx512f") || !__builtin_cpu_supports("avx512bw") || !__builtin_cpu_supports("avx2") ||
+        !__builtin_cpu_supports("fma"))
+        return -1;
+    if (pool_start(threads > 0 ? threads : omp_get_num_procs())) return -1;
+    g_fast = 1;
+    g_fast_threads = threads;
+    return 0;
+#else
+    (void)threads;
+    return -1;
+#endif
+}
+
 /* kernels::matmul: src/kernels.rs:249-275 (bias added after the chains) */
 static void omat_matmul(const omat* w, const float* x, int32_t m, const float* bias, float* y) {
     int32_t n = w->rows, K = w->cols, panels = n / PANEL;
     if (m == 0) return;
+    if (g_fast) {
+        fast_matmul(w, x, m, y);
+    } else {
 #pragma omp parallel for schedule(dynamic, 1)
-    for (int32_t p = 0; p < panels; p++) {
-        if (w->kind == OR_BF16)
-            mm_bf16_panel(x, m, K, w->packed + (size_t)p * K * PANEL, y, n, p);
-        else
-            mm_q_panel(x, m, K, w->q + (size_t)p * K * bytes_per_k(w->kind),
-                       w->s + (size_t)p * (K / GROUP) * PANEL, w->kind, y, n, p);
+        for (int32_t p = 0; p < panels; p++) {
+            if (w->kind == OR_BF16)
+                mm_bf16_panel(x, m, K, w->packed + (size_t)p * K * PANEL, y, n, p);
+            else
+                mm_q_panel(x, m, K, w->q + (size_t)p * K * bytes_per_k(w->kind),
+                           w->s + (size_t)p * (K / GROUP) * PANEL, w->kind, y, n, p);
+        }
     }
     if (bias)
         for (int32_t i = 0; i < m; i++)
@@ -820,7 +1213,8 @@ static void attend(const float* q, int32_t heads, int32_t hd, int32_t n, float s
         size_t base = (size_t)blocks[bi] * block_stride + head_off;
         for (int32_t o = 0; o < bs && p < n; o++, p++) {
             const float* kp = K + base + (size_t)o * hd;
-            for (int32_t j = 0; j < heads; j++) scores[(size_t)j * n + p] = or_dot(q + (size_t)j * hd, kp, hd) * scale;
+            for (int32_t j = 0; j < heads; j++)
+                scores[(size_t)j * n + p] = (g_fast ? dot8(q + (size_t)j * hd, kp, hd) : or_dot(q + (size_t)j * hd, kp, hd)) * scale;
         }
     }
     for (int32_t j = 0; j < heads; j++) {
@@ -842,7 +1236,10 @@ static void attend(const float* q, int32_t heads, int32_t hd, int32_t n, float s
             for (int32_t j = 0; j < heads; j++) {
                 float w = scores[(size_t)j * n + p];
                 float* oj = out + (size_t)j * hd;
-                for (int32_t d = 0; d < hd; d++) oj[d] = fmaf(w, vp[d], oj[d]);
+                if (g_fast)
+                    axpy16(oj, w, vp, hd);
+                else
+                    for (int32_t d = 0; d < hd; d++) oj[d] = fmaf(w, vp[d], oj[d]);
             }
         }
     }
@@ -856,6 +1253,48 @@ static void rope(float* x, const float* cs, const float* sn, int32_t hd) {
         x[i] = a * cs[i] + -b * sn[i];
         x[i + half] = b * cs[i] + a * sn[i];
     }
+}
+
+/* silu_mul on the fast path: the same element formula, in pool tasks of
+ * 1024 elements. */
+typedef struct {
+    const float* gate_up;
+    float* out;
+    int32_t inter, n;
+} silu_job;
+
+static void silu_task(void* arg, int32_t task) {
+    const silu_job* j = (const silu_job*)arg;
+    int32_t i1 = (task + 1) * 1024 < j->n ? (task + 1) * 1024 : j->n;
+    for (int32_t idx = task * 1024; idx < i1; idx++) {
+        int32_t r = idx / j->inter, i = idx % j->inter;
+        const float* g = j->gate_up + (size_t)r * 2 * j->inter;
+        float e = or_exp(-g[i]);
+        j->out[idx] = g[i] / (1.0f + e) * g[j->inter + i];
+    }
+}
+
+/* One (row, kv head) attention task of the fast path (the pool's tasks). */
+typedef struct {
+    const or_chunk* chunks;
+    const int32_t *owner, *pos;
+    const float* qkv;
+    float* att;
+    const float *K, *V;
+    int32_t group, hd, nkv, bs, qkv_dim, q_dim, maxn;
+    float scale;
+    size_t block_stride;
+} attn_job;
+
+static void attn_task(void* arg, int32_t task) {
+    const attn_job* j = (const attn_job*)arg;
+    int32_t rr = task / j->nkv, g = task % j->nkv;
+    const or_chunk* ch = &j->chunks[j->owner[rr]];
+    float* scores = (float*)malloc((size_t)j->group * j->maxn * 4);
+    attend(j->qkv + (size_t)rr * j->qkv_dim + (size_t)g * j->group * j->hd, j->group, j->hd, j->pos[rr] + 1, j->scale,
+           j->K, j->V, ch->blocks, j->bs, j->block_stride, (size_t)g * j->bs * j->hd, scores,
+           j->att + (size_t)rr * j->q_dim + (size_t)g * j->group * j->hd);
+    free(scores);
 }
 
 /* Model::forward: src/model.rs:267-362 */
@@ -935,6 +1374,11 @@ int32_t or_forward_taps(const or_model* m, or_kv* kv, const or_chunk* chunks, in
             kv_write(kv, li, slot[r], row + q_dim, row + q_dim + nkv * hd);
         }
         /* Model::attention: src/model.rs:394-432, one task per (row, kv head) */
+        if (g_fast) {
+            attn_job aj = {chunks, owner, pos, qkv, att, kv->k[li], kv->v[li], group, hd, nkv, bs, qkv_dim, q_dim,
+                           maxn, scale, block_stride};
+            pool_run(t * nkv, attn_task, &aj);
+        } else
 #pragma omp parallel
         {
             float* scores = (float*)malloc((size_t)group * maxn * 4);
@@ -954,7 +1398,12 @@ int32_t or_forward_taps(const or_model* m, or_kv* kv, const or_chunk* chunks, in
         or_rms_norm(x, l->mlp_norm, H, t, c->rms_eps, xn);
         if (tap) memcpy(tap + (size_t)t * (H + q_dim), xn, (size_t)t * H * 4);
         omat_matmul(&l->w_gate_up, xn, t, NULL, gate_up);
-        or_silu_mul(gate_up, I, t, act);
+        if (g_fast) {
+            silu_job sj = {gate_up, act, I, t * I};
+            pool_run((t * I + 1023) / 1024, silu_task, &sj);
+        } else {
+            or_silu_mul(gate_up, I, t, act);
+        }
         if (tap) memcpy(tap + (size_t)t * (2 * H + q_dim), act, (size_t)t * I * 4);
         omat_matmul(&l->w_down, act, t, NULL, proj);
         for (size_t i = 0; i < (size_t)t * H; i++) x[i] += proj[i];

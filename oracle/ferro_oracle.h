@@ -89,6 +89,12 @@ int32_t or_distribution(const float* logits, int32_t vocab, float temperature, f
 uint32_t or_draw(const uint32_t* tok, const float* p, int32_t n, uint64_t* rng);
 uint32_t or_argmax(const float* v, int32_t n);
 void or_set_threads(int32_t n);
+/* The CPU baseline's fast path: the reference's AVX-512 register tiles for
+ * the matmuls and eight-wide attention scores, on a spinning pool of
+ * `threads` threads (0: all cores), bit-identical to the portable loops.
+ * on = 0 returns to the portable loops. 0, or -1 when the CPU lacks
+ * AVX-512 F/BW (the portable loops stay). */
+int32_t or_set_fast(int32_t on, int32_t threads);
 
 /* QMatrix::quantize (src/quant.rs:82-143): codes/scales in the reference's
  * panel layout. q must hold rows*cols (int8) or rows*cols/2 (int4) bytes,

@@ -453,3 +453,46 @@ def test_speculative_sampling_keeps_the_target_distribution():
     assert 0 < accepted < proposed
     assert plain < 37.7, plain
     assert spec < 37.7, spec
+
+
+@pytest.fixture
+def fast_path():
+    """The oracle's fast path on (skips where the CPU lacks AVX-512), then off."""
+    if not oracle.fast(True, 4):
+        pytest.skip("no AVX-512 on this CPU")
+    yield
+    oracle.fast(False)
+
+
+@pytest.mark.parametrize("kind", [BF16, INT8, INT4])
+def test_fast_matmul_equals_the_portable_loops_bit_for_bit(kind, fast_path):
+    """src/quant.rs:471-506: the SIMD tiles give the portable path's bits, for
+    every tile shape (1 to 8 rows, one to four panels, the 60-row and
+    256-position blocks) and the panel ranges of the pool's tasks."""
+    rng = np.random.default_rng(11 + kind)
+    for rows, cols in ((96, 288), (224, 544), (32, 1024)):
+        w = (rng.standard_normal((rows, cols)) * 0.05).astype(np.float32)
+        mat = Matrix(BF16, rows, cols, bf16=f32_to_bf16(w)) if kind == BF16 else oracle.quantize(kind, w)
+        for m in (1, 2, 3, 4, 5, 7, 8, 9, 13, 60, 61, 67):
+            x = rng.standard_normal((m, cols)).astype(np.float32)
+            got = oracle.matmul(mat, x)
+            oracle.fast(False)
+            want = oracle.matmul(mat, x)
+            assert oracle.fast(True, 4)
+            assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), (kind, rows, cols, m)
+
+
+def test_fast_forward_equals_the_portable_loops_bit_for_bit(fast_path):
+    """The whole forward (eight-wide attention scores, sixteen-wide weighted
+    values, the tiles) gives the portable path's logits and hidden states."""
+    hm = load_model(GOLDEN / "llama-gqa")
+    om = oracle.Model(hm)
+    prompt = reference_prompts(1, 9)[0]
+    n = len(prompt)
+    got_l, got_h = om.forward(om.kv(64), [(prompt, 0, list(range(64)), 2)], hidden=True)
+    oracle.fast(False)
+    want_l, want_h = om.forward(om.kv(64), [(prompt, 0, list(range(64)), 2)], hidden=True)
+    assert oracle.fast(True, 4)
+    assert n > 16
+    assert np.array_equal(got_l.view(np.uint32), want_l.view(np.uint32))
+    assert np.array_equal(got_h.view(np.uint32), want_h.view(np.uint32))
