@@ -74,7 +74,7 @@ class BlockManager:
         return len(self._refs)
 
     def available(self) -> int:
-        """Blocks that can be allocated now (free or evictable)."""
+        """How many allocate() calls would succeed now: never-used blocks plus idle cached ones."""
         return len(self.free) + len(self.idle)
 
     def used(self) -> int:
@@ -101,7 +101,7 @@ class BlockManager:
 
     def release(self, b: int) -> None:
         if self._refs[b] <= 0:
-            raise AssertionError(f"block {b} released more often than taken")
+            raise AssertionError(f"block {b} has no reference left to drop")
         self._refs[b] -= 1
         if self._refs[b] == 0:
             if self.key[b] is not None:

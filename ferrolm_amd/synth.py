@@ -115,7 +115,11 @@ def awq_model(hm: HostModel, kind: int, seed: int) -> HostModel:
 
 
 def prompt_ids(n: int, vocab: int, seed: int) -> np.ndarray:
-    """n uniform token ids in [0, vocab) from the reference's Rng (below)."""
+    """n uniform token ids in [0, vocab): numpy's PCG64 seeded with stream_seed(seed, 99, 3).
+
+    The prompt only has to be the same on every run and in every test; the
+    synthetic weights, not the prompt, come from the reference's Rng.
+    """
     rng = np.random.default_rng(host.stream_seed(seed, 99, 3))
     return rng.integers(0, vocab, size=n, dtype=np.int64).astype(np.uint32)
 
