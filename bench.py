@@ -179,14 +179,15 @@ def main() -> int:
             f"(unprofiled {elapsed * 1e3:.1f} ms)")
         tkind = KIND_NAMES[wl.target_kind]
         dom = [x for x in recs if x["kind"] == tkind and not x["gemm"]] or recs
-        dom = max(dom, key=lambda x: x["us"])
-        ach = dom["bytes"] / dom["us"] / 1e3
-        roofline = {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                    "frac": round(ach / HBM_PEAK_GBS, 4),
-                    "traffic": MEASURED_TRAFFIC.get(dom["kind"]) if a.config == 2 else None,
-                    "kernel": f"k_gemv {dom['kind']} (target projections, m={k + 1})",
-                    "bytes_per_launch": round(dom["bytes"] / dom["launches"]),
-                    "us_per_launch": round(dom["us"] / dom["launches"], 3), "launches": dom["launches"]}
+        if dom:  # none when every projection ran inside the persistent forward (FERRO_PFWD=1)
+            dom = max(dom, key=lambda x: x["us"])
+            ach = dom["bytes"] / dom["us"] / 1e3
+            roofline = {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                        "frac": round(ach / HBM_PEAK_GBS, 4),
+                        "traffic": MEASURED_TRAFFIC.get(dom["kind"]) if a.config == 2 else None,
+                        "kernel": f"k_gemv {dom['kind']} (target projections, m={k + 1})",
+                        "bytes_per_launch": round(dom["bytes"] / dom["launches"]),
+                        "us_per_launch": round(dom["us"] / dom["launches"], 3), "launches": dom["launches"]}
 
     prefill = measure_prefill(ctx, target, draft, prompt, first[0])
 

@@ -1,7 +1,7 @@
-"""The persistent draft forward: a greedy draft round of one sequence as one
-launch (Engine::propose, src/engine.rs:658-717; each round is
-Model::forward with Logits::Last, src/model.rs:269-362, then
-sampler::argmax, src/sampler.rs:42-51).
+"""The persistent forward: a greedy draft round, or the target's verify pass
+with its accept, of one sequence as one launch (Engine::propose and
+Engine::execute, src/engine.rs:563-717; each is Model::forward,
+src/model.rs:269-362, then sampler::argmax, src/sampler.rs:42-51).
 
 - A target drafting for itself accepts every proposal and emits its own
   greedy tokens (tests/engine.rs:134-160), for GQA groups of 1, 3 and 4, a
@@ -9,18 +9,20 @@ sampler::argmax, src/sampler.rs:42-51).
   the check that every draft argmax is right.
 - With a one-layer draft, every step (emitted ids, accepted count, the
   draft's progress) equals oracle.spec_step from the device's own state,
-  and the draft cache equals the oracle's after the steps.
+  and the caches equal the oracle's after the steps: bf16, int8 and int4
+  weights (the draft is the target's first layer, so both launches take
+  the same weight kind).
 - Tails of 3 and 4 rows (a draft that lags the target), across a 64-position
   span boundary: the same, from the same state.
-- The same generation with and without the persistent path (FERRO_PDRAFT=1
-  at context creation turns it on) emits the same ids with the same
-  acceptance; the two draft caches agree to 1e-5 of their largest entry and
-  are not bit-identical (the persistent path really ran).
-- A wait limit of one poll (FERRO_PDRAFT_SPIN=1) makes the launch time out:
+- The same generation with and without the persistent path (FERRO_PFWD=1 at
+  context creation turns it on) emits the same ids with the same
+  acceptance; the caches agree to 1e-5 of their largest entry and are not
+  bit-identical (the persistent path really ran).
+- A wait limit of one poll (FERRO_PFWD_SPIN=1) makes the launch time out:
   the step reports an error instead of results, and the next context works.
 
 The persistent path is opt-in: every context here that should take it is
-made with FERRO_PDRAFT=1.
+made with FERRO_PFWD=1.
 """
 import os
 
@@ -29,8 +31,8 @@ import pytest
 
 import oracle
 from ferrolm_amd import gpu, spec
-from ferrolm_amd.synth import random_model
-from ferrolm_amd.weights import Config
+from ferrolm_amd.synth import quantize_model, random_model
+from ferrolm_amd.weights import BF16, INT4, INT8, Config
 
 pytestmark = pytest.mark.gpu
 
@@ -47,7 +49,7 @@ K = 3
 
 
 def log(msg):
-    print(f"[pdraft] {msg}", flush=True)
+    print(f"[pfwd] {msg}", flush=True)
 
 
 def prompt_for(cfg, n, seed):
@@ -70,7 +72,7 @@ def context(**env):
 
 @pytest.fixture(scope="module")
 def pctx():
-    c = context(FERRO_PDRAFT="1")
+    c = context(FERRO_PFWD="1")
     yield c
     c.close()
 
@@ -86,11 +88,14 @@ def kv_close(gkv, okv, layers, tol=1e-4):
             assert np.abs(g - o).max() <= tol * max(1e-30, np.abs(o).max()), i
 
 
-@pytest.mark.parametrize("name", list(CFGS))
-def test_self_draft_accepts_every_proposal(pctx, name):
+@pytest.mark.parametrize("name,kind", [(n, BF16) for n in CFGS] + [("gqa3", INT8), ("gqa3", INT4)],
+                         ids=[*CFGS, "gqa3-int8", "gqa3-int4"])
+def test_self_draft_accepts_every_proposal(pctx, name, kind):
     ctx = pctx
     cfg = CFGS[name]
     hm = random_model(cfg, seed=11, std=0.05)
+    if kind != BF16:
+        hm = quantize_model(hm, kind)
     om = oracle.Model(hm)
     prompt = prompt_for(cfg, 50, 3)
     want, _, _ = oracle.generate(om, None, prompt, 60, 0, kv_blocks=64)
@@ -102,10 +107,13 @@ def test_self_draft_accepts_every_proposal(pctx, name):
     assert st.spec_steps > 0 and st.accepted == st.proposed
 
 
-def test_one_layer_draft_steps_match_oracle(pctx):
+@pytest.mark.parametrize("kind", [BF16, INT8, INT4], ids=["bf16", "int8", "int4"])
+def test_one_layer_draft_steps_match_oracle(pctx, kind):
     ctx = pctx
     cfg = CFGS["gqa3"]
     hm = random_model(cfg, seed=5, std=0.05)
+    if kind != BF16:
+        hm = quantize_model(hm, kind)
     tm = gpu.Model(ctx, hm)
     dm = tm.truncated(1)
     r = spec.Runner(ctx, tm, dm, prompt_for(cfg, 40, 9), K, kv_blocks=64)
@@ -126,9 +134,10 @@ def test_one_layer_draft_steps_match_oracle(pctx):
         assert r.stats.accepted_per_step[-1] == acc, step
         assert (r.computed, r.dcomp) == (comp, dcomp), step
         accepted += acc
-    log(f"one-layer draft: {accepted} of {24 * K} accepted, context {r.computed}")
-    assert 0 < accepted < 24 * K  # proposals both accepted and rejected
+    log(f"one-layer draft, kind {kind}: {accepted} of {24 * K} accepted, context {r.computed}")
+    assert accepted < 24 * K  # proposals rejected (acceptance: the self-draft tests)
     kv_close(r.dkv, odkv, 1)
+    kv_close(r.tkv, okv, cfg.layers)
 
 
 @pytest.mark.parametrize("rows", [3, 4])
@@ -164,14 +173,15 @@ def test_matches_kernel_path():
     hm = random_model(cfg, seed=8, std=0.05)
     prompt = prompt_for(cfg, 45, 6)
     runs = []
-    for env in ({"FERRO_PDRAFT": "1"}, {}):
+    for env in ({"FERRO_PFWD": "1"}, {}):
         c = context(**env)
         try:
             tm = gpu.Model(c, hm)
             r = spec.Runner(c, tm, tm.truncated(2), prompt, K, kv_blocks=64)
             while len(r.generated) < 40:
                 r.step()
-            runs.append((list(r.generated), list(r.stats.accepted_per_step), [r.dkv.layer(i) for i in range(2)]))
+            runs.append((list(r.generated), list(r.stats.accepted_per_step),
+                         [r.dkv.layer(i) for i in range(2)] + [r.tkv.layer(i) for i in range(cfg.layers)]))
         finally:
             c.close()
     (g1, a1, kv1), (g2, a2, kv2) = runs
@@ -188,7 +198,7 @@ def test_matches_kernel_path():
 def test_wait_timeout_is_reported():
     cfg = CFGS["gqa1"]
     hm = random_model(cfg, seed=2, std=0.05)
-    c = context(FERRO_PDRAFT="1", FERRO_PDRAFT_SPIN="1")
+    c = context(FERRO_PFWD="1", FERRO_PFWD_SPIN="1")
     try:
         tm = gpu.Model(c, hm)
         r = spec.Runner(c, tm, tm.truncated(1), prompt_for(cfg, 20, 1), K, kv_blocks=16)
@@ -197,7 +207,7 @@ def test_wait_timeout_is_reported():
             r.step()
     finally:
         c.close()
-    c = context(FERRO_PDRAFT="1")
+    c = context(FERRO_PFWD="1")
     try:
         tm = gpu.Model(c, hm)
         got = spec.generate(c, tm, tm.truncated(1), prompt_for(cfg, 20, 1), 8, K, kv_blocks=16)
