@@ -41,11 +41,12 @@ sys.path.insert(0, str(ROOT))
 
 METRIC = "accepted tok/s + verify-step µs, 1.7B int4-AWQ target + 135M draft, k=3, bs=1"
 HBM_PEAK_GBS = 8000.0
-# HBM bytes per launch of the target int4 decode GEMVs, measured with rocprofv3 --pmc
-# FETCH_SIZE and WRITE_SIZE and scaled by a plain copy of known size (--copy-calib);
-# profiles/gemv_int4_cfg2_pmc.md has the commands and the per-GEMV figures. It is a
-# measurement of the current kernels, re-taken whenever they change.
-MEASURED_TRAFFIC = {"int4": 14_920_806}
+# L2-to-memory bytes per launch of the target int4 decode GEMVs (class mean), counted by
+# request size with rocprofv3 --pmc (TCC_EA0_RDREQ_{32,64,128}B, TCC_EA0_WRREQ_64B; a
+# plain copy of known size reads back exactly); profiles/gemv_int4_cfg2_pmc.md has the
+# commands and the per-GEMV figures. A measurement of the current kernels, re-taken
+# whenever they change.
+MEASURED_TRAFFIC = {"int4": 11_230_224}
 
 
 def log(msg: str) -> None:
