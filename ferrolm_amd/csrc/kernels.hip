@@ -440,6 +440,8 @@ __global__ __launch_bounds__(64 * WMAX) void k_gemv(const GemvArgs a) {
     // chunks; passes past np re-read the last one and are masked out), so no
     // register carries a possibly pending load across iterations and nothing
     // waits before the first weights are requested.
+    // whether this lane's input row (row 4 pp + (lane % 16) / 4 of the A operand) is below m
+    auto lane_alive = [&](int pp) { return pp * 4 + ((lane & 15) >> 2) < a.m; };
     auto chunks = [&](int c, auto uu) {
         constexpr int UU = decltype(uu)::value;
         long aq[UU][4][PG];
@@ -456,7 +458,10 @@ __global__ __launch_bounds__(64 * WMAX) void k_gemv(const GemvArgs a) {
 #pragma unroll
                 for (int p = 0; p < PG; p++) {
                     const int pp = pass0 + (PG == 1 ? 0 : min(p, np - 1));
-                    const size_t idx = ((size_t)(kb + j) * a.p_total + pp) * 64 + lane;
+                    // lanes of input rows past m read row 4 pp's slot instead (the same
+                    // addresses as its lanes, so no extra bytes move; those output rows
+                    // are dropped): at one row, a quarter of the operand's bytes
+                    const size_t idx = ((size_t)(kb + j) * a.p_total + pp) * 64 + (lane_alive(pp) ? lane : (lane & ~12));
                     if (Q) {
                         aq[u][j][p] = ((const long*)a.XA)[idx];
                         sx[u][j][p] = a.XS[(size_t)(kb + j) * a.p_total * 4 + pp * 4 + (lane >> 4)];
