@@ -436,6 +436,7 @@ struct Plan {
     int ns = 1;  // attention sub-spans per work item (k_attn's NS)
     int Wc = 0;  // work items launched: W rounded up to 16, the extra records empty, so
                  // the launch shapes (and a captured step graph) last for 16 more spans
+    int maxq = 0;  // queries of the largest attention row group (rows x GQA group)
     // wrec: one 16-word record per attention work item (a span of one row
     // group): row0, nrows, crow0, cpos0 (first row and position of the
     // group's chunk), p0, p1 (the span), 0, 0, then the physical ids of the
@@ -481,6 +482,7 @@ static int build_plan(const fg_config& c, const fg_kv& kv, int max_pos, const Ch
             maxq = std::max(maxq, nr * group);
         }
     P.ns = w1 * c.kv_heads > 1024 && maxq >= kAttnMfmaQueries ? 128 / span1 : 1;
+    P.maxq = maxq;
     const int span = span1 * P.ns;
     // Long chunks at hd 64 and 128 take the flash items (rf rows each, split into
     // parts of at most kFlashPart positions: on the 1.7B shape's 1024-token
@@ -766,6 +768,7 @@ static int run_forward(fg_ctx* ctx, const fg_model* m, fg_kv* kv, const Plan& P,
     aa.btab = meta + P.o_btab;
     aa.part = w.apart;
     aa.n_wi = P.Wc;
+    aa.maxq = P.maxq;
     aa.ns = P.ns;
     aa.nh = nh;
     aa.nkv = nkv;
@@ -1636,7 +1639,7 @@ static int spec_step(fg_ctx* ctx, const fg_model* target, fg_kv* tkv, const fg_m
         for (int r = 0; r <= k; r++) {
             const Plan& P = plans[r];
             for (int64_t v : {(int64_t)P.t, (int64_t)P.S, (int64_t)P.Wc, (int64_t)P.words, (int64_t)P.ns,
-                              (int64_t)P.flash})
+                              (int64_t)P.flash, (int64_t)P.maxq})
                 sig.push_back(v);
         }
         for (auto& g : ctx->gsets)

@@ -166,6 +166,7 @@ struct AttnArgs {
     // n_wi counts the partial slots, two per part.
     int flash;
     const int32_t* btab;
+    int maxq = 0;  // queries of the largest row group (0: unknown, the full QM)
 };
 // Attention over the paged cache (RoPE, K/V write of the new rows), then the
 // split merge straight into the output projection's pieces (consumer_kind < 0:

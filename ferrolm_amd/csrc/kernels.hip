@@ -1347,20 +1347,26 @@ void launch_gemv(hipStream_t st, int epi, const DMat& w, const GemvArgs& a, hipE
 // is scored from LDS, and the softmax runs online across sub-spans: a
 // running max and sum per query, the weighted values rescaled by
 // exp(old max - new max) (flash-decoding within the work item).
-template <int HD, int P, int QM, int NS>
-__global__ __launch_bounds__(256, 2) void k_attn(AttnArgs a) {
+//
+// QM is the partials' query stride (the merge's layout); QL <= QM the queries an
+// item holds (its LDS and registers), chosen per launch from the plan's largest
+// row group so that small items leave room for more workgroups per CU. MINW:
+// waves per SIMD the launch bounds ask for (3 lets three items share a CU).
+template <int HD, int P, int QM, int NS, int QL = QM, int MINW = 2>
+__global__ __launch_bounds__(256, MINW) void k_attn(AttnArgs a) {
     constexpr int HALF = HD / 2;
     // rows padded by 4 floats (16-byte aligned): lanes reading one column of
     // consecutive rows (the MFMA operands) hit distinct banks
     __shared__ __align__(16) float ks[P][HD + 4];
     __shared__ __align__(16) float vs[P][HD + 4];
-    __shared__ __align__(16) float qs[QM][HD + 4];
-    __shared__ __align__(16) float pr[QM][P + 4];
-    __shared__ int lim[QM];
-    __shared__ float mrun[NS > 1 ? QM : 1], lrun[NS > 1 ? QM : 1], fac[NS > 1 ? QM : 1];
+    __shared__ __align__(16) float qs[QL][HD + 4];
+    __shared__ __align__(16) float pr[QL][P + 4];
+    __shared__ int lim[QL];
+    __shared__ float mrun[NS > 1 ? QL : 1], lrun[NS > 1 ? QL : 1], fac[NS > 1 ? QL : 1];
 
     static_assert(P <= 64 && P % 16 == 0 && 64 % P == 0, "a sub-span covers at most four cache blocks");
     static_assert(NS * P <= 128, "a work item covers at most the eight cache blocks of its record");
+    static_assert(QL <= QM && QL % 8 == 0, "an item's queries fit the partials' stride");
     // grid (kv head, work item): every real item is dispatched before the
     // launch's unused capacity slots, which exit at once
     const int h = blockIdx.x, wi = blockIdx.y;
@@ -1446,11 +1452,16 @@ __global__ __launch_bounds__(256, 2) void k_attn(AttnArgs a) {
     // D[4(l/16) + r][l%16] in register r of lane l) over 16 x 16 tiles, with
     // operands from LDS; fewer queries take the VALU loops. Rows of qs and pr
     // past Q hold stale values: they only reach output rows that are dropped.
-    const bool mf = Q >= kAttnMfmaQueries;
+    // items of several sub-spans exist only in launches whose largest row group
+    // has kAttnMfmaQueries queries: all of them take the MFMA path (rows past Q
+    // are dropped), so the VALU path's registers are not carried across sub-spans
+    const bool mf = NS > 1 || Q >= kAttnMfmaQueries;
     const int mtu = (Q + 15) >> 4;
     constexpr int NTD = HD / 16;
-    constexpr int TPW = ((QM + 15) / 16 * NTD + 3) / 4;  // weighted-value tiles per wave (MFMA)
-    constexpr int OI = (QM * HD + 255) / 256;            // weighted values per thread (VALU)
+    constexpr int TPW = ((QL + 15) / 16 * NTD + 3) / 4;  // weighted-value tiles per wave (MFMA)
+    constexpr int OI = (QL * HD + 255) / 256;            // weighted values per thread (VALU)
+    // MFMA rows past QL (a 16-row tile of fewer queries) read the last row and are dropped
+    auto qrow = [&](int r) { return min(r, QL - 1); };
     f32x4 oc[TPW];
     float ov[OI];
 #pragma unroll
@@ -1512,13 +1523,14 @@ __global__ __launch_bounds__(256, 2) void k_attn(AttnArgs a) {
             constexpr int NTP = P / 16;
             for (int ti = wave; ti < mtu * NTP; ti += 4) {
                 const int mt = ti / NTP, nt = ti % NTP, kk = lane >> 4;
-                const float* qa = &qs[mt * 16 + (lane & 15)][kk];
+                const float* qa = &qs[qrow(mt * 16 + (lane & 15))][kk];
                 const float* kb = &ks[nt * 16 + (lane & 15)][kk];
                 f32x4 c = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
                 for (int d0 = 0; d0 < HD; d0 += 4) c = __builtin_amdgcn_mfma_f32_16x16x4f32(qa[d0], kb[d0], c, 0, 0, 0);
 #pragma unroll
-                for (int r = 0; r < 4; r++) pr[mt * 16 + 4 * kk + r][nt * 16 + (lane & 15)] = c[r] * a.scale;
+                for (int r = 0; r < 4; r++)
+                    if (mt * 16 + 4 * kk + r < QL) pr[mt * 16 + 4 * kk + r][nt * 16 + (lane & 15)] = c[r] * a.scale;
             }
             __syncthreads();
         }
@@ -1577,9 +1589,9 @@ __global__ __launch_bounds__(256, 2) void k_attn(AttnArgs a) {
                     const int mt = ti / NTD, nd = ti % NTD, kk = lane >> 4;
                     if (NS > 1) {
 #pragma unroll
-                        for (int r = 0; r < 4; r++) oc[j][r] *= fac[mt * 16 + 4 * kk + r];
+                        for (int r = 0; r < 4; r++) oc[j][r] *= fac[qrow(mt * 16 + 4 * kk + r)];
                     }
-                    const float* pa = &pr[mt * 16 + (lane & 15)][kk];
+                    const float* pa = &pr[qrow(mt * 16 + (lane & 15))][kk];
                     const float* vb = &vs[kk][nd * 16 + (lane & 15)];
 #pragma unroll
                     for (int k0 = 0; k0 < P; k0 += 4)
@@ -1857,6 +1869,18 @@ __global__ __launch_bounds__(64) void k_merge_pieces(AttnArgs a, int m, void* __
     write_pieces<CK>(v, kb, pass, passes, row, piece, lane, out, xs);
 }
 
+template <int HD, int P, int QM, int QL, int MINW>
+static void attn_ns(hipStream_t st, const AttnArgs& a) {
+    if (a.ns >= 4 && 4 * P <= 128)
+        hipLaunchKernelGGL((k_attn<HD, P, QM, (4 * P <= 128 ? 4 : 1), QL, MINW>), dim3(a.nkv, a.n_wi), dim3(256), 0,
+                           st, a);
+    else if (a.ns >= 2 && 2 * P <= 128)
+        hipLaunchKernelGGL((k_attn<HD, P, QM, (2 * P <= 128 ? 2 : 1), QL, MINW>), dim3(a.nkv, a.n_wi), dim3(256), 0,
+                           st, a);
+    else
+        hipLaunchKernelGGL((k_attn<HD, P, QM, 1, QL, MINW>), dim3(a.nkv, a.n_wi), dim3(256), 0, st, a);
+}
+
 template <int HD, int P, int QM>
 static void attention_hd(hipStream_t st, const AttnArgs& a, int m, int ck, Pieces& out) {
     if constexpr ((HD == 64 || HD == 128) && QM == 32) {
@@ -1865,12 +1889,13 @@ static void attention_hd(hipStream_t st, const AttnArgs& a, int m, int ck, Piece
             goto merge;
         }
     }
-    if (a.ns >= 4 && 4 * P <= 128)
-        hipLaunchKernelGGL((k_attn<HD, P, QM, (4 * P <= 128 ? 4 : 1)>), dim3(a.nkv, a.n_wi), dim3(256), 0, st, a);
-    else if (a.ns >= 2 && 2 * P <= 128)
-        hipLaunchKernelGGL((k_attn<HD, P, QM, (2 * P <= 128 ? 2 : 1)>), dim3(a.nkv, a.n_wi), dim3(256), 0, st, a);
+    // items of at most 8 or 24 queries hold fewer (three workgroups per CU)
+    if (QM > 8 && a.maxq > 0 && a.maxq <= 8)
+        attn_ns<HD, P, QM, 8, 3>(st, a);
+    else if (QM > 24 && a.maxq > 0 && a.maxq <= 24)
+        attn_ns<HD, P, QM, 24, 3>(st, a);
     else
-        hipLaunchKernelGGL((k_attn<HD, P, QM, 1>), dim3(a.nkv, a.n_wi), dim3(256), 0, st, a);
+        attn_ns<HD, P, QM, QM, 2>(st, a);
 merge:
     if (ck < 0) return;  // the consumer merges the spans itself
     if (ck == BF16)
