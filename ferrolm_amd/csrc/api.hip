@@ -776,6 +776,12 @@ static int run_forward(fg_ctx* ctx, const fg_model* m, fg_kv* kv, const Plan& P,
     aa.bs = kv->block_size;
     aa.scale = 1.0f / sqrtf((float)hd);
 
+    // When every row's logits are selected, in order (draft rounds, verify
+    // steps), the last layer's down projection writes the lm_head's pieces of
+    // norm * x itself, the same product k_pieces forms, so that launch is saved.
+    const bool lm_mm = P.S > kGemvRows;
+    bool sel_all = P.S == t;
+    for (int i = 0; sel_all && i < P.S; i++) sel_all = P.sel[i] == i;
     int ss_cols = 32;  // columns per sum-of-squares partial in w.ss (the embedding writes one per k-block)
     for (int li = 0; li < L; li++) {
         const DLayer& l = m->layers[li];
@@ -861,6 +867,13 @@ static int run_forward(fg_ctx* ctx, const fg_model* m, fg_kv* kv, const Plan& P,
             g.pa_kind = ck(nl.wqkv);
             g.pa_passes = passes;
             g.pa_kb = nl.wqkv.kb;
+        } else if (sel_all) {
+            g.g_next = m->norm;
+            g.pa = w.pa[cur ^ 1];
+            g.pxs = w.pxs[cur ^ 1];
+            g.pa_kind = lm_mm ? (int)MM : kind_of(m->lm_head);
+            g.pa_passes = w.lm_passes;
+            g.pa_kb = m->lm_head.kb;
         }
         g.nt = narrow_nt(l.w_down, g.pa && (g.pa_kind == INT8 || g.pa_kind == INT4));
         g.mm = mm;
@@ -879,8 +892,8 @@ static int run_forward(fg_ctx* ctx, const fg_model* m, fg_kv* kv, const Plan& P,
     // final norm of the selected rows (weight now, 1/rms in the epilogue), lm_head, argmax
     const int32_t* sel = meta + P.o_sel;
     Pieces pl = pieces(w, cur, m->lm_head.kb, w.lm_passes);
-    const bool lm_mm = P.S > kGemvRows;
-    launch_pieces(st, lm_mm ? (int)MM : kind_of(m->lm_head), w.x, H, P.S, H, m->norm, sel, pl);
+    if (!(sel_all && L > 0))
+        launch_pieces(st, lm_mm ? (int)MM : kind_of(m->lm_head), w.x, H, P.S, H, m->norm, sel, pl);
     GemvArgs g = gemv_args(m->lm_head, pl, P.S, w);
     g.mm = lm_mm;
     g.ss_in = w.ss;
