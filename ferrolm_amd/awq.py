@@ -45,6 +45,73 @@ Search = Callable[[int, np.ndarray, np.ndarray], tuple]
 Apply = Callable[[int, np.ndarray, np.ndarray, np.ndarray], Matrix]
 
 
+def xorshift64(v: int) -> int:
+    """Marsaglia's xorshift64 step with shifts (13, 7, 17), as Model::record
+    advances its generator (src/model.rs:383-385)."""
+    m = (1 << 64) - 1
+    v ^= (v << 13) & m
+    v ^= v >> 7
+    v ^= (v << 17) & m
+    return v
+
+
+class Reservoir:
+    """Model::record's sample (src/model.rs:56-70, 364-392): up to max_rows
+    rows per (layer, projection), a uniform reservoir over every row seen.
+    One xorshift generator (13, 7, 17; seeded 0x9E3779B97F4A7C15) is shared
+    by every layer and projection and advanced once per row past the first
+    max_rows, so rows must arrive in the reference's order: per forward,
+    layer by layer, qkv, o, gate_up, down, tokens in chunk order."""
+
+    def __init__(self, layers: int, max_rows: int):
+        self.max_rows = max_rows
+        self.rng = 0x9E3779B97F4A7C15
+        self.rows = [[[] for _ in range(4)] for _ in range(layers)]
+        self.seen = [[0] * 4 for _ in range(layers)]
+
+    def record(self, layer: int, which: int, x: np.ndarray) -> None:
+        kept, mx = self.rows[layer][which], self.max_rows
+        for r in np.asarray(x, np.float32):
+            n = self.seen[layer][which]
+            self.seen[layer][which] += 1
+            if n < mx:
+                kept.append(r.copy())
+                continue
+            self.rng = xorshift64(self.rng)
+            j = self.rng % (n + 1)
+            if j < mx:
+                kept[j] = r.copy()
+
+    def result(self) -> list:
+        """Per layer the four row sets as float32 [rows, width] arrays."""
+        return [[np.stack(rows).astype(np.float32) if rows else np.zeros((0, 0), np.float32) for rows in l]
+                for l in self.rows]
+
+
+def calibrate(ctx, model, seqs, max_rows: int) -> list:
+    """Model::calibrate (src/awq.rs:38-62) on the device: each sequence's
+    forward from position 0 in a fresh cache of its own 16-token blocks,
+    with the four projection inputs of every layer captured on the device
+    (fg_forward_capture) and sampled by Model::record's reservoir. Returns
+    calib[layer][which] for quantize_awq."""
+    from . import gpu
+
+    c = model.cfg
+    res = Reservoir(c.layers, max_rows)
+    for s in seqs:
+        s = np.ascontiguousarray(s, np.uint32)
+        nb = (len(s) + 15) // 16
+        kv = gpu.KvCache(ctx, c, max(nb, 1), 16)
+        try:
+            taps = gpu.forward_capture(ctx, model, kv, [(s, 0, np.arange(nb, dtype=np.uint32))])
+        finally:
+            kv.close()
+        for li in range(c.layers):
+            for which in range(4):
+                res.record(li, which, taps[li][which])
+    return res.result()
+
+
 def device(ctx) -> tuple[Search, Apply]:
     """The device's search and apply (fg_awq_search, fg_quantize) on ctx."""
     from . import gpu

@@ -735,7 +735,8 @@ static GemvArgs gemv_args(const DMat& d, const Pieces& in, int m, const Work& w)
 // and the hidden-state taps to host.
 static int run_forward(fg_ctx* ctx, const fg_model* m, fg_kv* kv, const Plan& P, const int32_t* meta,
                        const uint32_t* tok_dev, int tok_stride, Work& w, float* logits_dev, uint32_t* am_out,
-                       uint32_t* aux, int aux_stride, int aux_off, float* hidden_host) {
+                       uint32_t* aux, int aux_stride, int aux_off, float* hidden_host,
+                       float* cap = nullptr) {
     const fg_config& c = m->cfg;
     hipStream_t st = ctx->stream;
     const int t = P.t, H = c.hidden, hd = c.head_dim, nh = c.heads, nkv = c.kv_heads;
@@ -783,8 +784,13 @@ static int run_forward(fg_ctx* ctx, const fg_model* m, fg_kv* kv, const Plan& P,
     bool sel_all = P.S == t;
     for (int i = 0; sel_all && i < P.S; i++) sel_all = P.sel[i] == i;
     int ss_cols = 32;  // columns per sum-of-squares partial in w.ss (the embedding writes one per k-block)
+    // calibration capture: per layer the four projection inputs [t][H], [t][qd], [t][H], [t][inter]
+    const int qd = nh * hd;
+    const size_t cap_layer = (size_t)t * (2 * H + qd + c.intermediate);
     for (int li = 0; li < L; li++) {
         const DLayer& l = m->layers[li];
+        float* capl = cap ? cap + li * cap_layer : nullptr;
+        if (cap) launch_cap_norm(st, w.x, t, H, l.attn_norm, c.rms_eps, capl, H);
         // q/k/v of the normed rows: rinv from the sum-of-squares partials
         GemvArgs g = gemv_args(l.wqkv, pieces(w, cur, l.wqkv.kb, passes), t, w);
         g.out = w.qkv;
@@ -804,6 +810,8 @@ static int run_forward(fg_ctx* ctx, const fg_model* m, fg_kv* kv, const Plan& P,
         Pieces po = pieces(w, cur ^ 1, l.wo.kb, passes);
         const bool am = ctx->merge_in_o && merge_in_o(c, P, l.wo, mm);
         if (launch_attention(st, aa, t, am ? -1 : ck(l.wo), po))
+            return fail(FG_E_SHAPE, "no attention kernel for head_dim " + std::to_string(hd));
+        if (cap && launch_cap_merge(st, aa, t, capl + (size_t)t * H, qd))
             return fail(FG_E_SHAPE, "no attention kernel for head_dim " + std::to_string(hd));
         cur ^= 1;
         // o projection + residual; pieces of mlp_norm * x for gate/up
@@ -836,6 +844,7 @@ static int run_forward(fg_ctx* ctx, const fg_model* m, fg_kv* kv, const Plan& P,
         }
         ss_cols = mm ? 64 : 16 * g.nt;
         gemv(ctx, EPI_RESID, l.wo, g);
+        if (cap) launch_cap_norm(st, w.x, t, H, l.mlp_norm, c.rms_eps, capl + (size_t)t * (H + qd), H);
         cur ^= 1;
         // gate/up with SiLU; pieces of the activation for down
         g = gemv_args(l.w_gate_up, pieces(w, cur, l.w_gate_up.kb, passes), t, w);
@@ -851,6 +860,10 @@ static int run_forward(fg_ctx* ctx, const fg_model* m, fg_kv* kv, const Plan& P,
         g.pa_kb = l.w_down.kb;
         g.il = l.w_gate_up.il;
         g.mm = mm;
+        if (cap) {
+            g.cap = capl + (size_t)t * (2 * H + qd);
+            g.ldcap = c.intermediate;
+        }
         gemv(ctx, EPI_SILU, l.w_gate_up, g);
         cur ^= 1;
         // down projection + residual; pieces of the next layer's attn_norm * x
@@ -1207,6 +1220,50 @@ int fg_forward(fg_ctx* ctx, const fg_model* m, fg_kv* kv, const fg_chunk* chunks
         HIPCHK(hipMemcpyAsync(argmax_out, w.am, (size_t)P.S * 4, hipMemcpyDeviceToHost, ctx->stream));
     HIPCHK(hipStreamSynchronize(ctx->stream));
     return 0;
+}
+
+int fg_forward_capture(fg_ctx* ctx, const fg_model* m, fg_kv* kv, const fg_chunk* chunks, int32_t n_chunks,
+                       float* inputs_out) {
+    if (!ctx || !m || !kv || !inputs_out || (!chunks && n_chunks > 0) || n_chunks < 0)
+        return fail(FG_E_ARG, "null argument");
+    int rc = check_model_kv(m, kv);
+    if (rc) return rc;
+    HIPCHK(hipSetDevice(ctx->device));
+    std::vector<ChunkIn> in(n_chunks);
+    for (int i = 0; i < n_chunks; i++) {
+        if (chunks[i].n > 0 && !chunks[i].tokens) return fail(FG_E_ARG, "chunk without tokens");
+        // only the projection inputs are wanted: no logits rows (Logits::None)
+        in[i] = ChunkIn{chunks[i].tokens, chunks[i].n, chunks[i].pos, chunks[i].blocks, chunks[i].n_blocks,
+                        FG_LOGITS_NONE};
+    }
+    Plan P;
+    if ((rc = build_plan(m->cfg, *kv, m->max_pos, in.data(), n_chunks, P))) return rc;
+    if (P.t == 0 || m->layers.empty()) return 0;
+    const fg_config& c = m->cfg;
+    const size_t floats =
+        m->layers.size() * (size_t)P.t * (2 * (size_t)c.hidden + (size_t)c.heads * c.head_dim + c.intermediate);
+    if ((rc = ensure(&ctx->hmeta, &ctx->hmeta_cap, P.words * 4, ctx->stream, true))) return rc;
+    if ((rc = ensure(&ctx->dmeta, &ctx->dmeta_cap, P.words * 4, ctx->stream, false))) return rc;
+    pack_plan(P, (int32_t*)ctx->hmeta);
+    HIPCHK(hipMemcpyAsync(ctx->dmeta, ctx->hmeta, P.words * 4, hipMemcpyHostToDevice, ctx->stream));
+    Work w{};
+    const size_t need = layout_work(m, P, w, nullptr);
+    if ((rc = ensure(&ctx->ws, &ctx->ws_cap, need, ctx->stream, false))) return rc;
+    layout_work(m, P, w, ctx->ws);
+    float* cap = nullptr;
+    if (hipMalloc((void**)&cap, floats * 4) != hipSuccess) {
+        (void)hipGetLastError();
+        return fail(FG_E_NOMEM, "capture buffer of " + std::to_string(floats * 4) + " bytes");
+    }
+    const int32_t* meta = (const int32_t*)ctx->dmeta;
+    rc = run_forward(ctx, m, kv, P, meta, (const uint32_t*)(meta + P.o_tok), 1, w, nullptr, nullptr, nullptr, 0, 0,
+                     nullptr, cap);
+    if (!rc && hipMemcpyAsync(inputs_out, cap, floats * 4, hipMemcpyDeviceToHost, ctx->stream) != hipSuccess)
+        rc = fail(FG_E_DEVICE, "capture copy");
+    if (!rc && hipStreamSynchronize(ctx->stream) != hipSuccess) rc = fail(FG_E_DEVICE, "capture synchronize");
+    (void)hipStreamSynchronize(ctx->stream);
+    (void)hipFree(cap);
+    return rc;
 }
 
 // Distributions of rows carved from the context's sampling buffer starting at

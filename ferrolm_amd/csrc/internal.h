@@ -111,6 +111,10 @@ struct GemvArgs {
     void* pa = nullptr;             // next consumer's pieces (nullptr: none)
     float* pxs = nullptr;
     int pa_kind = 0, pa_passes = 0, pa_kb = 0;  // pa_kb: the consumer's padded k-blocks
+    // SILU: the activation rows also go out in f32 ([m][ldcap], nullptr: not);
+    // the calibration capture of the down projection's input
+    float* cap = nullptr;
+    int ldcap = 0;
     // ARGMAX
     float* logits = nullptr;
     float2* best = nullptr;
@@ -173,6 +177,10 @@ struct AttnArgs {
 // no merge, the output projection merges the spans itself). Returns -1, and
 // launches nothing, for a head dim without a kernel instance (16, 32, 64, 128).
 int launch_attention(hipStream_t st, const AttnArgs& a, int m, int consumer_kind, Pieces& out);
+// Calibration capture: rms_norm(x) * g of m residual rows into out [m][ldo], and
+// the attention output (the spans of launch_attention merged) into out [m][ldo].
+void launch_cap_norm(hipStream_t st, const float* x, int m, int H, const float* g, float eps, float* out, int ldo);
+int launch_cap_merge(hipStream_t st, const AttnArgs& a, int m, float* out, int ldo);
 
 void launch_argmax_final(hipStream_t st, const float2* best, int tiles, int rows, uint32_t* argmax_out,
                          uint32_t* aux, int aux_stride, int aux_off);

@@ -751,7 +751,9 @@ __global__ __launch_bounds__(64 * WMAX) void k_gemv(const GemvArgs a) {
             vt[r * YS + cc] = a.g_next ? gs[cc] * xn : xn;
         } else {
             const float gt = yt[r * YS + cc] * rs[r], up = yt[r * YS + OC + cc] * rs[r];
-            vt[r * YS + cc] = live ? gt / (1.0f + dev_exp(-gt)) * up : 0.0f;
+            const float v = live ? gt / (1.0f + dev_exp(-gt)) * up : 0.0f;
+            vt[r * YS + cc] = v;
+            if (a.cap && live) a.cap[(size_t)row * a.ldcap + blockIdx.x * OC + cc] = v;
         }
     }
     __syncthreads();
@@ -915,7 +917,9 @@ __device__ void gemm_epilogue(const GemvArgs& a, float* yt, float* part, float* 
             // channel cc: block b of the [gate il, up il] interleave, position j in it
             const int b = cc / a.il, j = cc % a.il;
             const float gt = yt[rr * YS + b * 2 * a.il + j] * rs[rr], up = yt[rr * YS + b * 2 * a.il + a.il + j] * rs[rr];
-            vt[rr * YS + cc] = live ? gt / (1.0f + dev_exp(-gt)) * up : 0.0f;
+            const float v = live ? gt / (1.0f + dev_exp(-gt)) * up : 0.0f;
+            vt[rr * YS + cc] = v;
+            if (a.cap && live) a.cap[(size_t)row * a.ldcap + tile * 32 + cc] = v;
         }
     }
     __syncthreads();
@@ -1911,6 +1915,61 @@ merge:
 
 int attn_span(int hd) { return hd >= 128 ? 32 : 64; }
 int attn_qmax(int hd) { return hd >= 64 ? 32 : 64; }
+
+// ---------------------------------------------------------------------------
+// Calibration capture (Model::record's inputs, src/model.rs:312-333): the f32
+// rows a layer's projections take, for the AWQ search. Not on the decode path.
+// ---------------------------------------------------------------------------
+
+// rms_norm (src/kernels.rs:597-607) of residual rows: dot's eight lanes, each an
+// fma chain over every eighth input in order, summed as hsum8 sums them
+// (src/kernels.rs:191-213), then r = 1 / sqrt(ms + eps) and g * (x * r). One
+// wave per row.
+__global__ __launch_bounds__(64) void k_cap_norm(const float* __restrict__ x, int H, const float* __restrict__ g,
+                                                 float eps, float* __restrict__ out, int ldo) {
+    const int row = blockIdx.x, lane = threadIdx.x;
+    const float* xr = x + (size_t)row * H;
+    float acc = 0.0f;
+    if (lane < 8)
+        for (int i = lane; i < H; i += 8) acc = fmaf(xr[i], xr[i], acc);
+    float l[8];
+#pragma unroll
+    for (int j = 0; j < 8; j++) l[j] = __shfl(acc, j);
+    const float ss = ((l[0] + l[4]) + (l[2] + l[6])) + ((l[1] + l[5]) + (l[3] + l[7]));
+    const float r = 1.0f / sqrtf(ss / (float)H + eps);
+    for (int i = lane; i < H; i += 64) out[(size_t)row * ldo + i] = g[i] * (xr[i] * r);
+}
+
+// The attention output rows in f32: k_merge_pieces' geometry and arithmetic
+// (the same bits it splits into pieces), one lane of four writing each value.
+template <int HD, int QM>
+__global__ __launch_bounds__(64) void k_cap_merge(AttnArgs a, int m, float* __restrict__ out, int ldo) {
+    const int kb = blockIdx.x, pass = blockIdx.y, lane = threadIdx.x;
+    const int c = lane & 15, row = pass * 4 + (c >> 2), piece = c & 3;
+    const int k0 = kb * 32 + (lane >> 4) * 8;
+    if (row >= m || k0 >= a.nh * HD) return;
+    float v[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    merge_spans<8>(a.part, *(const int4*)(a.mrec + (size_t)row * 4), a.nh, a.nkv, HD, QM, k0, piece, v);
+    if (piece == 0)
+#pragma unroll
+        for (int s = 0; s < 8; s++) out[(size_t)row * ldo + k0 + s] = v[s];
+}
+
+void launch_cap_norm(hipStream_t st, const float* x, int m, int H, const float* g, float eps, float* out, int ldo) {
+    if (m > 0) hipLaunchKernelGGL(k_cap_norm, dim3(m), dim3(64), 0, st, x, H, g, eps, out, ldo);
+}
+
+int launch_cap_merge(hipStream_t st, const AttnArgs& a, int m, float* out, int ldo) {
+    if (m <= 0 || a.n_wi <= 0) return 0;
+    const dim3 grid((a.nh * a.hd + 31) / 32, (m + 3) / 4);
+    switch (a.hd) {
+        case 16: hipLaunchKernelGGL((k_cap_merge<16, 64>), grid, dim3(64), 0, st, a, m, out, ldo); return 0;
+        case 32: hipLaunchKernelGGL((k_cap_merge<32, 64>), grid, dim3(64), 0, st, a, m, out, ldo); return 0;
+        case 64: hipLaunchKernelGGL((k_cap_merge<64, 32>), grid, dim3(64), 0, st, a, m, out, ldo); return 0;
+        case 128: hipLaunchKernelGGL((k_cap_merge<128, 32>), grid, dim3(64), 0, st, a, m, out, ldo); return 0;
+        default: return -1;
+    }
+}
 
 int launch_attention(hipStream_t st, const AttnArgs& a, int m, int consumer_kind, Pieces& out) {
     if (m <= 0 || a.n_wi <= 0) return 0;

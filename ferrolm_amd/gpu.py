@@ -108,6 +108,7 @@ EXPORTS = {
     "fg_kv_write": (C.c_int, [C.c_void_p, C.c_void_p, C.c_int32, f32p, f32p]),
     "fg_forward": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.POINTER(FgChunk), C.c_int32, f32p, u32p, i32p,
                              f32p]),
+    "fg_forward_capture": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.POINTER(FgChunk), C.c_int32, f32p]),
     "fg_spec_step": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.POINTER(FgSpecSeq),
                                C.c_int32, C.c_int32, u32p, i32p, i32p]),
     "fg_spec_step_sampled": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p,
@@ -343,6 +344,35 @@ def forward(ctx: Context, model: Model, kv: KvCache, chunks, logits: bool = True
                            ptr(hid, f32p)))
     assert nrows.value == rows
     return ForwardOut(lg, am, hid)
+
+
+def forward_capture(ctx: Context, model: Model, kv: KvCache, chunks) -> list:
+    """Model::forward with Model::record's taps (src/model.rs:312-333) on the
+    device (fg_forward_capture). chunks: (tokens, pos, blocks). Returns per
+    layer the four projection inputs [qkv, o, gate_up, down] of every token
+    in chunk order, as float32 arrays [tokens, width]."""
+    c = model.cfg
+    arr = (FgChunk * max(1, len(chunks)))()
+    keep = []
+    t = 0
+    for i, (tok, pos, blocks) in enumerate(chunks):
+        tok = np.ascontiguousarray(tok, dtype=np.uint32)
+        blocks = np.ascontiguousarray(blocks, dtype=np.uint32)
+        keep += [tok, blocks]
+        arr[i] = FgChunk(ptr(tok, u32p), len(tok), pos, ptr(blocks, u32p), len(blocks), LOGITS_NONE)
+        t += len(tok)
+    widths = (c.hidden, c.heads * c.head_dim, c.hidden, c.intermediate)
+    out = np.zeros((c.layers, t * sum(widths)), np.float32)
+    if t and c.layers:
+        check(lib().fg_forward_capture(ctx.h, model.h, kv.h, arr, len(chunks), ptr(out, f32p)))
+    layers = []
+    for li in range(c.layers):
+        o, four = 0, []
+        for w in widths:
+            four.append(out[li, o:o + t * w].reshape(t, w))
+            o += t * w
+        layers.append(four)
+    return layers
 
 
 @dataclass

@@ -180,6 +180,20 @@ int fg_forward(fg_ctx* ctx, const fg_model* m, fg_kv* kv,
                const fg_chunk* chunks, int32_t n_chunks, float* logits_out,
                uint32_t* argmax_out, int32_t* rows_out, float* hidden_out);
 
+/* The capture of Model::calibrate (src/awq.rs:38-62): Model::forward with
+ * Model::record's taps (src/model.rs:312-333). Runs the chunks like
+ * fg_forward (no logits rows, whatever their mode) and writes the f32
+ * inputs of every layer's four projections, tokens in chunk order, layer
+ * after layer: [qkv: tokens x hidden = rms_norm(x, attn_norm)]
+ * [o: tokens x heads*head_dim = attention output]
+ * [gate_up: tokens x hidden = rms_norm(x, mlp_norm)]
+ * [down: tokens x intermediate = silu(gate) * up]. Model::record's
+ * reservoir sampling runs on the host over these rows. Allocates a device
+ * buffer of the output's size for the call (FG_E_NOMEM when it cannot). */
+int fg_forward_capture(fg_ctx* ctx, const fg_model* m, fg_kv* kv,
+                       const fg_chunk* chunks, int32_t n_chunks,
+                       float* inputs_out);
+
 /* ---- speculative step ------------------------------------------------- */
 /* One greedy speculative step for n_seqs sequences, entirely on device:
  * Engine::propose's k draft rounds (src/engine.rs:658-717), the target's

@@ -155,3 +155,37 @@ def test_quantized_model_round_trips_through_its_file(tmp_path, fixture):
             assert (a.bqkv is None) == (b.bqkv is None)
         lo = [oracle.Model(m).forward(oracle.Model(m).kv(3), [(toks, 0, [0, 1, 2], 2)]) for m in (back, model)]
         assert np.array_equal(lo[0], lo[1])
+
+
+def test_reservoir_generator_known_answers():
+    """Model::record's generator is Marsaglia's xorshift64 (13, 7, 17): the
+    first three outputs from his example seed 88172645463325252, as printed
+    in "Xorshift RNGs" (J. Stat. Softw. 8(14), 2003)."""
+    v, out = 88172645463325252, []
+    for _ in range(3):
+        v = awq.xorshift64(v)
+        out.append(v)
+    assert out == [8748534153485358512, 3040900993826735515, 3453997556048239312]
+
+
+def test_host_reservoir_keeps_the_rows_model_record_keeps():
+    """The product's reservoir (awq.Reservoir, fed per forward as the device
+    capture delivers rows) keeps the same rows in the same slots as the
+    oracle's Model::calibrate, for a stream that overflows max_rows many
+    times (8 x 64 rows into 24) and one that fits."""
+    hm = load_model(GOLDEN / "llama-gqa")
+    om = oracle.Model(hm)
+    seqs = [reference_tokens(64, 10 + i) for i in range(8)]
+    for max_rows in (24, 600):
+        want = oracle.calibrate(om, seqs, max_rows)
+        res = awq.Reservoir(hm.cfg.layers, max_rows)
+        for s in seqs:
+            kv = om.kv(4)
+            _, taps = om.forward(kv, [(s, 0, list(range(4)), 0)], taps=True)
+            for li in range(hm.cfg.layers):
+                for which in range(4):
+                    res.record(li, which, taps[li][which])
+        got = res.result()
+        for gl, wl in zip(got, want):
+            for g, w in zip(gl, wl):
+                assert g.shape == w.shape and np.array_equal(g, w)

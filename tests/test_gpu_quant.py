@@ -112,3 +112,62 @@ def test_device_awq_search_rejects_bad_arguments(ctx):
         np.float32))
     assert (alpha, ep, ea) == (0.0, 0.0, 0.0)
     assert not m.s.any() and np.all(m.q == 0x88)
+
+
+def _captures_close(dev, ora, tol=1e-4):
+    """Same rows in the same slots (the reservoir draws depend only on the
+    row counts), values within tol of the oracle's, row by row (relative L2;
+    the residual stream's own bar in the forward tests)."""
+    assert len(dev) == len(ora)
+    for li, (dl, ol) in enumerate(zip(dev, ora)):
+        for which, (d, o) in enumerate(zip(dl, ol)):
+            assert d.shape == o.shape, (li, which, d.shape, o.shape)
+            if d.size:
+                rel = np.linalg.norm(d - o, axis=-1) / np.maximum(np.linalg.norm(o, axis=-1), 1e-30)
+                assert rel.max() < tol, (li, which, float(rel.max()))
+
+
+def test_device_calibration_matches_model_calibrate(ctx):
+    """Model::calibrate (src/awq.rs:38-62) with the capture on the device
+    (fg_forward_capture: the norms of the residual rows, the merged attention
+    output and the SwiGLU activation of the gate/up epilogue) and the host
+    reservoir, against the oracle's: sequences of 1 to 64 tokens (decode-sized
+    GEMV steps, the bf16 merge-in-projection path at up to 4 rows), a stream
+    that overflows the reservoir and one that fits. The device's rows then
+    drive the AWQ search on the device, bit-equal to the oracle's search on
+    the same rows: calibration, search and quantization end to end without
+    the checker."""
+    hm = load_model(GOLDEN / "llama-gqa")
+    om = oracle.Model(hm)
+    m = gpu.Model(ctx, hm)
+    seqs = [reference_tokens(n, 30 + i) for i, n in enumerate((64, 3, 37, 64, 1, 64, 20, 64))]
+    for max_rows in (256, 40):
+        dev = awq.calibrate(ctx, m, seqs, max_rows)
+        _captures_close(dev, oracle.calibrate(om, seqs, max_rows))
+    qm, choices = awq.quantize_awq(hm, INT4, dev, *awq.device(ctx))
+    oqm, ochoices = awq.quantize_awq(hm, INT4, dev, *oracle_awq())
+    assert [(x.alpha, x.error_plain, x.error_awq) for x in choices] == \
+        [(x.alpha, x.error_plain, x.error_awq) for x in ochoices]
+    for a, b in zip(qm.layers, oqm.layers):
+        for name in ("wqkv", "wo", "w_gate_up", "w_down"):
+            assert np.array_equal(getattr(a, name).q, getattr(b, name).q)
+            assert np.array_equal(getattr(a, name).s, getattr(b, name).s)
+
+
+@pytest.mark.parametrize("kind", [0, INT8, INT4], ids=["bf16", "int8", "int4"])
+def test_device_calibration_on_the_gemm_path(ctx, kind):
+    """A 1024-wide model: 40- and 1024-token sequences run every projection
+    as the MFMA GEMM (the SwiGLU capture in the GEMM epilogue, with split K),
+    the 1024-token one with the flash prefill attention's partials; the
+    captured rows against the oracle's."""
+    from ferrolm_amd.synth import random_model
+    from ferrolm_amd.weights import Config
+    cfg = Config(vocab=1024, hidden=1024, intermediate=2048, layers=2, heads=16, kv_heads=4, head_dim=64,
+                 rms_eps=1e-5, max_position=2048)
+    hm = random_model(cfg, seed=41, std=0.03)
+    if kind:
+        hm = plain_quantized(hm, kind, lambda k, w: gpu.quantize(ctx, k, w))
+    rng = np.random.default_rng(42)
+    seqs = [[int(x) for x in rng.integers(3, 1000, n)] for n in (40, 1024)]
+    dev = awq.calibrate(ctx, gpu.Model(ctx, hm), seqs, 2048)
+    _captures_close(dev, oracle.calibrate(oracle.Model(hm), seqs, 2048))
