@@ -632,6 +632,12 @@ static constexpr int kGemvRows = 15;
 static constexpr int kGemvSplitGroups = 1024;  // output groups a split-K GEMV may have (counters per context)
 static constexpr int kGemmMinHidden = 1024;
 static constexpr int kNarrowGemmRows = 256;
+// Floats of the GEMM split-K partial tiles ([split][row][column]) in a plan's
+// workspace: 32 MiB. At 4 MiB the split of the 80-row products into 4096
+// outputs stopped at two (80 x 4096 x 4 floats do not fit); four splits take
+// the 4096 x 14336 int4 down from 56.4 to 38.7 us and the 4096 x 4096 o from
+// 24.9 to 19.7 us (single-matrix products, event-timed).
+static constexpr size_t kKpartFloats = (size_t)1 << 23;
 static bool step_gemm(int t, int H) { return t > kGemvRows && (H >= kGemmMinHidden || t >= kNarrowGemmRows); }
 
 // n-tiles per workgroup of a bf16 projection with fewer than 256 tiles: one, so
@@ -696,7 +702,7 @@ static size_t layout_work(const fg_model* m, const Plan& P, Work& w, void* base)
     w.best = cv.take<float2>((size_t)(c.vocab / 32) * S);
     w.am = cv.take<uint32_t>(S);
     // the split rule keeps splits x rows x N within 64 x 256 x 64 floats
-    w.kpart_cap = step_gemm(t, H) || S > kGemvRows ? (size_t)1 << 20 : 0;
+    w.kpart_cap = step_gemm(t, H) || S > kGemvRows ? kKpartFloats : 0;
     w.kpart = w.kpart_cap ? cv.take<float>(w.kpart_cap) : nullptr;
     // GEMV split K: [group][split][16 rows][group columns] over the hidden columns
     w.gpart = w.passes == 1 ? cv.take<float>((size_t)kGemvSplitMax * 16 * H) : nullptr;
@@ -1948,7 +1954,7 @@ static size_t layout_mat(const DMat& d, int m, Pieces& p, float** xbuf, float** 
     *xbuf = cv.take<float>((size_t)m * d.cols);
     *ybuf = cv.take<float>((size_t)m * d.rows);
     *bbuf = cv.take<float>((size_t)d.rows);
-    w.kpart_cap = m > kGemvRows ? (size_t)1 << 20 : 0;
+    w.kpart_cap = m > kGemvRows ? kKpartFloats : 0;
     w.kpart = w.kpart_cap ? cv.take<float>(w.kpart_cap) : nullptr;
     return cv.off + 256;
 }
