@@ -1536,13 +1536,25 @@ static void pf_launch(fg_ctx* ctx, const fg_model* m, int si, fg_kv* kv, int t, 
     launch_pfwd(ctx->stream, m->pf_kind, ctx->pf_groups, a);
 }
 
+// chunks (n_chunks, greedy only): other sequences' prefill chunks and plain
+// rows, carried by the verify forward after the verify rows (Engine::execute's
+// one target pass); chunk_am gets the argmax of their FG_LOGITS_LAST rows.
 static int spec_step(fg_ctx* ctx, const fg_model* target, fg_kv* tkv, const fg_model* draft, fg_kv* dkv,
                      const fg_spec_seq* seqs, int32_t n_seqs, int32_t k, const fg_sampling* params, uint64_t* rng,
-                     uint32_t* out_tokens, int32_t* out_count, int32_t* out_accepted) {
+                     uint32_t* out_tokens, int32_t* out_count, int32_t* out_accepted, const fg_chunk* chunks = nullptr,
+                     int32_t n_chunks = 0, uint32_t* chunk_am = nullptr) {
     if (!ctx || !target || !tkv || !draft || !dkv || !seqs || n_seqs <= 0 || k <= 0 || !out_tokens || !out_count ||
-        !out_accepted || (params && !rng))
+        !out_accepted || (params && !rng) || n_chunks < 0 || (n_chunks > 0 && !chunks))
         return fail(FG_E_ARG, "bad argument");
     const bool sampling = params != nullptr;
+    if (sampling && n_chunks > 0) return fail(FG_E_ARG, "chunks ride only with greedy steps");
+    int c_last = 0;  // FG_LOGITS_LAST rows of the chunks
+    for (int c = 0; c < n_chunks; c++) {
+        if (chunks[c].n > 0 && !chunks[c].tokens) return fail(FG_E_ARG, "chunk without tokens");
+        if (chunks[c].logits == FG_LOGITS_ALL) return fail(FG_E_ARG, "chunks take FG_LOGITS_NONE or FG_LOGITS_LAST");
+        c_last += chunks[c].logits == FG_LOGITS_LAST && chunks[c].n > 0;
+    }
+    if (c_last > 0 && !chunk_am) return fail(FG_E_ARG, "bad argument");
     bool wide = false;  // a sampled sequence with top_k 0 or above kSampleCap
     for (int i = 0; sampling && i < n_seqs; i++) wide |= sample_wide(*(const SampleParams*)&params[i]);
     if (wide && draft->cfg.vocab != target->cfg.vocab)
@@ -1568,9 +1580,16 @@ static int spec_step(fg_ctx* ctx, const fg_model* target, fg_kv* tkv, const fg_m
             in[s] = ChunkIn{nullptr, 1, seqs[s].pos + r, seqs[s].draft_blocks, seqs[s].n_draft_blocks, FG_LOGITS_LAST};
         if ((rc = build_plan(draft->cfg, *dkv, draft->max_pos, in.data(), n_seqs, plans[r]))) return rc;
     }
+    // the verify rows (device tokens), then the chunks (host tokens, checked and
+    // packed by build_plan; copied after the verify tokens for the launch)
+    std::vector<ChunkIn> vin(n_seqs + n_chunks);
     for (int s = 0; s < n_seqs; s++)
-        in[s] = ChunkIn{nullptr, K1, seqs[s].pos, seqs[s].blocks, seqs[s].n_blocks, FG_LOGITS_ALL};
-    if ((rc = build_plan(target->cfg, *tkv, target->max_pos, in.data(), n_seqs, plans[k]))) return rc;
+        vin[s] = ChunkIn{nullptr, K1, seqs[s].pos, seqs[s].blocks, seqs[s].n_blocks, FG_LOGITS_ALL};
+    for (int c = 0; c < n_chunks; c++)
+        vin[n_seqs + c] = ChunkIn{chunks[c].tokens, chunks[c].n, chunks[c].pos, chunks[c].blocks,
+                                  chunks[c].n_blocks, chunks[c].logits};
+    if ((rc = build_plan(target->cfg, *tkv, target->max_pos, vin.data(), n_seqs + n_chunks, plans[k]))) return rc;
+    const int c_rows = plans[k].t - n_seqs * K1;  // the chunks' rows
     (void)zero_tok;
     // One packed upload: every plan, then the verify token rows and outputs.
     std::vector<size_t> base(k + 1);
@@ -1580,7 +1599,7 @@ static int spec_step(fg_ctx* ctx, const fg_model* target, fg_kv* tkv, const fg_m
         words += plans[r].words;
     }
     const size_t o_vtok = words;
-    words += (size_t)n_seqs * K1 + 64;
+    words += (size_t)n_seqs * K1 + c_rows + 64;
     // persistent launches (one sequence): the draft rounds' first positions (k
     // words) and the draft's block table, then the verify's first position and
     // the target's block table (room rounded up to 64 blocks, so the layout and
@@ -1589,7 +1608,7 @@ static int spec_step(fg_ctx* ctx, const fg_model* target, fg_kv* tkv, const fg_m
     bool any_pd = false;
     for (int r = 0; r < k; r++)
         any_pd |= (pd[r] = pf_eligible(ctx, const_cast<fg_model*>(draft), n_seqs, sampling, plans[r], false));
-    const bool pv = pf_eligible(ctx, const_cast<fg_model*>(target), n_seqs, sampling, plans[k], true);
+    const bool pv = n_chunks == 0 && pf_eligible(ctx, const_cast<fg_model*>(target), n_seqs, sampling, plans[k], true);
     const size_t o_dbt = words;
     if (any_pd) words += (size_t)k + ((size_t)seqs[0].n_draft_blocks + 63) / 64 * 64 + 64;
     const size_t o_tbt = words;
@@ -1608,7 +1627,7 @@ static int spec_step(fg_ctx* ctx, const fg_model* target, fg_kv* tkv, const fg_m
     const size_t o_acc = words;
     words += (size_t)n_seqs + 64;
     const size_t o_am = words;
-    words += (size_t)n_seqs * K1 + 64;
+    words += (size_t)n_seqs * K1 + c_last + 64;
     if ((rc = ensure(&ctx->hmeta, &ctx->hmeta_cap, words * 4, ctx->stream, true))) return rc;
     if ((rc = ensure(&ctx->dmeta, &ctx->dmeta_cap, words * 4, ctx->stream, false))) return rc;
     int32_t* h = (int32_t*)ctx->hmeta;
@@ -1630,6 +1649,7 @@ static int spec_step(fg_ctx* ctx, const fg_model* target, fg_kv* tkv, const fg_m
         hv[s * K1] = seqs[s].tail[seqs[s].n_tail - 1];
         for (int j = 1; j < K1; j++) hv[s * K1 + j] = 0;
     }
+    for (int r = n_seqs * K1; r < plans[k].t; r++) hv[r] = plans[k].tokens[r];
     if (sampling) {
         memcpy(h + o_prm, params, (size_t)n_seqs * sizeof(SampleParams));
         memcpy(h + o_rng, rng, (size_t)n_seqs * 8);
@@ -1697,7 +1717,8 @@ static int spec_step(fg_ctx* ctx, const fg_model* target, fg_kv* tkv, const fg_m
         }
         return 0;
     };
-    bool use_graph = ctx->graphs && !ctx->prof;
+    // steps that carry chunks launch directly (their plans vary step to step)
+    bool use_graph = ctx->graphs && !ctx->prof && n_chunks == 0;
     fg_ctx::GraphSet* gset = nullptr;
     if (use_graph) {
         // everything the captured launches bake in: object identities, the
@@ -1793,6 +1814,7 @@ static int spec_step(fg_ctx* ctx, const fg_model* target, fg_kv* tkv, const fg_m
     memcpy(out_tokens, h + o_out, (size_t)n_seqs * K1 * 4);
     memcpy(out_count, h + o_cnt, (size_t)n_seqs * 4);
     memcpy(out_accepted, h + o_acc, (size_t)n_seqs * 4);
+    if (c_last > 0) memcpy(chunk_am, h + o_am + (size_t)n_seqs * K1, (size_t)c_last * 4);
     float a = 0, b = 0;
     HIPCHK(hipEventElapsedTime(&a, ctx->ev[0], ctx->ev[1]));
     HIPCHK(hipEventElapsedTime(&b, ctx->ev[1], ctx->ev[2]));
@@ -1864,6 +1886,13 @@ int fg_spec_step(fg_ctx* ctx, const fg_model* target, fg_kv* tkv, const fg_model
                  int32_t* out_accepted) {
     return spec_step(ctx, target, tkv, draft, dkv, seqs, n_seqs, k, nullptr, nullptr, out_tokens, out_count,
                      out_accepted);
+}
+
+int fg_spec_step_mixed(fg_ctx* ctx, const fg_model* target, fg_kv* tkv, const fg_model* draft, fg_kv* dkv,
+                       const fg_spec_seq* seqs, int32_t n_seqs, int32_t k, const fg_chunk* chunks, int32_t n_chunks,
+                       uint32_t* out_tokens, int32_t* out_count, int32_t* out_accepted, uint32_t* chunk_argmax_out) {
+    return spec_step(ctx, target, tkv, draft, dkv, seqs, n_seqs, k, nullptr, nullptr, out_tokens, out_count,
+                     out_accepted, chunks, n_chunks, chunk_argmax_out);
 }
 
 int fg_spec_step_sampled(fg_ctx* ctx, const fg_model* target, fg_kv* tkv, const fg_model* draft, fg_kv* dkv,

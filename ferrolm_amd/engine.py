@@ -7,15 +7,19 @@ running sequences, their block tables, the block manager with its prefix
 cache, the token budget of a step, preemption with recompute. Every step's
 work runs on the device through the C ABI:
 
-  - prefill chunks and plain decode rows: one fg_forward (greedy: its argmax
-    gives the token; with sampling requests fg_forward_sampled draws it);
-  - speculating sequences: one fg_spec_step (fg_spec_step_sampled when any
-    of them samples): the draft rounds, the target's verify pass over k+1
-    rows, acceptance and the draft/target rollback counters, on the device.
+  - a greedy step with both speculating sequences and prefill chunks or plain
+    rows: one fg_spec_step_mixed, whose verify forward carries the chunks after
+    the verify rows, as the reference runs one target forward per step;
+  - otherwise prefill chunks and plain decode rows: one fg_forward (greedy:
+    its argmax gives the token; with sampling requests fg_forward_sampled
+    draws it), and speculating sequences: one fg_spec_step
+    (fg_spec_step_sampled when any of them samples): the draft rounds, the
+    target's verify pass over k+1 rows, acceptance and the draft/target
+    rollback counters, on the device.
 
-The reference runs prefill chunks and verify rows in one target forward; here
-they are two device calls. They touch disjoint cache blocks (shared prefix
-blocks are full prompt blocks, never written), so the result is the same.
+Steps with a sampled request make those two calls; they touch disjoint cache
+blocks (shared prefix blocks are full prompt blocks, never written), so the
+result is the same as one forward's.
 
 Block ids from the block manager index the device caches directly. Prefix
 keys are 64-bit hashes of (parent key, block tokens) of this build's own
@@ -205,6 +209,7 @@ class Stats:
     preemptions: int = 0
     spec_proposed: int = 0
     spec_accepted: int = 0
+    mixed_steps: int = 0  # steps whose verify forward also carried chunks (no reference counterpart)
     peak_running: int = 0
     running: int = 0
     waiting: int = 0
@@ -404,6 +409,27 @@ class Engine:
                 budget -= n
         return plans
 
+    def _spec_seq(self, i: int) -> gpu.SpecSeq:
+        s = self.running[i]
+        return gpu.SpecSeq(tail=np.array(s.tokens[s.draft_computed:], np.uint32), draft_pos=s.draft_computed,
+                           pos=s.computed, blocks=np.array(s.blocks, np.uint32),
+                           draft_blocks=np.array(s.draft_blocks, np.uint32))
+
+    def _accept(self, plans: list, spec: list, toks, acc, rng, new: list) -> None:
+        """The rollback of src/engine.rs:613-615 for each speculating plan."""
+        k = self.cfg.spec_k
+        for r, j in enumerate(spec):
+            s = self.running[plans[j][0]]
+            if rng is not None:
+                s.rng = int(rng[r])
+            a = int(acc[r])
+            base = len(s.tokens)
+            self.stats.spec_proposed += k
+            self.stats.spec_accepted += a
+            s.computed = base + a  # both caches hold the accepted proposals
+            s.draft_computed = min(base + k - 1, base + a)
+            new[j] = [int(t) for t in toks[r]]
+
     def _execute(self, plans: list) -> None:
         """Engine::execute (src/engine.rs:499-654) with the device calls."""
         bs = self.cfg.block_size
@@ -411,8 +437,35 @@ class Engine:
         is_spec = [self.draft is not None and len(self.running[i].tokens) - self.running[i].computed == 1 and n > 1
                    for i, n in plans]
         new = [[] for _ in plans]
-        # prefill chunks and plain decode rows: one forward
         plain = [j for j, sp in enumerate(is_spec) if not sp]
+        spec = [j for j, sp in enumerate(is_spec) if sp]
+        # One target pass over every plan (src/engine.rs:511-542) when every
+        # request of the step is greedy: the speculative step carries the prefill
+        # chunks and plain rows in its verify forward. Otherwise (a sampled
+        # request) two device calls.
+        greedy = all(self.running[i].req.params.greedy for i, _ in plans)
+        if plain and spec and greedy:
+            chunks, last = [], []
+            for j in plain:
+                i, n = plans[j]
+                s = self.running[i]
+                done = s.computed + n == len(s.tokens)
+                chunks.append((s.tokens[s.computed:s.computed + n], s.computed, s.blocks,
+                               gpu.LOGITS_LAST if done else gpu.LOGITS_NONE))
+                if done:
+                    last.append(j)
+            seqs = [self._spec_seq(plans[j][0]) for j in spec]
+            toks, acc, am = gpu.spec_step_mixed(self.ctx, self.model, self.kv, self.draft, self.dkv, seqs, k,
+                                                chunks)
+            self.stats.mixed_steps += 1
+            for r, j in enumerate(last):
+                new[j] = [int(am[r])]
+            for j in plain:
+                i, n = plans[j]
+                self.running[i].computed += n
+            self._accept(plans, spec, toks, acc, None, new)
+            plain, spec = [], []
+        # prefill chunks and plain decode rows: one forward
         if plain:
             chunks, last = [], []
             for j in plain:
@@ -437,30 +490,13 @@ class Engine:
                 i, n = plans[j]
                 self.running[i].computed += n
         # speculating sequences: one device speculative step
-        spec = [j for j, sp in enumerate(is_spec) if sp]
         if spec:
-            seqs = []
-            for j in spec:
-                s = self.running[plans[j][0]]
-                seqs.append(gpu.SpecSeq(tail=np.array(s.tokens[s.draft_computed:], np.uint32),
-                                        draft_pos=s.draft_computed, pos=s.computed,
-                                        blocks=np.array(s.blocks, np.uint32),
-                                        draft_blocks=np.array(s.draft_blocks, np.uint32)))
+            seqs = [self._spec_seq(plans[j][0]) for j in spec]
             sampled = any(not self.running[plans[j][0]].req.params.greedy for j in spec)
             params = [self.running[plans[j][0]].req.params.device() for j in spec] if sampled else None
             rng = np.array([self.running[plans[j][0]].rng for j in spec], np.uint64) if sampled else None
             toks, acc = gpu.spec_step(self.ctx, self.model, self.kv, self.draft, self.dkv, seqs, k, params, rng)
-            for r, j in enumerate(spec):
-                s = self.running[plans[j][0]]
-                if sampled:
-                    s.rng = int(rng[r])
-                a = int(acc[r])
-                base = len(s.tokens)
-                self.stats.spec_proposed += k
-                self.stats.spec_accepted += a
-                s.computed = base + a  # both caches hold the accepted proposals
-                s.draft_computed = min(base + k - 1, base + a)
-                new[j] = [int(t) for t in toks[r]]
+            self._accept(plans, spec, toks, acc, rng, new)
         # tokens out, finished sequences, newly full blocks into the prefix cache
         eos = set(self.model.cfg.eos)
         finished = []

@@ -111,6 +111,9 @@ EXPORTS = {
     "fg_forward_capture": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.POINTER(FgChunk), C.c_int32, f32p]),
     "fg_spec_step": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.POINTER(FgSpecSeq),
                                C.c_int32, C.c_int32, u32p, i32p, i32p]),
+    "fg_spec_step_mixed": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p,
+                                     C.POINTER(FgSpecSeq), C.c_int32, C.c_int32, C.POINTER(FgChunk), C.c_int32,
+                                     u32p, i32p, i32p, u32p]),
     "fg_spec_step_sampled": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p,
                                        C.POINTER(FgSpecSeq), C.c_int32, C.c_int32, C.POINTER(FgSampling), u64p,
                                        u32p, i32p, i32p]),
@@ -441,6 +444,39 @@ def spec_step(ctx: Context, target: Model, tkv: KvCache, draft: Model, dkv: KvCa
         check(lib().fg_spec_step_sampled(ctx.h, target.h, tkv.h, draft.h, dkv.h, arr, n, k, _sampling_arrays(params),
                                          rng.ctypes.data_as(u64p), ptr(out, u32p), ptr(cnt, i32p), ptr(acc, i32p)))
     return [out[i, :cnt[i]].copy() for i in range(n)], acc
+
+
+def spec_step_mixed(ctx: Context, target: Model, tkv: KvCache, draft: Model, dkv: KvCache, seqs: list, k: int,
+                    chunks: list):
+    """A greedy speculative step whose verify pass also carries other
+    sequences' chunks (fg_spec_step_mixed): chunks are (tokens, pos, blocks,
+    mode) with mode LOGITS_NONE or LOGITS_LAST. Returns (tokens per sequence,
+    accepted counts, the argmax of each LOGITS_LAST chunk in order)."""
+    n = len(seqs)
+    arr = (FgSpecSeq * n)()
+    keep = []
+    for i, s in enumerate(seqs):
+        tail = np.ascontiguousarray(s.tail, np.uint32)
+        bl = np.ascontiguousarray(s.blocks, np.uint32)
+        db = np.ascontiguousarray(s.draft_blocks, np.uint32)
+        keep += [tail, bl, db]
+        arr[i] = FgSpecSeq(ptr(tail, u32p), len(tail), s.draft_pos, s.pos, ptr(bl, u32p), len(bl), ptr(db, u32p),
+                           len(db))
+    carr = (FgChunk * max(1, len(chunks)))()
+    last = 0
+    for i, (tok, pos, blocks, mode) in enumerate(chunks):
+        tok = np.ascontiguousarray(tok, dtype=np.uint32)
+        blocks = np.ascontiguousarray(blocks, dtype=np.uint32)
+        keep += [tok, blocks]
+        carr[i] = FgChunk(ptr(tok, u32p), len(tok), pos, ptr(blocks, u32p), len(blocks), mode)
+        last += 1 if mode == LOGITS_LAST and len(tok) else 0
+    out = np.zeros((n, k + 1), np.uint32)
+    cnt = np.zeros(n, np.int32)
+    acc = np.zeros(n, np.int32)
+    am = np.zeros(max(1, last), np.uint32)
+    check(lib().fg_spec_step_mixed(ctx.h, target.h, tkv.h, draft.h, dkv.h, arr, n, k, carr, len(chunks),
+                                   ptr(out, u32p), ptr(cnt, i32p), ptr(acc, i32p), ptr(am, u32p)))
+    return [out[i, :cnt[i]].copy() for i in range(n)], acc, am[:last]
 
 
 def last_step_times(ctx: Context) -> np.ndarray:

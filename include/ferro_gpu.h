@@ -210,6 +210,23 @@ int fg_spec_step(fg_ctx* ctx, const fg_model* target, fg_kv* target_kv,
                  uint32_t* out_tokens, int32_t* out_count,
                  int32_t* out_accepted);
 
+/* fg_spec_step whose verify pass also carries other sequences' chunks:
+ * prefill chunks and plain decode rows (FG_LOGITS_NONE or FG_LOGITS_LAST,
+ * host tokens), after the verify rows of the same target forward, as
+ * Engine::execute runs one target pass over every plan of an engine step
+ * (src/engine.rs:511-542). The chunks do not touch the draft (its cache
+ * catches up in the first draft round, as in Engine::propose). Outputs as
+ * fg_spec_step, plus chunk_argmax_out[i]: sampler::argmax of the i-th
+ * FG_LOGITS_LAST chunk row (chunks with n > 0, in order). Greedy only
+ * (sampled steps make two calls). A step with chunks launches directly,
+ * without the step graphs. */
+int fg_spec_step_mixed(fg_ctx* ctx, const fg_model* target, fg_kv* target_kv,
+                       const fg_model* draft, fg_kv* draft_kv,
+                       const fg_spec_seq* seqs, int32_t n_seqs, int32_t k,
+                       const fg_chunk* chunks, int32_t n_chunks,
+                       uint32_t* out_tokens, int32_t* out_count,
+                       int32_t* out_accepted, uint32_t* chunk_argmax_out);
+
 /* fg_spec_step under per-sequence sampling (Engine::propose and
  * Engine::execute with !params.greedy(), src/engine.rs:575-610, 691-700):
  * each draft round draws its proposal from sampler::distribution of the

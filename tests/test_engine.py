@@ -155,6 +155,14 @@ def test_speculative_greedy_decoding_matches_the_target_exactly(ctx, models):
         assert st.spec_proposed > 0
         if layers == 3:
             assert st.spec_accepted == st.spec_proposed, "the target as its own draft"
+    # a small token budget: prompts are prefilled in chunks while earlier
+    # requests speculate, and those steps run one target forward
+    # (fg_spec_step_mixed: the chunks ride in the verify pass)
+    got, st = serve(ctx, models, EngineConfig(spec_k=3, kv_blocks=200, max_batch_tokens=40), reqs,
+                    draft=models.truncated(1))
+    for i, (g, _) in enumerate(got):
+        assert g == want[i], (i, "mixed")
+    assert st.mixed_steps > 0, "no step carried chunks in its verify pass"
 
 
 @pytest.mark.gpu

@@ -83,6 +83,21 @@ def test_spec_step_refusals(ctx, setup):
     good = gpu.SpecSeq(tail=np.array(prompt, np.uint32), draft_pos=0, pos=pos, blocks=np.array([0], np.uint32),
                        draft_blocks=np.array([0], np.uint32))
     refused(ctx, kv, lambda: gpu.spec_step(ctx, m, kv, draft, dkv, [good], 0), "bad argument")
+    # chunks riding in the verify pass (fg_spec_step_mixed): no FG_LOGITS_ALL,
+    # tokens inside the vocabulary
+    V = hm.cfg.vocab
+    refused(ctx, kv, lambda: gpu.spec_step_mixed(ctx, m, kv, draft, dkv, [good], 3,
+                                                 [([5, 6, 7], 0, [2], gpu.LOGITS_ALL)]),
+            "chunks take FG_LOGITS_NONE or FG_LOGITS_LAST")
+    refused(ctx, kv, lambda: gpu.spec_step_mixed(ctx, m, kv, draft, dkv, [good], 3,
+                                                 [([5, V, 7], 0, [2], gpu.LOGITS_LAST)]),
+            "token outside the vocabulary")
+    # a valid mixed step: the chunk's greedy token equals a plain forward's
+    toks, acc, am = gpu.spec_step_mixed(ctx, m, kv, draft, dkv, [good], 3, [([5, 6, 7], 0, [2], gpu.LOGITS_LAST),
+                                                                            ([8, 9], 0, [3], gpu.LOGITS_NONE)])
+    assert 1 <= len(toks[0]) <= 4 and 0 <= int(acc[0]) <= 3 and am.shape == (1,)
+    kv2 = gpu.KvCache(ctx, hm.cfg, 8)
+    assert int(am[0]) == int(gpu.forward(ctx, m, kv2, [([5, 6, 7], 0, [2], gpu.LOGITS_LAST)]).argmax[0])
     # and a valid step runs
     toks, acc = gpu.spec_step(ctx, m, kv, draft, dkv, [good], 3)
     assert 1 <= len(toks[0]) <= 4 and 0 <= int(acc[0]) <= 3
