@@ -454,6 +454,9 @@ struct Plan {
 };
 
 
+// one-span attention items from which decode-sized row groups at hd 64 take two sub-spans
+static constexpr int64_t kTwoSubSpanItems = 8192;
+
 static int build_plan(const fg_config& c, const fg_kv& kv, int max_pos, const ChunkIn* ch, int nch, Plan& P) {
     const int bs = kv.block_size;
     const int group = c.heads / c.kv_heads;
@@ -482,6 +485,12 @@ static int build_plan(const fg_config& c, const fg_kv& kv, int max_pos, const Ch
             maxq = std::max(maxq, nr * group);
         }
     P.ns = w1 * c.kv_heads > 1024 && maxq >= kAttnMfmaQueries ? 128 / span1 : 1;
+    // Decode-sized row groups at hd 64 take two sub-spans per item once the
+    // launch holds at least kTwoSubSpanItems one-span items (on the MFMA path,
+    // the queries padded to a 16-row tile): the second sub-span's loads fly
+    // while the first is scored. cfg3 at 32 sequences (16,896 items): verify
+    // 6105-6111 against 5867 us; 32-position spans instead: 6182 us.
+    if (c.head_dim == 64 && w1 * c.kv_heads >= kTwoSubSpanItems) P.ns = 128 / span1;
     P.maxq = maxq;
     const int span = span1 * P.ns;
     // Long chunks at hd 64 and 128 take the flash items (rf rows each, split into
