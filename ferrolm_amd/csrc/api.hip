@@ -455,7 +455,7 @@ struct Plan {
 
 
 // one-span attention items from which decode-sized row groups at hd 64 take two sub-spans
-static constexpr int64_t kTwoSubSpanItems = 8192;
+static constexpr int64_t kTwoSubSpanItems = 4096;
 
 static int build_plan(const fg_config& c, const fg_kv& kv, int max_pos, const ChunkIn* ch, int nch, Plan& P) {
     const int bs = kv.block_size;
@@ -489,7 +489,10 @@ static int build_plan(const fg_config& c, const fg_kv& kv, int max_pos, const Ch
     // launch holds at least kTwoSubSpanItems one-span items (on the MFMA path,
     // the queries padded to a 16-row tile): the second sub-span's loads fly
     // while the first is scored. cfg3 at 32 sequences (16,896 items): verify
-    // 6105-6111 against 5867 us; 32-position spans instead: 6182 us.
+    // 6105-6111 against 5867 us; 32-position spans instead: 6182 us. At 8
+    // sequences (about 4,400 items) verify 2595-2599 against 2546-2549 us; the
+    // 135M draft at 32 sequences (1,584 items) is slower with them (draft
+    // 5594-5601 against 5456-5458 us), so the bar sits between.
     if (c.head_dim == 64 && w1 * c.kv_heads >= kTwoSubSpanItems) P.ns = 128 / span1;
     P.maxq = maxq;
     const int span = span1 * P.ns;
