@@ -177,7 +177,9 @@ static hipEvent_t prof_event(fg_ctx* c) {
 
 // launch_gemv, timed by its own dispatch while profiling (fg_profile). The
 // speculative step launches directly (no graph) while profiling is on.
-static void gemv(fg_ctx* c, int epi, const DMat& w, const GemvArgs& a) {
+static void gemv(fg_ctx* c, int epi, const DMat& w, const GemvArgs& a0) {
+    GemvArgs a = a0;
+    if (a.mm) a.gcnt = c->gcnt;  // a split GEMM of small tiles meets on these counters and finishes in place
     if (!c->prof || c->capturing) {
         launch_gemv(c->stream, epi, w, a);
         return;

@@ -1100,6 +1100,60 @@ __global__ __launch_bounds__(512) void k_gemm(const GemvArgs a) {
     if (kw == 1) put(cs * 2);
     __syncthreads();
     if (kw == 0) take(cs * 2);
+    if (CS == 1 && RTW <= 2 && ks > 1 && a.gcnt) {
+        // Split K finished in place (tiles of at most 32 rows: the 1B draft's
+        // 16-row rounds of cfg4, 6595-6601 -> 6410-6418 us per step in a same-box
+        // A/B; the target's 48- and 80-row tiles were slower this way, cfg4
+        // verify 8796 -> 9091 us, and keep k_gemm_finish): each workgroup of the
+        // tile stores its partial
+        // with agent-coherent (L2-bypassing) stores and, once they have completed,
+        // bumps the tile's counter; the last to arrive reads every partial the
+        // same way, sums them in split order (k_gemm_finish's order: the same bits
+        // whichever arrives last) and runs the epilogue. It resets the counter
+        // for the next launch.
+        __shared__ int last;
+        if (wave == 0)
+#pragma unroll
+            for (int i = 0; i < RTW; i++)
+#pragma unroll
+                for (int t = 0; t < 4; t++)
+#pragma unroll
+                    for (int r = 0; r < 4; r++) {
+                        const int rr = i * 16 + 4 * (lane >> 4) + r, cc = t * 16 + (lane & 15);
+                        if (rr < rows && col0 + cc < a.N)
+                            __hip_atomic_store(a.kpart + ((size_t)blockIdx.z * a.m + row0 + rr) * a.N + col0 + cc,
+                                               acc[i][t][r], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    }
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+        if (tid == 0) {
+            unsigned* cnt = a.gcnt + ((size_t)blockIdx.y * gridDim.x + blockIdx.x) * 32;
+            const unsigned old = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            last = old == (unsigned)ks - 1;
+            if (last) __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        __syncthreads();
+        if (!last) return;
+        constexpr int KSMAX = 8;
+        for (int idx = tid; idx < 16 * RTW * 64; idx += NTHR) {
+            const int rr = idx >> 6, cc = idx & 63;
+            const bool live = rr < rows && col0 + cc < a.N;
+            const size_t at = ((size_t)min(row0 + rr, a.m - 1)) * a.N + min(col0 + cc, a.N - 1);
+            float pv[KSMAX];
+#pragma unroll
+            for (int z = 0; z < KSMAX; z++)
+                pv[z] = z < ks ? __hip_atomic_load(a.kpart + (size_t)z * a.m * a.N + at, __ATOMIC_RELAXED,
+                                                   __HIP_MEMORY_SCOPE_AGENT)
+                               : 0.0f;
+            float v = pv[0];
+#pragma unroll
+            for (int z = 1; z < KSMAX; z++)
+                if (z < ks) v += pv[z];
+            yt[rr * YS + cc] = live ? v : 0.0f;
+        }
+        if (col0 < a.N) gemm_epilogue<EPI, NTHR, 16 * RTW>(a, yt, part, rs, row0, rows, col0);
+        return;
+    }
     for (int c = 0; c < CS; c++) {
     if (c > 0) __syncthreads();  // the previous column set's epilogue is done with yt
     const int colc = col0 + c * 64;
@@ -1189,7 +1243,9 @@ static void gemm_rtw(hipStream_t st, int epi, const DMat& w, const GemvArgs& a0,
     const dim3 grid(cg, groups, ks);
     // timed from the start of the main kernel to the end of the split's finish
     auto run = [&](auto kern, auto fin) {
-        if (ks == 1) {
+        // one column set of at most two row tiles, with meeting counters: the
+        // split is finished in the kernel
+        if (ks == 1 || (CS == 1 && RTW <= 2 && a.gcnt)) {
             launch_timed(kern, grid, dim3(512), st, a, e0, e1);
         } else {
             launch_timed(kern, grid, dim3(512), st, a, e0, nullptr);
