@@ -494,7 +494,9 @@ static int build_plan(const fg_config& c, const fg_kv& kv, int max_pos, const Ch
     // 6105-6111 against 5867 us; 32-position spans instead: 6182 us. At 8
     // sequences (about 4,400 items) verify 2595-2599 against 2546-2549 us; the
     // 135M draft at 32 sequences (1,584 items) is slower with them (draft
-    // 5594-5601 against 5456-5458 us), so the bar sits between.
+    // 5594-5601 against 5456-5458 us), so the bar sits between. cfg4's 1B draft
+    // (about 4,600 items of 4 queries): device time 1% more, but half the item
+    // records to pack and upload per round, step 15.8 -> 15.4 ms.
     if (c.head_dim == 64 && w1 * c.kv_heads >= kTwoSubSpanItems) P.ns = 128 / span1;
     P.maxq = maxq;
     const int span = span1 * P.ns;
