@@ -590,7 +590,15 @@ static int build_plan(const fg_config& c, const fg_kv& kv, int max_pos, const Ch
         P.t += k.n;
     }
     P.S = (int)P.sel.size();
-    P.Wc = std::max(16, (P.W + 15) / 16 * 16);
+    // launch capacity (unused slots exit at once): a multiple of 16 work items,
+    // or of a power of two near W/16 for large launches, so that a step graph
+    // keyed on it outlives the context growth of many sequences (at 32 of them
+    // a launch gains an item every two or four steps, and each new capacity
+    // captures the step's graphs again: cfg3 at 32 sequences, 48 steps,
+    // 2627-2649 -> 2716-2723 tok/s with this rounding)
+    int wstep = 16;
+    while (wstep * 16 <= P.W) wstep *= 2;
+    P.Wc = std::max(16, (P.W + wstep - 1) / wstep * wstep);
     P.wrec.resize((size_t)P.Wc * 16, 0);
     size_t o = 0;
     auto place = [&](size_t n) {
