@@ -1490,21 +1490,41 @@ __global__ __launch_bounds__(256, MINW) void k_attn(AttnArgs a) {
             vv[it] = ld_nt_f4(src_of(p, kvd) + d);
         }
     };
-    load_sub(p0, min(p0 + P, p1));
-    // q, rotated: 4 (d, d + HALF) pairs per item
-    for (int i = tid; i < Q * (HALF / 4); i += 256) {
+    // q's loads go first: loads retire in order, so staging q then waits on q
+    // alone while the keys and values are still in flight (and, on the VALU path
+    // of one sub-span, the scores wait on the keys alone). 4 (d, d + HALF) pairs
+    // per item; past the item's queries the last is loaded again (unconditional
+    // loads) and not stored.
+    constexpr int QI = QL * (HALF / 4), QIT = (QI + 255) / 256;
+    const int qn = Q * (HALF / 4);
+    float4 qx1[QIT], qx2[QIT], qcs[QIT], qsn[QIT];
+#pragma unroll
+    for (int it = 0; it < QIT; it++) {
+        const int i = min(tid + it * 256, qn - 1);
         const int q = i / (HALF / 4), d = (i % (HALF / 4)) * 4, r = q / G, j = q % G, row = row0 + r;
         const int pos = pos_of_row0 + r;
         const float* src = a.qkv + (size_t)row * a.ld + (size_t)(h * G + j) * HD;
-        const float4 x1 = *(const float4*)(src + d), x2 = *(const float4*)(src + d + HALF);
-        const float4 c = *(const float4*)(a.cos_t + (size_t)pos * HALF + d);
-        const float4 sn = *(const float4*)(a.sin_t + (size_t)pos * HALF + d);
-        const float a1[4] = {x1.x, x1.y, x1.z, x1.w}, a2[4] = {x2.x, x2.y, x2.z, x2.w};
-        const float cc[4] = {c.x, c.y, c.z, c.w}, ss[4] = {sn.x, sn.y, sn.z, sn.w};
+        qx1[it] = *(const float4*)(src + d);
+        qx2[it] = *(const float4*)(src + d + HALF);
+        qcs[it] = *(const float4*)(a.cos_t + (size_t)pos * HALF + d);
+        qsn[it] = *(const float4*)(a.sin_t + (size_t)pos * HALF + d);
+    }
+    load_sub(p0, min(p0 + P, p1));
+    // q, rotated
 #pragma unroll
-        for (int e = 0; e < 4; e++) {
-            qs[q][d + e] = __fadd_rn(__fmul_rn(a1[e], cc[e]), __fmul_rn(-a2[e], ss[e]));
-            qs[q][d + HALF + e] = __fadd_rn(__fmul_rn(a2[e], cc[e]), __fmul_rn(a1[e], ss[e]));
+    for (int it = 0; it < QIT; it++) {
+        const int i = tid + it * 256;
+        if (i < qn) {
+            const int q = i / (HALF / 4), d = (i % (HALF / 4)) * 4;
+            const float a1[4] = {qx1[it].x, qx1[it].y, qx1[it].z, qx1[it].w};
+            const float a2[4] = {qx2[it].x, qx2[it].y, qx2[it].z, qx2[it].w};
+            const float cc[4] = {qcs[it].x, qcs[it].y, qcs[it].z, qcs[it].w};
+            const float ss[4] = {qsn[it].x, qsn[it].y, qsn[it].z, qsn[it].w};
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                qs[q][d + e] = __fadd_rn(__fmul_rn(a1[e], cc[e]), __fmul_rn(-a2[e], ss[e]));
+                qs[q][d + HALF + e] = __fadd_rn(__fmul_rn(a2[e], cc[e]), __fmul_rn(a1[e], ss[e]));
+            }
         }
     }
     // From kAttnMfmaQueries queries on, the scores and the weighted values run on f32 MFMA
@@ -1554,21 +1574,21 @@ __global__ __launch_bounds__(256, MINW) void k_attn(AttnArgs a) {
                 }
             }
         }
+        auto store_v = [&]() {
 #pragma unroll
-        for (int it = 0; it < VIT; it++) {
-            const int i = tid + it * 256;
-            if (i < VI) {
-                const bool live = sp0 + i / (HD / 4) < sp1;
-                *(float4*)&vs[i / (HD / 4)][(i % (HD / 4)) * 4] =
-                    make_float4(live ? vv[it].x : 0.0f, live ? vv[it].y : 0.0f, live ? vv[it].z : 0.0f,
-                                live ? vv[it].w : 0.0f);
+            for (int it = 0; it < VIT; it++) {
+                const int i = tid + it * 256;
+                if (i < VI) {
+                    const bool live = sp0 + i / (HD / 4) < sp1;
+                    *(float4*)&vs[i / (HD / 4)][(i % (HD / 4)) * 4] =
+                        make_float4(live ? vv[it].x : 0.0f, live ? vv[it].y : 0.0f, live ? vv[it].z : 0.0f,
+                                    live ? vv[it].w : 0.0f);
+                }
             }
-        }
-        __syncthreads();
-        // the next sub-span's loads fly while this one is scored
-        if (NS > 1 && sp1 < p1) load_sub(sp1, min(sp1 + P, p1));
-        // this group's new rows in the sub-span go to the cache
-        {
+        };
+        // this group's new rows in the sub-span go to the cache (from ks and vs;
+        // other items read new positions from the q/k/v rows, never the cache)
+        auto new_rows_to_cache = [&]() {
             const int n0 = max(max(sp0, cpos0), cpos0 + row0 - crow0);
             const int n1 = min(sp1, cpos0 + row0 + nrows - crow0);
             for (int i = tid; i < (n1 - n0) * HD; i += 256) {
@@ -1577,7 +1597,17 @@ __global__ __launch_bounds__(256, MINW) void k_attn(AttnArgs a) {
                 a.kc[at] = ks[o][d];
                 a.vc[at] = vs[o][d];
             }
-        }
+        };
+        // An item of one sub-span scores its keys while its values are still
+        // arriving: the values go to LDS after the softmax (before the barrier
+        // that precedes the weighted values). With more sub-spans the next one's
+        // loads reuse the value registers right after the first barrier.
+        constexpr bool late_v = NS == 1;
+        if (!late_v) store_v();
+        __syncthreads();
+        // the next sub-span's loads fly while this one is scored
+        if (NS > 1 && sp1 < p1) load_sub(sp1, min(sp1 + P, p1));
+        if (!late_v) new_rows_to_cache();
         if (mf) {
             // scores, scaled, into pr
             constexpr int NTP = P / 16;
@@ -1598,7 +1628,12 @@ __global__ __launch_bounds__(256, MINW) void k_attn(AttnArgs a) {
         // each wave holds whole queries (one per P lanes) and reduces them in
         // registers. Across sub-spans the exponentials are taken against the
         // running max, and the running sum is rescaled to it.
-        for (int base = wave * 64; base < Q * P; base += 256) {
+        // (unrolled to its bound: a loop here would make the compiler drain the
+        // value loads still in flight before entering it)
+#pragma unroll
+        for (int pass = 0; pass < (QL * P + 255) / 256; pass++) {
+            const int base = wave * 64 + pass * 256;
+            if (base >= Q * P) break;
             const int i = base + lane, q = i / P, o = i % P, p = sp0 + o;
             float sc = -INFINITY;
             if (q < Q && p < sp1 && p <= lim[q] && mf) {
@@ -1639,7 +1674,9 @@ __global__ __launch_bounds__(256, MINW) void k_attn(AttnArgs a) {
                 }
             }
         }
+        if (late_v) store_v();
         __syncthreads();
+        if (late_v) new_rows_to_cache();
         if (mf) {
             // weighted values: O = fac O + P V, tile ti = wave + 4 j
 #pragma unroll
