@@ -36,6 +36,7 @@ from dataclasses import dataclass, field
 import numpy as np
 
 from . import gpu
+from .spec import TableCache
 
 ROOT = 0  # the key before a sequence's first block (src/kv.rs:98)
 
@@ -243,6 +244,7 @@ class Engine:
         c = model.cfg
         self.kv = gpu.KvCache(ctx, c, cfg.kv_blocks)
         self.blocks = BlockManager(cfg.kv_blocks, cfg.block_size, cfg.prefix_cache)
+        self.tables = TableCache()  # uint32 copies of the running sequences' block tables
         if draft is not None:
             if draft.cfg.vocab != c.vocab:
                 raise ValueError("draft and target must share a vocabulary")
@@ -282,6 +284,8 @@ class Engine:
 
     # ---- bookkeeping ----------------------------------------------------
     def _release(self, s: _Seq) -> None:
+        self.tables.drop((id(s), 0))
+        self.tables.drop((id(s), 1))
         for b in s.blocks:
             self.blocks.release(b)
         s.blocks, s.keys, s.computed = [], [], 0
@@ -412,8 +416,8 @@ class Engine:
     def _spec_seq(self, i: int) -> gpu.SpecSeq:
         s = self.running[i]
         return gpu.SpecSeq(tail=np.array(s.tokens[s.draft_computed:], np.uint32), draft_pos=s.draft_computed,
-                           pos=s.computed, blocks=np.array(s.blocks, np.uint32),
-                           draft_blocks=np.array(s.draft_blocks, np.uint32))
+                           pos=s.computed, blocks=self.tables.get((id(s), 0), s.blocks),
+                           draft_blocks=self.tables.get((id(s), 1), s.draft_blocks))
 
     def _accept(self, plans: list, spec: list, toks, acc, rng, new: list) -> None:
         """The rollback of src/engine.rs:613-615 for each speculating plan."""

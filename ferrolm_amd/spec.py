@@ -66,6 +66,27 @@ class ShuffledPool(BlockPool):
         return True
 
 
+class TableCache:
+    """uint32 copies of block tables for the device calls, reused until a table
+    grows: a table list only ever grows in place (a released table is replaced
+    by a new list), so the same list object at the same length holds the same
+    ids. At 32 sequences of up to 2k tokens, converting every table on every
+    step cost about as much host time as the rest of the step's host work."""
+
+    def __init__(self):
+        self._c = {}
+
+    def get(self, key, table: list) -> np.ndarray:
+        e = self._c.get(key)
+        if e is None or e[0] is not table or len(e[1]) != len(table):
+            e = (table, np.array(table, np.uint32))
+            self._c[key] = e
+        return e[1]
+
+    def drop(self, key) -> None:
+        self._c.pop(key, None)
+
+
 class Batch:
     """Several greedy requests decoded together (ignore_eos). The prompts are
     prefilled in one forward over all their chunks (Logits::Last each); then
@@ -89,6 +110,7 @@ class Batch:
         n = len(self.tokens)
         self.tb, self.db = [[] for _ in range(n)], [[] for _ in range(n)]
         self.computed, self.dcomp = [0] * n, [0] * n
+        self.tables = TableCache()
         self.stats = GenStats()
 
     def prefill(self, max_tokens: int = 0) -> list:
@@ -141,8 +163,8 @@ class Batch:
                     not self.dpool.grow(self.db[i], len(t) + k - 1):
                 raise RuntimeError("out of cache blocks")
             seqs.append(gpu.SpecSeq(tail=np.array(t[self.dcomp[i]:], np.uint32), draft_pos=self.dcomp[i],
-                                    pos=self.computed[i], blocks=np.array(self.tb[i], np.uint32),
-                                    draft_blocks=np.array(self.db[i], np.uint32)))
+                                    pos=self.computed[i], blocks=self.tables.get((i, 0), self.tb[i]),
+                                    draft_blocks=self.tables.get((i, 1), self.db[i])))
         toks, acc = gpu.spec_step(self.ctx, self.target, self.tkv, self.draft, self.dkv, seqs, k, self.params,
                                   self.rng)
         t_us = gpu.last_step_times(self.ctx)

@@ -121,3 +121,19 @@ def test_benchmark_shapes():
     assert per * s.layers == 1_610_612_736
     t, d, kind, k, plen = synth.shapes_for(2)
     assert kind == INT4 and k == 3 and plen == 1024 and d.hidden == 576
+
+
+def test_table_cache_reuses_a_table_until_it_grows_or_is_replaced():
+    from ferrolm_amd.spec import TableCache
+    c = TableCache()
+    t = [5, 9]
+    a = c.get("s", t)
+    assert a.dtype == np.uint32 and list(a) == [5, 9]
+    assert c.get("s", t) is a              # unchanged: the same array
+    t.append(2)
+    b = c.get("s", t)
+    assert list(b) == [5, 9, 2] and b is not a
+    u = [7, 7, 7]                          # a released table's replacement, same length
+    assert list(c.get("s", u)) == [7, 7, 7]
+    c.drop("s")
+    assert list(c.get("s", u)) == [7, 7, 7]
