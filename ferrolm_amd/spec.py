@@ -208,6 +208,7 @@ class Runner:
             self.dkv = dkv or gpu.KvCache(ctx, draft.cfg, kv_blocks + max_seqs)
         self.tpool, self.dpool = BlockPool(kv_blocks), BlockPool(kv_blocks + max_seqs)
         self.tb, self.db = [], []
+        self.tables = TableCache()
         self.tokens = list(prompt)
         self.computed = 0
         self.dcomp = 0
@@ -228,8 +229,8 @@ class Runner:
             raise RuntimeError("out of cache blocks")
         if spec:
             seq = gpu.SpecSeq(tail=np.array(self.tokens[self.dcomp:], np.uint32), draft_pos=self.dcomp,
-                              pos=self.computed, blocks=np.array(self.tb, np.uint32),
-                              draft_blocks=np.array(self.db, np.uint32))
+                              pos=self.computed, blocks=self.tables.get(0, self.tb),
+                              draft_blocks=self.tables.get(1, self.db))
             toks, acc = gpu.spec_step(self.ctx, self.target, self.tkv, self.draft, self.dkv, [seq], k,
                                       None if self.params is None else [self.params], self.rng)
             t_us = gpu.last_step_times(self.ctx)
