@@ -1309,6 +1309,16 @@ static void gemv_pg(hipStream_t st, const DMat& w, const GemvArgs& a, hipEvent_t
         const int W = std::max(1, std::min(maxw, KC));
         launch_timed(k_gemv<KIND, NT, EPI, 1>, dim3(groups, 1, 1), dim3(64 * W), st, a, e0, e1);
     } else if constexpr (NT <= 4) {
+        // Up to 8 passes (32 rows): one pass per workgroup along z, each reading
+        // the weights again from L2, for 8x the workgroups of a decode launch
+        // (cfg3's 135M draft rounds at 32 sequences: draft 5374-5377 -> 5015-5025
+        // us per step, at 8 sequences 3828 -> 3457 us). More passes take groups
+        // of four, which share one weight read.
+        if (a.p_total <= 8) {
+            const int W = std::max(1, std::min(maxw, KC));
+            launch_timed(k_gemv<KIND, NT, EPI, 1>, dim3(groups, 1, a.p_total), dim3(64 * W), st, a, e0, e1);
+            return;
+        }
         const int pg = (a.p_total + 3) / 4;
         int W = (4096 + groups * pg - 1) / (groups * pg);
         W = std::max(1, std::min(std::min(W, maxw), KC));
