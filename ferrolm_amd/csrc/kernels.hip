@@ -1313,8 +1313,11 @@ static void gemv_pg(hipStream_t st, const DMat& w, const GemvArgs& a, hipEvent_t
         // the weights again from L2, for 8x the workgroups of a decode launch
         // (cfg3's 135M draft rounds at 32 sequences: draft 5374-5377 -> 5015-5025
         // us per step, at 8 sequences 3828 -> 3457 us). More passes take groups
-        // of four, which share one weight read.
-        if (a.p_total <= 8) {
+        // of four, which share one weight read; for gate/up, whose weights are
+        // the largest, already past 4 passes (at 32 sequences draft 5078-5080 ->
+        // 4929-4954 us; at 8 sequences, 2 passes, one per workgroup stays faster:
+        // 3457 against 3559 us).
+        if (a.p_total <= (EPI == EPI_SILU ? 4 : 8)) {
             const int W = std::max(1, std::min(maxw, KC));
             launch_timed(k_gemv<KIND, NT, EPI, 1>, dim3(groups, 1, a.p_total), dim3(64 * W), st, a, e0, e1);
             return;
