@@ -1272,6 +1272,13 @@ static void gemm_kind(hipStream_t st, int epi, const DMat& w, const GemvArgs& a,
     // tiles, for more workgroups (measured on the cfg2 prompt's forwards: the
     // 135M draft 3.97 -> 3.31 ms, the 1.7B target's o and down 14.13 -> 14.03 ms
     // per forward)
+    // 80 to 160 rows into 16384 or more outputs (gate/up and the lm_heads of the
+    // batched verifies): 128-column tiles too. Same-box A/B: cfg4 verify
+    // 8644-8650 -> 8383-8386 us, cfg3 at 32 sequences 5682 -> 5485 us.
+    if (rt >= 5 && rt < 16 && rtw == 5 && w.n_tiles >= 1024) {
+        gemm_rtw<KIND, 5, 2>(st, epi, w, a, groups, e0, e1);
+        return;
+    }
     if (rt >= 16 && w.n_tiles < 256)
         gemm_rtw<KIND, 2, 1>(st, epi, w, a, (rt + 1) / 2, e0, e1);
     else
