@@ -1274,7 +1274,9 @@ static void gemm_kind(hipStream_t st, int epi, const DMat& w, const GemvArgs& a,
     // per forward)
     // 80 to 160 rows into 16384 or more outputs (gate/up and the lm_heads of the
     // batched verifies): 128-column tiles too. Same-box A/B: cfg4 verify
-    // 8644-8650 -> 8383-8386 us, cfg3 at 32 sequences 5682 -> 5485 us.
+    // 8644-8650 -> 8383-8386 us, cfg3 at 32 sequences 5682 -> 5485 us. At 40
+    // rows (three-tile groups) they were slower: cfg3 at 8 sequences 2562 ->
+    // 2690 us.
     if (rt >= 5 && rt < 16 && rtw == 5 && w.n_tiles >= 1024) {
         gemm_rtw<KIND, 5, 2>(st, epi, w, a, groups, e0, e1);
         return;
