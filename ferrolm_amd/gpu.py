@@ -223,7 +223,8 @@ class Context:
             self.h = None
 
     def __del__(self):
-        self.close()
+        if lib is not None:  # at interpreter exit the module's globals are already cleared
+            self.close()
 
 
 class Model:
@@ -281,7 +282,8 @@ class Model:
             self.h = None
 
     def __del__(self):
-        self.close()
+        if lib is not None:  # at interpreter exit the module's globals are already cleared
+            self.close()
 
 
 class KvCache:
@@ -316,7 +318,8 @@ class KvCache:
             self.h = None
 
     def __del__(self):
-        self.close()
+        if lib is not None:  # at interpreter exit the module's globals are already cleared
+            self.close()
 
 
 @dataclass
@@ -537,7 +540,8 @@ class Mat:
             self.h = None
 
     def __del__(self):
-        self.close()
+        if lib is not None:  # at interpreter exit the module's globals are already cleared
+            self.close()
 
 
 def _qmatrix_buffers(kind: int, rows: int, cols: int):
