@@ -15,8 +15,9 @@ device work). `value` = tokens emitted in the timed steps / their wall time
 the device time of the verify pass (HIP events, mean over the timed steps).
 
 roofline: GEMV launches are bracketed with HIP events (fg_profile) during
-a second pass over K steps from the same state; the dominant GEMV kernel
-class gives achieved = algorithmic bytes per launch / mean launch time.
+a second pass over K steps from the same state; the target's int4 GEMV
+class gives achieved = algorithmic bytes per launch / mean launch time
+(no roofline when no target GEMV was recorded).
 cpu_baseline: the C oracle (the reference's CPU algorithm restated) resumes
 from a copy of the GPU's KV state before the timed steps and runs as many
 spec steps as fit in --cpu-seconds on the host cores; its emitted tokens are
@@ -24,6 +25,10 @@ compared with the GPU's from the same state. It runs the oracle's fast path
 where the CPU has AVX-512: the reference's register tiles, eight-wide
 attention scores and spinning thread pool, bit-identical to the portable
 loops. The record names the CPU model, the path and the threads.
+batched: the batched verify configurations on the same box, after the
+headline (unless --no-batched): cfg3 at 32 sequences and cfg4 at 16, each
+its emitted tok/s over all sequences, verify and draft step times and the
+verify GEMMs' MFMA roofline (see measure_batched).
 """
 from __future__ import annotations
 
@@ -76,6 +81,9 @@ def main() -> int:
     ap.add_argument("--cpu-seconds", type=float, default=20.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-profile", action="store_true")
+    ap.add_argument("--no-batched", action="store_true",
+                    help="skip the batched verify sub-records (cfg3 B=32, cfg4 B=16) of the headline run")
+    ap.add_argument("--batched-steps", type=int, default=12)
     ap.add_argument("--batch", type=int, default=0, help="sequences for configs 3/4 (default: the config's own)")
     ap.add_argument("--serve", action="store_true",
                     help="serve 32 requests with a shared prefix through the engine (continuous batching) instead")
@@ -179,8 +187,8 @@ def main() -> int:
         log(f"profiled pass: {prof_elapsed * 1e3:.1f} ms for {a.steps} steps "
             f"(unprofiled {elapsed * 1e3:.1f} ms)")
         tkind = KIND_NAMES[wl.target_kind]
-        dom = [x for x in recs if x["kind"] == tkind and not x["gemm"]] or recs
-        if dom:  # none when every projection ran inside the persistent forward (FERRO_PFWD=1)
+        dom = [x for x in recs if x["kind"] == tkind and not x["gemm"]]
+        if dom:
             dom = max(dom, key=lambda x: x["us"])
             ach = dom["bytes"] / dom["us"] / 1e3
             roofline = {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
@@ -239,6 +247,20 @@ def main() -> int:
         parity = {"steps_compared": len(cpu_emitted), "steps_identical": same}
         log(f"cpu baseline: {cpu['value']} tok/s ({cpu['ms_per_step']} ms/step); parity {same}/{len(cpu_emitted)}")
 
+    batched = None
+    if a.config == 2 and not a.no_batched:
+        # the headline's models and caches are not needed any more
+        del r
+        target.close()
+        draft.close()
+        batched = []
+        for c, B in ((3, 32), (4, 16)):
+            bwl = synth.build(c, seed=a.seed)
+            bt, bd = gpu.Model(ctx, bwl.target), gpu.Model(ctx, bwl.draft)
+            batched.append(measure_batched(a, bwl, ctx, bt, bd, B, a.batched_steps, 3))
+            bt.close()
+            bd.close()
+
     line = {
         "metric": METRIC, "value": round(value, 2), "unit": "tok/s", "n_gpus": 1, "steps": a.steps,
         "warmup": a.warmup, "ms_per_step": round(elapsed / a.steps * 1e3, 4), "higher_is_better": True,
@@ -249,7 +271,7 @@ def main() -> int:
                    "target_layers": cfg.layers, "hidden": cfg.hidden, "k": k, "batch": wl.batch,
                    "prompt": wl.prompt_len, "context_at_timed_start": ctx_start},
         "verify_step_us": round(verify_us, 2), "draft_us": round(draft_us, 2), "acceptance": round(acceptance, 4),
-        "roofline": roofline, "cpu_baseline": cpu, "parity": parity, "prefill": prefill,
+        "roofline": roofline, "cpu_baseline": cpu, "parity": parity, "prefill": prefill, "batched": batched,
     }
     print(json.dumps(line), flush=True)
     return 0
@@ -293,36 +315,39 @@ def measure_prefill(ctx, target, draft, prompt, first_token, reps=5):
     return out
 
 
-def run_batched(a, wl, ctx, target, draft) -> int:
+def measure_batched(a, wl, ctx, target, draft, B: int, steps: int, warmup: int) -> dict:
     """Batched verify (configs 3 and 4): B sequences with context lengths drawn
     uniformly (cfg3 128-2048, cfg4 512-4096), block tables from a shuffled pool,
-    every step one device speculative step over all of them. Reports emitted
-    tok/s over all sequences, the verify step's device time, and the MFMA rate of
-    the verify GEMMs (algorithmic 2*rows*n*k over their summed launch time). No
-    CPU baseline here: the oracle would need a host copy of the whole cache; the
-    per-sequence parity of batched steps is a GPU test."""
+    every step one device speculative step over all of them (Engine::execute
+    over decoding sequences, src/engine.rs:499-654). Returns emitted tok/s over
+    all sequences, the verify and draft device times per step, and the MFMA
+    roofline of the target's verify GEMMs: the dominant weight kind's GEMM
+    launches (events around each, in a second pass of `steps` steps), the
+    algorithmic 2*rows*n*k over their summed time against the dense bf16 peak.
+    No CPU baseline here: the oracle would need a host copy of the whole cache;
+    every sequence's step is checked against the oracle by a GPU test."""
     from ferrolm_amd import gpu, spec, synth
     from ferrolm_amd.weights import KIND_NAMES
-    B = a.batch if a.batch > 1 else wl.batch
     k = wl.k
     cfg = wl.target.cfg
-    lo, hi = (512, 4096) if a.config == 4 else (128, 2048)
+    lo, hi = (512, 4096) if wl.name == "cfg4" else (128, 2048)
     rng = np.random.default_rng(a.seed)
     lens = [int(x) for x in rng.integers(lo, hi + 1, B)]
     prompts = [[int(t) for t in synth.prompt_ids(n, cfg.vocab, a.seed + 1 + i)] for i, n in enumerate(lens)]
-    total = a.warmup + 2 * a.steps
+    total = warmup + 2 * steps
     blocks = sum((n + total * (k + 1) + 32) // 16 + 2 for n in lens)
     b = spec.Batch(ctx, target, draft, prompts, k, kv_blocks=blocks, seed=a.seed)
     t1 = time.time()
     b.prefill(max_tokens=2048)
-    log(f"prefill of {B} prompts ({sum(lens)} tokens, {min(lens)}..{max(lens)}): {time.time() - t1:.2f}s")
-    for _ in range(a.warmup):
+    log(f"{wl.name} B={B}: prefill of {B} prompts ({sum(lens)} tokens, {min(lens)}..{max(lens)}): "
+        f"{time.time() - t1:.2f}s")
+    for _ in range(warmup):
         b.step()
     st0 = len(b.stats.verify_us)
     ctx.sync()
     tt = time.perf_counter()
     n_tok = 0
-    for _ in range(a.steps):
+    for _ in range(steps):
         n_tok += sum(len(e) for e in b.step())
     ctx.sync()
     elapsed = time.perf_counter() - tt
@@ -330,44 +355,60 @@ def run_batched(a, wl, ctx, target, draft) -> int:
     verify_us = float(np.mean(b.stats.verify_us[st0:]))
     draft_us = float(np.mean(b.stats.draft_us[st0:]))
     acceptance = b.stats.accepted / max(1, b.stats.proposed)
-    log(f"timed {a.steps} steps x {B} sequences: {elapsed * 1e3:.1f} ms, {n_tok} tokens, {value:.1f} tok/s, "
+    log(f"{wl.name} B={B}: timed {steps} steps: {elapsed * 1e3:.1f} ms, {n_tok} tokens, {value:.1f} tok/s, "
         f"verify {verify_us:.1f} us, draft {draft_us:.1f} us")
     roofline = None
     if not a.no_profile:
         gpu.profile(ctx, True)
         gpu.profile_read(ctx, reset=True)
-        for _ in range(a.steps):
+        for _ in range(steps):
             b.step()
         ctx.sync()
         recs = gpu.profile_read(ctx, reset=True)
         gpu.profile(ctx, False)
         for rec in recs:
             what = "gemm" if rec["gemm"] else f"gemv passes<={rec['passes']}"
-            log(f"{what} {rec['kind']}: {rec['launches']} launches, "
+            log(f"{wl.name} {what} {rec['kind']}: {rec['launches']} launches, "
                 f"{rec['us'] / rec['launches']:.2f} us avg, {rec['bytes'] / rec['us'] / 1e3:.0f} GB/s, "
                 f"{rec['flops'] / rec['us'] / 1e6:.1f} TFLOP/s")
         tkind = KIND_NAMES[wl.target_kind]
-        dom = max([x for x in recs if x["kind"] == tkind and x["gemm"]] or recs, key=lambda x: x["us"])
-        ach = dom["flops"] / dom["us"] / 1e6
-        # the GEMM runs bf16 MFMA on two activation pieces (hi + lo): it issues twice the
-        # algorithmic flops; both rates are priced against the dense bf16 peak
-        roofline = {"bound": "mfma", "achieved": round(ach, 2), "peak": 2500.0, "unit": "TFLOP/s",
-                    "frac": round(ach / 2500.0, 5), "mfma_issue_frac": round(2 * ach / 2500.0, 5),
-                    "traffic": None,
-                    "kernel": f"k_gemm {dom['kind']} weights, bf16 MFMA (target verify GEMMs, {B * (k + 1)} rows)",
-                    "flops_per_launch": round(dom["flops"] / dom["launches"]),
-                    "us_per_launch": round(dom["us"] / dom["launches"], 3), "launches": dom["launches"]}
+        dom = [x for x in recs if x["kind"] == tkind and x["gemm"]]
+        if dom:
+            dom = max(dom, key=lambda x: x["us"])
+            ach = dom["flops"] / dom["us"] / 1e6
+            # the GEMM runs bf16 MFMA on two activation pieces (hi + lo): it issues
+            # twice the algorithmic flops; both rates are priced against the dense
+            # bf16 peak
+            roofline = {"bound": "mfma", "achieved": round(ach, 2), "peak": 2500.0, "unit": "TFLOP/s",
+                        "frac": round(ach / 2500.0, 5), "mfma_issue_frac": round(2 * ach / 2500.0, 5),
+                        "traffic": None,
+                        "kernel": f"k_gemm {dom['kind']} weights, bf16 MFMA (target verify GEMMs, {B * (k + 1)} rows)",
+                        "flops_per_launch": round(dom["flops"] / dom["launches"]),
+                        "us_per_launch": round(dom["us"] / dom["launches"], 3), "launches": dom["launches"]}
+    rec = {"workload": f"{wl.name}: {KIND_NAMES[wl.target_kind]} target ({cfg.layers} layers, hidden {cfg.hidden}) "
+                       f"+ bf16 draft, k={k}, {B} sequences, contexts {lo}-{hi}, shuffled 16-token blocks",
+           "value": round(value, 2), "unit": "tok/s", "batch": B, "k": k, "steps": steps, "warmup": warmup,
+           "ms_per_step": round(elapsed / steps * 1e3, 4), "verify_step_us": round(verify_us, 2),
+           "draft_us": round(draft_us, 2), "acceptance": round(acceptance, 4), "roofline": roofline}
+    del b
+    return rec
+
+
+def run_batched(a, wl, ctx, target, draft) -> int:
+    """--config 3 / 4: the batched verify (measure_batched) as the line."""
+    from ferrolm_amd.weights import KIND_NAMES
+    B = a.batch if a.batch > 1 else wl.batch
+    cfg = wl.target.cfg
+    r = measure_batched(a, wl, ctx, target, draft, B, a.steps, a.warmup)
     metric = (f"accepted tok/s + verify-step µs, {cfg.hidden}-hidden {KIND_NAMES[wl.target_kind]} target + draft, "
-              f"k={k}, bs={B}")
+              f"k={wl.k}, bs={B}")
     line = {
-        "metric": metric, "value": round(value, 2), "unit": "tok/s", "n_gpus": 1, "steps": a.steps,
-        "warmup": a.warmup, "ms_per_step": round(elapsed / a.steps * 1e3, 4), "higher_is_better": True,
+        "metric": metric, "value": r["value"], "unit": "tok/s", "n_gpus": 1, "steps": a.steps,
+        "warmup": a.warmup, "ms_per_step": r["ms_per_step"], "higher_is_better": True,
         "scaling": "weak", "vs_baseline": None, "dtype": KIND_NAMES[wl.target_kind], "data": "synthetic",
-        "config": {"workload": f"{wl.name}: {KIND_NAMES[wl.target_kind]} target ({cfg.layers} layers, hidden "
-                               f"{cfg.hidden}) + bf16 draft, k={k}, {B} sequences, contexts {lo}-{hi}, "
-                               f"shuffled 16-token blocks", "batch": B, "k": k},
-        "verify_step_us": round(verify_us, 2), "draft_us": round(draft_us, 2), "acceptance": round(acceptance, 4),
-        "roofline": roofline, "cpu_baseline": None, "parity": None,
+        "config": {"workload": r["workload"], "batch": B, "k": wl.k},
+        "verify_step_us": r["verify_step_us"], "draft_us": r["draft_us"], "acceptance": r["acceptance"],
+        "roofline": r["roofline"], "cpu_baseline": None, "parity": None,
     }
     print(json.dumps(line), flush=True)
     return 0

@@ -22,7 +22,7 @@ ROOT = PKG.parent
 CSRC = PKG / "csrc"
 OBJ = PKG / "_build"
 LIB = PKG / "libferro_gpu.so"
-SOURCES = ["kernels.hip", "pfwd.hip", "sampling.hip", "quant.hip", "api.hip"]
+SOURCES = ["kernels.hip", "sampling.hip", "quant.hip", "api.hip"]
 HOST_SOURCES = ["host.cpp"]  # plain C++ (g++), no contraction: exact load-time arithmetic
 ARCH = os.environ.get("FERRO_OFFLOAD_ARCH", "gfx950")
 

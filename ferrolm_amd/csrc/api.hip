@@ -5,7 +5,6 @@
 #include "ferro_gpu.h"
 #include "ferro_host.h"
 #include "internal.h"
-#include "pfwd.h"
 
 #include <algorithm>
 #include <mutex>
@@ -95,26 +94,6 @@ struct fg_ctx {
     // split-K GEMV meeting counters (GemvArgs::gcnt): zeroed once here, left at
     // zero by every launch's last workgroups
     unsigned* gcnt = nullptr;
-    // the persistent forward (pfwd.hip; opt-in, FERRO_PFWD=1): per model
-    // its barrier counters and control words (epoch, finished workgroups,
-    // abort), one exchange buffer for every model, and pinned words the abort
-    // flags are read back into after a step
-    bool pfwd = true;
-    struct PfState {
-        uint64_t serial = 0;  // the model's serial number (0: free)
-        unsigned* bar = nullptr;
-        int nbar = 0;
-        unsigned* ctl = nullptr;
-        uint64_t used = 0;
-    };
-    static constexpr int kPfStates = 4;
-    PfState pfs[kPfStates];
-    uint64_t pf_clock = 0;
-    float* pf_x = nullptr;
-    size_t pf_x_cap = 0;  // floats
-    unsigned* pf_abort = nullptr;  // pinned, one word per state
-    int pf_groups = 0;             // workgroups of a launch (all resident at once; 0: not usable)
-    int pf_spin = kPfSpin;         // polls a wait may take (FERRO_PFWD_SPIN: the time-out path's test)
     // GEMV launch profiling (fg_profile)
     bool prof = false;
     std::vector<hipEvent_t> pev;
@@ -212,15 +191,6 @@ static std::atomic<uint64_t> g_serial{1};
 
 struct fg_model {
     uint64_t serial = g_serial++;
-    // the persistent forward (made on first use): 1 eligible, -1 not, 0 not yet known;
-    // the weight kind of every layer matrix, the layer records with their work
-    // units, the LDS sizes and the exchange layout
-    int pf_ok = 0;
-    int pf_kind = 0;
-    PfLayer* pf_layers = nullptr;
-    int pf_xk = 0, pf_pkb = 0;
-    int pf_gl = 0;  // workgroups that run the layers
-    PfXch pf_xo{};
     fg_config cfg{};
     std::vector<DLayer> layers;
     uint16_t* embed = nullptr;
@@ -1005,24 +975,6 @@ int fg_ctx_create(int device, fg_ctx** out) {
     }
     HIPCHK(hipMemset(c->gcnt, 0, kGemvSplitGroups * 32 * sizeof(unsigned)));
     c->scratch = scratch_address(device);
-    // the persistent forward of single-sequence greedy steps is opt-in
-    // (FERRO_PFWD=1): on MI355X its barriers and exchanges cost more per stage
-    // than the step graphs' kernel boundaries; it needs every one of its
-    // kPfGroups workgroups resident at once
-    const char* npf = std::getenv("FERRO_PFWD");
-    c->pfwd = npf && npf[0] == '1';
-    if (c->pfwd) {
-        c->pf_groups = pfwd_init() == hipSuccess ? kPfGroups : 0;
-        int cus = 0;
-        if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess ||
-            cus < kPfGroups) {
-            (void)hipGetLastError();
-            c->pf_groups = 0;
-        }
-        if (!c->pf_groups) c->pfwd = false;
-        const char* sp = std::getenv("FERRO_PFWD_SPIN");
-        if (sp && std::atoi(sp) > 0) c->pf_spin = std::atoi(sp);
-    }
     const char* ng = std::getenv("FERRO_NO_GRAPH");
     c->graphs = !(ng && ng[0] == '1');
     const char* sm = std::getenv("FERRO_SEPARATE_MERGE");
@@ -1041,12 +993,6 @@ void fg_ctx_destroy(fg_ctx* c) {
     if (c->dmeta) (void)hipFree(c->dmeta);
     if (c->hmeta) (void)hipHostFree(c->hmeta);
     if (c->gcnt) (void)hipFree(c->gcnt);
-    for (auto& st : c->pfs) {
-        if (st.bar) (void)hipFree(st.bar);
-        if (st.ctl) (void)hipFree(st.ctl);
-    }
-    if (c->pf_x) (void)hipFree(c->pf_x);
-    if (c->pf_abort) (void)hipHostFree(c->pf_abort);
     for (auto& e : c->ev)
         if (e) (void)hipEventDestroy(e);
     for (auto& e : c->pev) (void)hipEventDestroy(e);
@@ -1152,7 +1098,6 @@ int fg_model_truncated(fg_ctx* ctx, const fg_model* base, int32_t layers, fg_mod
 
 void fg_model_destroy(fg_model* m) {
     if (!m) return;
-    if (m->pf_layers) (void)hipFree(m->pf_layers);
     if (m->owns)
         for (void* p : m->allocs) (void)hipFree(p);
     delete m;
@@ -1333,233 +1278,6 @@ static int check_sampling(const fg_sampling* p, int n, bool* wide) {
     return 0;
 }
 
-// ---------------------------------------------------------------------------
-// The persistent forward (pfwd.hip) of single-sequence greedy steps
-// ---------------------------------------------------------------------------
-// Work units of a layer matrix for `groups` workgroups: (ntg n-tiles) x (ks
-// slices of the chunks), at most one unit per workgroup. Chosen to carry the
-// fewest (tile, chunk) pairs per unit, counting at most one pair per wave as
-// equal (they cost one round trip), then the fewest slices, then the fewest
-// tiles; gate/up keeps whole interleave groups and no slices. False when no
-// choice fits.
-static bool pf_units(const DMat& d, int groups, int ntg_fixed, PfMat& m, int ks_max = 4) {
-    m = PfMat{d.w, d.s, d.kb, 1, 1, 0};
-    const int T = d.n_tiles, KC = d.kb / 4;
-    if (ntg_fixed) {
-        // whole interleave groups of ntg_fixed tiles, as few per unit as fit the grid
-        if (T % ntg_fixed) return false;
-        for (int ntg = ntg_fixed; ntg <= kPfMaxNtg; ntg += ntg_fixed) {
-            const int units = (T + ntg - 1) / ntg;
-            if (units <= groups) {
-                m.ntg = ntg;
-                m.units = units;
-                return true;
-            }
-        }
-        return false;
-    }
-    long best = -1;
-    for (int ntg = 1; ntg <= kPfMaxNtg; ntg++)
-        for (int ks : {1, 2, 4}) {
-            if (ks > KC || ks > ks_max) continue;
-            const int units = (T + ntg - 1) / ntg * ks;
-            if (units > groups) continue;
-            const long pairs = std::max<long>((long)ntg * ((KC + ks - 1) / ks), kPfWaves);
-            const long key = (pairs * 8 + ks) * 8 + ntg;
-            if (best < 0 || key < best) {
-                best = key;
-                m.ntg = ntg;
-                m.ks = ks;
-                m.units = units;
-            }
-        }
-    return best >= 0;
-}
-
-// Whether model m can run as one persistent launch, and (once) its layer
-// records: head_dim 64, at most kPfMaxGqa query heads per kv head, every layer
-// matrix of one weight kind (gate/up interleaved in 32-row groups for the
-// quantized kinds), a bf16 lm_head, work units that fit the grid and LDS that
-// fits a CU.
-static int pf_prepare(fg_ctx* ctx, fg_model* m) {
-    if (m->pf_ok) return 0;
-    m->pf_ok = -1;
-    const fg_config& c = m->cfg;
-    const int L = (int)m->layers.size();
-    // workgroups that run the layers: all of them (measured on the cfg2 draft:
-    // 32, 64 and 128 layer workgroups took 3892, 3648 and 3581 us per step
-    // against 3536 us at 256)
-    const int G = ctx->pf_groups;
-    if (!G || L < 1 || c.head_dim != 64 || c.heads % c.kv_heads || c.heads / c.kv_heads > kPfMaxGqa ||
-        c.kv_heads > G || c.hidden % 16 || c.intermediate % 16 || c.vocab % 16 || m->lm_head.kind != BF16 ||
-        m->lm_head.kb * 32 < c.hidden)
-        return 0;
-    const int kind = m->layers[0].wqkv.kind;
-    std::vector<PfLayer> h(L);
-    int xk = c.hidden, pkb = 0;
-    for (int i = 0; i < L; i++) {
-        const DLayer& l = m->layers[i];
-        for (const DMat* d : {&l.wqkv, &l.wo, &l.w_gate_up, &l.w_down})
-            if (d->kind != kind) return 0;
-        const int il = l.w_gate_up.il;
-        if (kind == BF16 ? (il != 16 && il != 32) : il != 32) return 0;
-        if (i > 0 && il != m->layers[0].w_gate_up.il) return 0;
-        PfLayer& y = h[i];
-        // the o and down partials are summed while the next input is staged: two slices at most
-        if (!pf_units(l.wqkv, G, 0, y.qkv) || !pf_units(l.wo, G, 0, y.o, 2) ||
-            !pf_units(l.w_gate_up, G, 2 * il / 16, y.gu) || !pf_units(l.w_down, G, 0, y.down, 2))
-            return 0;
-        y.attn_norm = l.attn_norm;
-        y.mlp_norm = l.mlp_norm;
-        y.bqkv = l.bqkv;
-        for (const PfMat* u : {&y.qkv, &y.o, &y.gu, &y.down}) pkb = std::max(pkb, 4 * ((u->kb / 4 + u->ks - 1) / u->ks));
-        for (const PfMat* u : {&y.o, &y.down}) xk = std::max(xk, 128 * ((u->kb / 4 + u->ks - 1) / u->ks));
-        if (y.qkv.ks != h[0].qkv.ks || y.o.ks != h[0].o.ks || y.down.ks != h[0].down.ks) return 0;
-    }
-    // the lm_head's bf16 pieces share the pieces buffer
-    pkb = std::max(pkb, kind == BF16 ? m->lm_head.kb : (m->lm_head.kb + 1) / 2 * 2);
-    if (kind != BF16) pkb = std::max(pkb, 2 * m->lm_head.kb);
-    xk = round_up(xk, 128);
-    if (pfwd_lds_bytes(kind, xk, pkb) > (size_t)kPfLdsMax) return 0;
-    const int qd = c.heads * 64, qkvd = qd + 2 * c.kv_heads * 64;
-    m->pf_xo = pfwd_xch(kind, L, c.hidden, c.intermediate, qd, qkvd, c.kv_heads, c.heads / c.kv_heads, h[0].qkv.ks,
-                        h[0].o.ks, h[0].down.ks, G, ctx->pf_groups);
-    m->pf_gl = G;
-    HIPCHK(hipMalloc((void**)&m->pf_layers, h.size() * sizeof(PfLayer)));
-    HIPCHK(hipMemcpy(m->pf_layers, h.data(), h.size() * sizeof(PfLayer), hipMemcpyHostToDevice));
-    m->pf_kind = kind;
-    m->pf_xk = xk;
-    m->pf_pkb = pkb;
-    m->pf_ok = 1;
-    return 0;
-}
-
-// Whether plan P of model m runs as one persistent launch: greedy, one
-// sequence of 1 to kPfMaxRows new rows, logits of the last row (a draft round)
-// or of every row (a verify).
-static bool pf_eligible(fg_ctx* ctx, fg_model* m, int n_seqs, bool sampling, const Plan& P, bool verify) {
-    if (!ctx->pfwd || n_seqs != 1 || sampling || P.t < 1 || P.t > kPfMaxRows || P.S != (verify ? P.t : 1))
-        return false;
-    if (pf_prepare(ctx, m)) {
-        (void)hipGetLastError();
-        return false;
-    }
-    return m->pf_ok > 0;
-}
-
-// Clears a state's counters and control words and restarts its epoch at 1 (no
-// launch of it may be in flight).
-static int pf_reset(fg_ctx::PfState& st) {
-    HIPCHK(hipMemset(st.bar, 0, (size_t)st.nbar * kPfCounters * kPfCounterWords * sizeof(unsigned)));
-    HIPCHK(hipMemset(st.ctl, 0, kPfCtlWords * sizeof(unsigned)));
-    const unsigned one = 1;
-    HIPCHK(hipMemcpy(st.ctl + kPfCtlEpoch, &one, sizeof(one), hipMemcpyHostToDevice));
-    return 0;
-}
-
-// The state of model m (its counters for every barrier of one launch, zeroed
-// at epoch 1 when new) and an exchange buffer that holds its layout. Runs
-// before any capture; *si is the state's index.
-static int pf_setup(fg_ctx* ctx, const fg_model* m, int* si) {
-    const int nbar = pfwd_barriers((int)m->layers.size());
-    int rc;
-    if (!ctx->pf_abort) {
-        HIPCHK(hipHostMalloc((void**)&ctx->pf_abort, fg_ctx::kPfStates * sizeof(unsigned), hipHostMallocDefault));
-        for (int i = 0; i < fg_ctx::kPfStates; i++) ctx->pf_abort[i] = 0;
-    }
-    int pick = -1;
-    for (int i = 0; i < fg_ctx::kPfStates; i++)
-        if (ctx->pfs[i].serial == m->serial) pick = i;
-    if (pick < 0) {
-        HIPCHK(hipStreamSynchronize(ctx->stream));
-        pick = 0;
-        for (int i = 0; i < fg_ctx::kPfStates; i++)
-            if (ctx->pfs[i].used < ctx->pfs[pick].used) pick = i;
-        fg_ctx::PfState& st = ctx->pfs[pick];
-        if (st.nbar < nbar) {
-            if (st.bar) HIPCHK(hipFree(st.bar));
-            st.bar = nullptr;
-            st.nbar = 0;
-            HIPCHK(hipMalloc((void**)&st.bar, (size_t)nbar * kPfCounters * kPfCounterWords * sizeof(unsigned)));
-            st.nbar = nbar;
-        }
-        if (!st.ctl) HIPCHK(hipMalloc((void**)&st.ctl, kPfCtlWords * sizeof(unsigned)));
-        st.serial = m->serial;
-        drop_graphs(ctx);  // step graphs bake the states' addresses in
-        if ((rc = pf_reset(st))) return rc;
-    }
-    ctx->pfs[pick].used = ++ctx->pf_clock;
-    if (m->pf_xo.total > ctx->pf_x_cap) {
-        HIPCHK(hipStreamSynchronize(ctx->stream));
-        drop_graphs(ctx);
-        if (ctx->pf_x) HIPCHK(hipFree(ctx->pf_x));
-        ctx->pf_x = nullptr;
-        ctx->pf_x_cap = 0;
-        HIPCHK(hipMalloc((void**)&ctx->pf_x, m->pf_xo.total * sizeof(float)));
-        ctx->pf_x_cap = m->pf_xo.total;
-    }
-    *si = pick;
-    return 0;
-}
-
-// One persistent launch of model m over t rows of one sequence: positions from
-// device word *pos0 on, tokens tok[row * tok_stride], block table `blocks`;
-// the argmax of the last logits_rows rows into am (and aux[aux_off], stride
-// aux_stride); with k > 0 the greedy accept of the verify tokens vtok into
-// out / cnt / acc.
-static void pf_launch(fg_ctx* ctx, const fg_model* m, int si, fg_kv* kv, int t, const int32_t* pos0,
-                      const int32_t* blocks, const uint32_t* tok, int tok_stride, int logits_rows, uint32_t* am,
-                      uint32_t* aux, int aux_stride, int aux_off, int k, const uint32_t* vtok, uint32_t* out,
-                      int32_t* cnt, int32_t* acc) {
-    const fg_config& c = m->cfg;
-    PfArgs a{};
-    a.layers = m->pf_layers;
-    a.L = (int)m->layers.size();
-    a.kc = kv->k;
-    a.vc = kv->v;
-    a.layer_floats = kv->layer_floats();
-    a.H = c.hidden;
-    a.I = c.intermediate;
-    a.nh = c.heads;
-    a.nkv = c.kv_heads;
-    a.qd = c.heads * 64;
-    a.kvd = c.kv_heads * 64;
-    a.V = c.vocab;
-    a.il = m->layers[0].w_gate_up.il;
-    a.eps = c.rms_eps;
-    a.scale = 1.0f / sqrtf(64.0f);
-    a.embed = m->embed;
-    a.lm = m->lm_head.w;
-    a.lm_kb = m->lm_head.kb;
-    a.norm = m->norm;
-    a.cos_t = m->cos_t;
-    a.sin_t = m->sin_t;
-    a.t = t;
-    a.pos0 = pos0;
-    a.tok = tok;
-    a.tok_stride = tok_stride;
-    a.blocks = blocks;
-    a.logits_rows = logits_rows;
-    a.xk = m->pf_xk;
-    a.pkb = m->pf_pkb;
-    a.x = ctx->pf_x;
-    a.xo = m->pf_xo;
-    a.bar = ctx->pfs[si].bar;
-    a.ctl = ctx->pfs[si].ctl;
-    a.spin = ctx->pf_spin;
-    a.gl = m->pf_gl;
-    a.am = am;
-    a.aux = aux;
-    a.aux_stride = aux_stride;
-    a.aux_off = aux_off;
-    a.k = k;
-    a.vtok = vtok;
-    a.out = out;
-    a.cnt = cnt;
-    a.acc = acc;
-    launch_pfwd(ctx->stream, m->pf_kind, ctx->pf_groups, a);
-}
-
 // chunks (n_chunks, greedy only): other sequences' prefill chunks and plain
 // rows, carried by the verify forward after the verify rows (Engine::execute's
 // one target pass); chunk_am gets the argmax of their FG_LOGITS_LAST rows.
@@ -1624,19 +1342,6 @@ static int spec_step(fg_ctx* ctx, const fg_model* target, fg_kv* tkv, const fg_m
     }
     const size_t o_vtok = words;
     words += (size_t)n_seqs * K1 + c_rows + 64;
-    // persistent launches (one sequence): the draft rounds' first positions (k
-    // words) and the draft's block table, then the verify's first position and
-    // the target's block table (room rounded up to 64 blocks, so the layout and
-    // a step graph keyed on it change only every 1024 positions)
-    std::vector<bool> pd(k, false);
-    bool any_pd = false;
-    for (int r = 0; r < k; r++)
-        any_pd |= (pd[r] = pf_eligible(ctx, const_cast<fg_model*>(draft), n_seqs, sampling, plans[r], false));
-    const bool pv = n_chunks == 0 && pf_eligible(ctx, const_cast<fg_model*>(target), n_seqs, sampling, plans[k], true);
-    const size_t o_dbt = words;
-    if (any_pd) words += (size_t)k + ((size_t)seqs[0].n_draft_blocks + 63) / 64 * 64 + 64;
-    const size_t o_tbt = words;
-    if (pv) words += 1 + ((size_t)seqs[0].n_blocks + 63) / 64 * 64 + 64;
     // sampling: parameters and generator states (uploaded with the plans; the
     // states come back with the outputs)
     words = (words + 15) / 16 * 16;  // 64-byte aligned parameters and states
@@ -1656,18 +1361,6 @@ static int spec_step(fg_ctx* ctx, const fg_model* target, fg_kv* tkv, const fg_m
     if ((rc = ensure(&ctx->dmeta, &ctx->dmeta_cap, words * 4, ctx->stream, false))) return rc;
     int32_t* h = (int32_t*)ctx->hmeta;
     for (int r = 0; r <= k; r++) pack_plan(plans[r], h + base[r]);
-    int si_d = -1, si_t = -1;  // persistent states of the draft and the target
-    if (any_pd) {
-        if ((rc = pf_setup(ctx, draft, &si_d))) return rc;
-        for (int r = 0; r < k; r++) h[o_dbt + r] = r == 0 ? seqs[0].draft_pos : seqs[0].pos + r;
-        for (int b = 0; b < seqs[0].n_draft_blocks; b++) h[o_dbt + k + b] = (int32_t)seqs[0].draft_blocks[b];
-    }
-    if (pv) {
-        if ((rc = pf_setup(ctx, target, &si_t))) return rc;
-        h[o_tbt] = seqs[0].pos;
-        for (int b = 0; b < seqs[0].n_blocks; b++) h[o_tbt + 1 + b] = (int32_t)seqs[0].blocks[b];
-    }
-    if (any_pd && pv && si_d == si_t) return fail(FG_E_ARG, "draft and target must be different models");
     uint32_t* hv = (uint32_t*)(h + o_vtok);
     for (int s = 0; s < n_seqs; s++) {
         hv[s * K1] = seqs[s].tail[seqs[s].n_tail - 1];
@@ -1702,11 +1395,6 @@ static int spec_step(fg_ctx* ctx, const fg_model* target, fg_kv* tkv, const fg_m
             const int stride = r == 0 ? 1 : K1;
             // the draft's proposal d_{r+1} goes to verify row s, column r+1: the
             // greedy argmax, replaced by a draw for sampled sequences
-            if (pd[r]) {
-                pf_launch(ctx, draft, si_d, dkv, plans[r].t, dm + o_dbt + r, dm + o_dbt + k, tok, stride, 1,
-                          (uint32_t*)(dm + o_am), vtok, K1, r + 1, 0, nullptr, nullptr, nullptr, nullptr);
-                continue;
-            }
             int e = run_forward(ctx, draft, dkv, plans[r], meta, tok, stride, w, sampling ? w.logits : nullptr,
                                 (uint32_t*)(dm + o_am), vtok, K1, r + 1, nullptr);
             if (e) return e;
@@ -1719,12 +1407,6 @@ static int spec_step(fg_ctx* ctx, const fg_model* target, fg_kv* tkv, const fg_m
         return 0;
     };
     auto verify_phase = [&]() -> int {
-        if (pv) {
-            // the verify and the greedy accept in one persistent launch
-            pf_launch(ctx, target, si_t, tkv, K1, dm + o_tbt, dm + o_tbt + 1, vtok, 1, K1, (uint32_t*)(dm + o_am),
-                      nullptr, 0, 0, k, vtok, (uint32_t*)(dm + o_out), dm + o_cnt, dm + o_acc);
-            return 0;
-        }
         layout_work(target, plans[k], w, ctx->ws);
         int e = run_forward(ctx, target, tkv, plans[k], dm + base[k], vtok, 1, w, sampling ? w.logits : nullptr,
                             (uint32_t*)(dm + o_am), nullptr, 0, 0, nullptr);
@@ -1751,12 +1433,7 @@ static int spec_step(fg_ctx* ctx, const fg_model* target, fg_kv* tkv, const fg_m
                                     (int64_t)tkv->serial, (int64_t)dkv->serial, (int64_t)(uintptr_t)ctx->ws,
                                     (int64_t)ctx->ws_cap, (int64_t)(uintptr_t)ctx->dmeta, (int64_t)ctx->dmeta_cap,
                                     (int64_t)sampling, (int64_t)wide, (int64_t)(uintptr_t)ctx->sbuf,
-                                    (int64_t)ctx->sbuf_cap, (int64_t)(uintptr_t)ctx->pf_x, (int64_t)ctx->pf_x_cap,
-                                    (int64_t)o_out};
-        for (int r = 0; r < k; r++) sig.push_back((int64_t)pd[r]);
-        sig.push_back((int64_t)pv);
-        sig.push_back(si_d);
-        sig.push_back(si_t);
+                                    (int64_t)ctx->sbuf_cap, (int64_t)o_out};
         for (int r = 0; r <= k; r++) {
             const Plan& P = plans[r];
             for (int64_t v : {(int64_t)P.t, (int64_t)P.S, (int64_t)P.Wc, (int64_t)P.words, (int64_t)P.ns,
@@ -1815,25 +1492,7 @@ static int spec_step(fg_ctx* ctx, const fg_model* target, fg_kv* tkv, const fg_m
     HIPCHK(hipGetLastError());
     HIPCHK(hipEventRecord(ctx->ev[2], ctx->stream));
     HIPCHK(hipMemcpyAsync(h + o_rng, dm + o_rng, (words - o_rng) * 4, hipMemcpyDeviceToHost, ctx->stream));
-    for (int si : {si_d, si_t})
-        if (si >= 0)
-            HIPCHK(hipMemcpyAsync(ctx->pf_abort + si, ctx->pfs[si].ctl + kPfCtlAbort, sizeof(unsigned),
-                                  hipMemcpyDeviceToHost, ctx->stream));
     HIPCHK(hipStreamSynchronize(ctx->stream));
-    bool aborted = false;
-    for (int si : {si_d, si_t})
-        if (si >= 0 && ctx->pf_abort[si]) aborted = true;
-    if (aborted) {
-        // a wait of a persistent launch timed out: its outputs are not valid; the
-        // states start over (every workgroup has finished)
-        for (int si : {si_d, si_t})
-            if (si >= 0) {
-                ctx->pf_abort[si] = 0;
-                if ((rc = pf_reset(ctx->pfs[si]))) return rc;
-            }
-        HIPCHK(hipDeviceSynchronize());
-        return fail(FG_E_DEVICE, "a persistent forward timed out waiting for its inputs");
-    }
     if (sampling) memcpy(rng, h + o_rng, (size_t)n_seqs * 8);
     memcpy(out_tokens, h + o_out, (size_t)n_seqs * K1 * 4);
     memcpy(out_count, h + o_cnt, (size_t)n_seqs * 4);

@@ -1,4 +1,4 @@
-// Device helpers shared by the kernel files (kernels.hip, pfwd.hip): vector
+// Device helpers of the hot-path kernels (kernels.hip): vector
 // types, non-temporal loads, bf16 conversion, the Cephes exp of the reference,
 // cross-lane reductions and the activation-piece conversions. Not part of the
 // public interface.

@@ -2,7 +2,10 @@
 activation pieces in the library's static device scratch instead of the
 context workspace. Its output must equal fg_matmul_device's bit for bit
 (the same kernels), on two calls in a row with the second on fewer rows,
-for each weight format; inputs beyond its limits are refused.
+for each weight format, through the multi-pass GEMVs (13 then 5 rows) and
+the one-pass ones (4 then 1 row: the decode GEMVs, the int4 16-wave kernel
+among them); inputs beyond its limits are refused, and a call at the limit
+of one pass still equals fg_matmul_device.
 
 Device buffers come from hipMalloc of the HIP runtime the library itself
 uses (the caller's allocations, not the entry point's); the library's
@@ -57,14 +60,15 @@ def call(fn, ctx, mat, x, m, y):
     gpu.check(fn(ctx.h, mat.h, x, m, y))
 
 
+@pytest.mark.parametrize("rows_pair", [(13, 5), (4, 1)])
 @pytest.mark.parametrize("kind", [BF16, INT8, INT4])
-def test_matches_the_allocating_entry_point(ctx, kind):
+def test_matches_the_allocating_entry_point(ctx, kind, rows_pair):
     hip = Hip()
     rows, cols = 768, 2048
     mat = gpu.Mat(ctx, matrix(kind, rows, cols, 7 + kind))
     lib = gpu.lib()
     nan = np.full((16, rows), np.nan, np.float32)
-    for m in (13, 5):  # two calls in a row, the second on fewer rows
+    for m in rows_pair:  # two calls in a row, the second on fewer rows
         x_np = np.random.default_rng(m).standard_normal((m, cols)).astype(np.float32)
         x, want, got = hip.alloc(x_np.nbytes), hip.alloc(nan.nbytes), hip.alloc(nan.nbytes)
         try:
@@ -85,15 +89,18 @@ def test_refuses_beyond_its_limits(ctx):
     hip = Hip()
     lib = gpu.lib()
     wide = gpu.Mat(ctx, matrix(BF16, 32, 16384, 3))  # 512 k-blocks: 4 passes need 2.1 MB
-    x, y = hip.alloc(16 * 16384 * 4), hip.alloc(16 * 32 * 4)
+    x, y, want = hip.alloc(16 * 16384 * 4), hip.alloc(16 * 32 * 4), hip.alloc(16 * 32 * 4)
     try:
-        hip.put(x, np.zeros((16, 16384), np.float32))
+        hip.put(x, np.random.default_rng(11).standard_normal((16, 16384)).astype(np.float32))
         with pytest.raises(gpu.FgError, match="2 MiB scratch"):
             call(lib.fg_matmul_device_noalloc, ctx, wide, x, 13, y)
         with pytest.raises(gpu.FgError, match="at most 15 rows"):
             call(lib.fg_matmul_device_noalloc, ctx, wide, x, 16, y)
         call(lib.fg_matmul_device_noalloc, ctx, wide, x, 4, y)  # one pass fits
+        call(lib.fg_matmul_device, ctx, wide, x, 4, want)
         ctx.sync()
-        assert np.array_equal(hip.get(y, (4, 32)), np.zeros((4, 32), np.float32))
+        g, w = hip.get(y, (4, 32)), hip.get(want, (4, 32))
+        assert np.isfinite(w).all() and np.abs(w).max() > 0
+        assert np.array_equal(g.view(np.uint32), w.view(np.uint32))
     finally:
-        hip.free(x, y)
+        hip.free(x, y, want)
