@@ -91,6 +91,7 @@ struct fg_ctx {
     hipEvent_t ev[3] = {nullptr, nullptr, nullptr};
     float last_us[3] = {0, 0, 0};
     bool merge_in_o = true;  // small bf16 output projections merge the attention spans themselves
+    bool mlp_fuse = true;    // bf16 layers of one pass fuse gate/up and down (EPI_MLP)
     // split-K GEMV meeting counters (GemvArgs::gcnt): zeroed once here, left at
     // zero by every launch's last workgroups
     unsigned* gcnt = nullptr;
@@ -599,9 +600,11 @@ static void pack_plan(const Plan& P, int32_t* h) {
 // Workspace of one forward pass over a plan.
 struct Work {
     float *x, *ss, *qkv, *apart, *logits;
+    float* x2;  // the fused MLP's layer input x + acc (formed by the next q/k/v, read by its o projection)
     float* kpart;  // GEMM split-K partial tiles (steps of more than kGemvRows rows)
     size_t kpart_cap;
     float* gpart;  // GEMV split-K partial tiles (decode steps of one pass)
+    long long* acc;  // the fused MLP's residual accumulator (steps of one pass): [kAccCopies][4][hidden]
     void* pa[2];   // activation pieces, ping-pong: each kernel reads one and writes the other
     float* pxs[2];
     float2* best;
@@ -674,6 +677,28 @@ static bool merge_in_o(const fg_config& c, const Plan& P, const DMat& wo, bool m
     return part_bytes <= 160 * 1024;
 }
 
+// Whether the layers of a forward fuse gate/up and down (EPI_MLP: each gate/up
+// workgroup multiplies its channels' activations by their columns of the down
+// projection and adds the result to a fixed-point accumulator; the next
+// layer's q/k/v forms x + acc and its norm itself, AX): bf16 layers, one pass
+// of at most 4 rows on the GEMV path, at most 1024 wide, no hidden-state or
+// calibration taps (x is complete only at the next layer's q/k/v). One launch
+// less per layer but the last: the 135M draft's rounds.
+static bool mlp_fuse(const fg_ctx* ctx, const fg_model* m, const Plan& P, bool mm) {
+    const fg_config& c = m->cfg;
+    if (!ctx->mlp_fuse || mm || P.t < 1 || P.t > 4 || c.hidden > 1024 || c.hidden % 8 || m->layers.size() < 2)
+        return false;
+    for (const DLayer& l : m->layers) {
+        if (l.wqkv.kind != BF16 || l.w_gate_up.kind != BF16 || l.w_down.kind != BF16 || l.w_gate_up.il != 16 ||
+            l.w_down.rows != c.hidden || l.w_down.cols != c.intermediate)
+            return false;
+        // the down columns of a gate/up group: 32 items per n-tile, at most four per thread
+        const int wv = std::max(1, std::min(8, l.w_gate_up.kb / 4));
+        if ((l.w_down.rows / 16) * 32 > 4 * 64 * wv || l.wqkv.kb > 32) return false;
+    }
+    return true;
+}
+
 static size_t layout_work(const fg_model* m, const Plan& P, Work& w, void* base) {
     const fg_config& c = m->cfg;
     const int t = P.t, H = c.hidden, S = std::max(P.S, 1);
@@ -700,6 +725,8 @@ static size_t layout_work(const fg_model* m, const Plan& P, Work& w, void* base)
     w.kpart = w.kpart_cap ? cv.take<float>(w.kpart_cap) : nullptr;
     // GEMV split K: [group][split][16 rows][group columns] over the hidden columns
     w.gpart = w.passes == 1 ? cv.take<float>((size_t)kGemvSplitMax * 16 * H) : nullptr;
+    w.acc = w.passes == 1 ? cv.take<long long>((size_t)kAccCopies * 4 * H) : nullptr;
+    w.x2 = w.passes == 1 ? cv.take<float>((size_t)4 * H) : nullptr;
     return cv.off + 256;
 }
 
@@ -784,6 +811,7 @@ static int run_forward(fg_ctx* ctx, const fg_model* m, fg_kv* kv, const Plan& P,
     bool sel_all = P.S == t;
     for (int i = 0; sel_all && i < P.S; i++) sel_all = P.sel[i] == i;
     int ss_cols = 32;  // columns per sum-of-squares partial in w.ss (the embedding writes one per k-block)
+    const bool fuse = w.acc && !hidden_host && !cap && mlp_fuse(ctx, m, P, mm);
     // calibration capture: per layer the four projection inputs [t][H], [t][qd], [t][H], [t][inter]
     const int qd = nh * hd;
     const size_t cap_layer = (size_t)t * (2 * H + qd + c.intermediate);
@@ -803,6 +831,16 @@ static int run_forward(fg_ctx* ctx, const fg_model* m, fg_kv* kv, const Plan& P,
         g.eps = c.rms_eps;
         g.nt = narrow_nt(l.wqkv, false);
         g.mm = mm;
+        if (fuse && li > 0) {
+            // the previous layer's MLP left its output in the accumulator
+            g.ax = true;
+            g.acc = w.acc;
+            g.acc_ld = H;
+            g.g_in = l.attn_norm;
+            g.x = w.x;
+            g.x_alt = w.x2;
+            g.ldx = H;
+        }
         gemv(ctx, EPI_QKV, l.wqkv, g);
         // attention (RoPE, cache write) and the merge into wo's pieces
         aa.kc = kv->k + li * kv->layer_floats();
@@ -826,6 +864,7 @@ static int run_forward(fg_ctx* ctx, const fg_model* m, fg_kv* kv, const Plan& P,
             g.aqm = attn_qmax(hd);
         }
         g.x = w.x;
+        if (fuse && li > 0) g.x_alt = w.x2;  // the layer input x + acc, formed by this layer's q/k/v
         g.ldx = H;
         g.ss_out = w.ss;
         g.ss_m = t;
@@ -843,9 +882,33 @@ static int run_forward(fg_ctx* ctx, const fg_model* m, fg_kv* kv, const Plan& P,
             g.gcnt = ctx->gcnt;
         }
         ss_cols = mm ? 64 : 16 * g.nt;
+        const bool fuse_l = fuse && li + 1 < L;
+        if (fuse_l) {
+            g.acc = w.acc;  // zeroed here for the fused MLP
+            g.acc_ld = H;
+        }
         gemv(ctx, EPI_RESID, l.wo, g);
         if (cap) launch_cap_norm(st, w.x, t, H, l.mlp_norm, c.rms_eps, capl + (size_t)t * (H + qd), H);
         cur ^= 1;
+        if (fuse_l) {
+            // gate/up, SiLU and down in one launch, into the accumulator
+            g = gemv_args(l.w_gate_up, pieces(w, cur, l.w_gate_up.kb, passes), t, w);
+            g.ss_in = w.ss;
+            g.ss_tiles = (H + ss_cols - 1) / ss_cols;
+            g.ss_m = t;
+            g.hidden = H;
+            g.eps = c.rms_eps;
+            g.il = l.w_gate_up.il;
+            g.acc = w.acc;
+            g.acc_ld = H;
+            g.W2 = (const uint8_t*)l.w_down.w;
+            g.N2 = l.w_down.rows;
+            g.KB2 = l.w_down.kb;
+            gemv(ctx, EPI_MLP, l.w_gate_up, g);
+            cur ^= 1;
+            cur ^= 1;
+            continue;
+        }
         // gate/up with SiLU; pieces of the activation for down
         g = gemv_args(l.w_gate_up, pieces(w, cur, l.w_gate_up.kb, passes), t, w);
         g.ss_in = w.ss;
@@ -979,6 +1042,8 @@ int fg_ctx_create(int device, fg_ctx** out) {
     c->graphs = !(ng && ng[0] == '1');
     const char* sm = std::getenv("FERRO_SEPARATE_MERGE");
     c->merge_in_o = !(sm && sm[0] == '1');
+    const char* nf = std::getenv("FERRO_NO_MLP_FUSE");
+    c->mlp_fuse = !(nf && nf[0] == '1');
     *out = c;
     return 0;
 }

@@ -17,6 +17,7 @@ typedef uint16_t u16x8 __attribute__((ext_vector_type(8)));
 typedef int8_t i8x8 __attribute__((ext_vector_type(8)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef long long i64x2 __attribute__((ext_vector_type(2)));
 
 // A load marked non-temporal (NT) or plain. Data read once per step (quantized
 // weights and their scales, the lm_heads, the KV cache) is loaded

@@ -78,7 +78,18 @@ enum Epi {
     EPI_RESID = 2,   // x += y; sum of squares per (k-block, row); pieces of g * x for the next consumer
     EPI_SILU = 3,    // silu(gate * rinv) * (up * rinv) -> pieces for the down projection
     EPI_ARGMAX = 4,  // logits y * rinv (optionally stored) -> per 32-column tile (max, index)
+    EPI_MLP = 5,     // silu(gate * rinv) * (up * rinv) of the group's channels, times their columns
+                     // of the down projection, added to the residual accumulator (GemvArgs::acc)
 };
+
+// The fused MLP of a bf16 layer (EPI_MLP) leaves the down projection's output
+// in a fixed-point accumulator instead of x: int64 sums of round(y * 2^kAccFrac),
+// exact and so independent of the order the workgroups add in. Each workgroup
+// adds into copy blockIdx.x % kAccCopies (the workgroups of one XCD share a
+// copy, so the atomics of different XCDs do not contend); a consumer sums the
+// copies. Layout [copy][row (4)][acc_ld]. Range: |y| < 2^26.
+constexpr int kAccCopies = 8;
+constexpr int kAccFrac = 36;
 
 struct GemvArgs {
     const uint8_t* W = nullptr;
@@ -132,6 +143,21 @@ struct GemvArgs {
     const float* apart = nullptr;
     const int32_t* amrec = nullptr;
     int anh = 0, ankv = 0, ahd = 0, aqm = 0;
+    // The residual accumulator of a fused MLP (kAccCopies copies of [4][acc_ld]).
+    // EPI_MLP adds into it; EPI_RESID (the output projection before it) zeroes the
+    // group's columns of every copy; with ax (EPI_QKV of the next layer) the
+    // input rows are x + the copies' sum, normed here (g_in, hidden, eps) into
+    // the operand, and stored to x_alt (not to x, which the launch's other
+    // workgroups are still reading). EPI_RESID reads its residual rows from
+    // x_alt when set (then writes the sum to x as always).
+    long long* acc = nullptr;
+    int acc_ld = 0;
+    bool ax = false;
+    const float* g_in = nullptr;
+    float* x_alt = nullptr;
+    // EPI_MLP: the down projection (bf16, the device layout) of N2 outputs, KB2 k-blocks
+    const uint8_t* W2 = nullptr;
+    int N2 = 0, KB2 = 0;
 };
 
 // start/stop (optional) are recorded by the dispatch itself (hipExtLaunchKernelGGL),

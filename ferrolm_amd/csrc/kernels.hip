@@ -306,7 +306,11 @@ void launch_embed(hipStream_t st, const uint32_t* tokens, int stride, const uint
 // AM: the input is the attention output, merged by the workgroup itself from
 // the span partials (instead of a separate merge kernel writing pieces):
 // bf16 weights, one pass, at most 1024 inputs.
-template <int KIND, int NT, int EPI, int PG, int WMAX = 8, bool AM = false>
+// AX: the input is the residual x plus the fixed-point accumulator of the
+// previous layer's fused MLP, normed by the workgroup itself (sum of squares
+// over the whole row, 1/rms in the epilogue, g_in as the norm weight): bf16
+// q/k/v, one pass, at most 1024 inputs; x + acc is stored to x_alt.
+template <int KIND, int NT, int EPI, int PG, int WMAX = 8, bool AM = false, bool AX = false>
 __global__ __launch_bounds__(64 * WMAX) void k_gemv(const GemvArgs a) {
     constexpr bool Q = KIND != BF16;
     // weights read once per step: quantized ones and the lm_heads (non-temporal loads)
@@ -315,11 +319,12 @@ __global__ __launch_bounds__(64 * WMAX) void k_gemv(const GemvArgs a) {
     // flight; with 16 waves (4 per SIMD, 128 VGPRs) half as many, the other waves
     // of the SIMD covering each one's wait
     constexpr int U = PG == 1 ? (KIND == INT4 ? 4 : NT >= 6 ? 1 : 2) / (WMAX == 16 ? 2 : 1) : 1;
-    constexpr bool NEED_R = EPI == EPI_QKV || EPI == EPI_SILU || EPI == EPI_ARGMAX;
+    // 1/rms of the input rows from the producers' sum-of-squares partials (AX forms its own)
+    constexpr bool NEED_R = (EPI == EPI_QKV || EPI == EPI_SILU || EPI == EPI_ARGMAX || EPI == EPI_MLP) && !AX;
     constexpr int YS = NT * 16 > 64 ? NT * 16 : 64;  // row stride of the output tile in LDS
     // finished output columns per group (EPI_RESID, EPI_SILU): 16 or 32, a half
-    // or a whole k-block of the next consumer
-    constexpr int OC = EPI == EPI_SILU ? NT * 8 : NT * 16;
+    // or a whole k-block of the next consumer; EPI_MLP: its channels
+    constexpr int OC = EPI == EPI_SILU || EPI == EPI_MLP ? NT * 8 : NT * 16;
     __shared__ float red[WMAX * NT * PG * 64];
     __shared__ __align__(16) float yt[16 * YS];
     __shared__ float rs[16];
@@ -327,8 +332,10 @@ __global__ __launch_bounds__(64 * WMAX) void k_gemv(const GemvArgs a) {
     __shared__ __align__(16) float et[16 * YS];  // epilogue inputs: x tile (EPI_RESID) or bias
     __shared__ __align__(16) float gs[32];       // g_next of this group's 32 columns (EPI_RESID)
     __shared__ __align__(16) float vt[16 * YS];  // finished values for the next consumer's pieces
-    constexpr int AMKB = 32;  // AM: the operand of up to 32 k-blocks, [kb][lane] bf16 pieces as in global memory
-    __shared__ __align__(16) u16x8 xm[AM ? AMKB * 64 : 1];
+    constexpr int AMKB = 32;  // AM, AX: the operand of up to 32 k-blocks, [kb][lane] bf16 pieces as in global memory
+    __shared__ __align__(16) u16x8 xm[AM || AX ? AMKB * 64 : 1];
+    static_assert(!AX || (KIND == BF16 && PG == 1 && EPI == EPI_QKV), "AX: bf16 q/k/v of one pass");
+    static_assert(EPI != EPI_MLP || (KIND == BF16 && PG == 1 && NT == 2), "EPI_MLP: bf16 gate/up of one pass");
 
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, W = blockDim.x >> 6;
     const int tile0 = blockIdx.x * NT;
@@ -416,12 +423,27 @@ __global__ __launch_bounds__(64 * WMAX) void k_gemv(const GemvArgs a) {
         pre[it] = 0.0f;
         if (idx < rows * COLS) {
             const int r = idx / COLS, cc = idx % COLS, row = pass0 * 4 + r;
-            if (EPI == EPI_RESID && row < a.m) pre[it] = a.x[(size_t)row * a.ldx + blockIdx.x * OC + cc];
+            if (EPI == EPI_RESID && row < a.m)
+                pre[it] = (a.x_alt ? a.x_alt : a.x)[(size_t)row * a.ldx + blockIdx.x * OC + cc];
             if ((EPI == EPI_QKV || EPI == EPI_STORE) && a.bias) pre[it] = a.bias[tile0 * 16 + cc];
         }
     }
     float gv = 1.0f;
     if (EPI == EPI_RESID && a.g_next && threadIdx.x < OC) gv = a.g_next[blockIdx.x * OC + threadIdx.x];
+    // EPI_MLP: the down projection's columns of this group's 16 channels (half
+    // of k-block blockIdx.x / 2: 512 bytes of each n-tile), requested now so
+    // they arrive with the gate/up weights; item i = (n-tile i / 32, lane 32 h +
+    // i % 32), items past the last re-read it (unconditional loads)
+    constexpr int DWI = EPI == EPI_MLP ? 4 : 1;
+    u32x4 dw[DWI];
+    if constexpr (EPI == EPI_MLP) {
+        const int n_items = (a.N2 >> 4) * 32, kb2 = blockIdx.x >> 1, hh = blockIdx.x & 1;
+#pragma unroll
+        for (int it = 0; it < DWI; it++) {
+            const int i = min((int)threadIdx.x + it * (int)blockDim.x, n_items - 1);
+            dw[it] = ((const u32x4*)a.W2)[((size_t)(i >> 5) * a.KB2 + kb2) * 64 + 32 * hh + (i & 31)];
+        }
+    }
 
     float accq[NT][PG];
     f32x4 accb[NT][PG];
@@ -594,6 +616,102 @@ __global__ __launch_bounds__(64 * WMAX) void k_gemv(const GemvArgs a) {
                 }
             }
         }
+    } else if constexpr (AX) {
+        // The wave's weights first; then per item (row slot, 8 inputs): x + acc
+        // (every copy requested before any is added; the copies sum exactly),
+        // stored to x_alt by one workgroup per item, the four bf16 pieces of
+        // g * (x + acc) straight into the operand (rows past m and inputs past
+        // the row: zero), and the row's sum of squares; the rows' 1/rms (the
+        // waves' sums in wave order) is needed only by the epilogue.
+        const int wv = __builtin_amdgcn_readfirstlane(wave);
+        const int a0 = wv * KC / W, a1 = (wv + 1) * KC / W;
+        bf16x8 wm[NT][4];
+        {
+            const int cc = min(a0, KC - 1);
+#pragma unroll
+            for (int t = 0; t < NT; t++)
+#pragma unroll
+                for (int j = 0; j < 4; j++)
+                    wm[t][j] = ((const bf16x8*)a.W)[((size_t)(tile0 + t) * KB + cc * 4 + j) * 64 + lane];
+        }
+        const int H = a.hidden, G8 = KB * 4;
+        float sq[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        for (int idx = threadIdx.x; idx < 4 * G8; idx += blockDim.x) {
+            const int r = idx / G8, kg = idx - r * G8, k0 = kg * 8;
+            float v[8];
+#pragma unroll
+            for (int e = 0; e < 8; e++) v[e] = 0.0f;
+            if (r < a.m && k0 < H) {  // H is a multiple of 8
+                const float* xp = a.x + (size_t)r * a.ldx + k0;
+                const float4 xv0 = *(const float4*)xp, xv1 = *(const float4*)(xp + 4);
+                i64x2 cv[kAccCopies][4];
+#pragma unroll
+                for (int c = 0; c < kAccCopies; c++)
+#pragma unroll
+                    for (int q = 0; q < 4; q++)
+                        cv[c][q] = *(const i64x2*)(a.acc + ((size_t)c * 4 + r) * a.acc_ld + k0 + 2 * q);
+                const float4 g0 = *(const float4*)(a.g_in + k0), g1 = *(const float4*)(a.g_in + k0 + 4);
+                const float xs[8] = {xv0.x, xv0.y, xv0.z, xv0.w, xv1.x, xv1.y, xv1.z, xv1.w};
+                const float gs8[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
+                const float unit = 1.0f / (float)(1ll << kAccFrac);
+                float xn[8], q2 = 0.0f;
+#pragma unroll
+                for (int e = 0; e < 8; e++) {
+                    long long sum = 0;
+#pragma unroll
+                    for (int c = 0; c < kAccCopies; c++) sum += cv[c][e >> 1][e & 1];
+                    xn[e] = xs[e] + (float)sum * unit;
+                    q2 = fmaf(xn[e], xn[e], q2);
+                    v[e] = gs8[e] * xn[e];
+                }
+                if (idx % (int)gridDim.x == (int)blockIdx.x) {
+                    float* op = a.x_alt + (size_t)r * a.ldx + k0;
+                    *(float4*)op = make_float4(xn[0], xn[1], xn[2], xn[3]);
+                    *(float4*)(op + 4) = make_float4(xn[4], xn[5], xn[6], xn[7]);
+                }
+#pragma unroll
+                for (int rr = 0; rr < 4; rr++)
+                    if (rr == r) sq[rr] += q2;
+            }
+            // the four pieces at once (bf16_piece's successive roundings)
+            u16x8 o[4];
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                float x = v[e];
+#pragma unroll
+                for (int pc = 0; pc < 4; pc++) {
+                    const uint32_t h = f32_to_bf16_bits(x);
+                    o[pc][e] = (uint16_t)h;
+                    x = x - bf16_bits_to_f32(h);
+                }
+            }
+#pragma unroll
+            for (int pc = 0; pc < 4; pc++) xm[(kg >> 2) * 64 + (kg & 3) * 16 + r * 4 + pc] = o[pc];
+        }
+        // (the partials go to rtmp, which nothing else uses here: red is
+        // rewritten by the waves' products while these are being summed)
+#pragma unroll
+        for (int rr = 0; rr < 4; rr++) {
+            const float v = group_reduce<64, false>(sq[rr]);
+            if (lane == 0) rtmp[wave * 4 + rr] = v;
+        }
+        __syncthreads();
+        if (threadIdx.x < 4) {
+            float v = 0.0f;
+            for (int w = 0; w < W; w++) v += rtmp[w * 4 + threadIdx.x];
+            rs[threadIdx.x] = 1.0f / sqrtf(v / (float)H + a.eps);
+        }
+        if (a0 < a1) {
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const u16x8 o = xm[(a0 * 4 + j) * 64 + lane];
+                bf16x8 ab;
+                __builtin_memcpy(&ab, &o, sizeof(ab));
+#pragma unroll
+                for (int t = 0; t < NT; t++)
+                    accb[t][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ab, wm[t][j], accb[t][0], 0, 0, 0);
+            }
+        }
     } else {
         int c = c0;
         for (; c + U <= c1; c += U) chunks(c, std::integral_constant<int, U>{});
@@ -614,6 +732,8 @@ __global__ __launch_bounds__(64 * WMAX) void k_gemv(const GemvArgs a) {
 #pragma unroll
     for (int it = 0; it < EPI_IT; it++) asm volatile("" : "+v"(pre[it]));
     asm volatile("" : "+v"(gv));
+#pragma unroll
+    for (int it = 0; it < DWI; it++) asm volatile("" : "+v"(dw[it]));
     if (NEED_R && rfast && (int)threadIdx.x < rslots) {
         // the 16 partials of a row sit in 16 consecutive lanes (whole waves take part)
         float v = 0.0f;
@@ -691,6 +811,47 @@ __global__ __launch_bounds__(64 * WMAX) void k_gemv(const GemvArgs a) {
         __syncthreads();
     }
 
+    if constexpr (EPI == EPI_MLP) {
+        // The activations of the group's 16 channels (the EPI_SILU arithmetic),
+        // then each output n of the down projection from these channels: an item
+        // holds 8 channels of one output (one fma chain), the other 8 sit in lane
+        // ^ 16 (row swap; both lanes end with the same sum), and the sum goes into
+        // this XCD's accumulator copy as round(y * 2^kAccFrac).
+        for (int idx = threadIdx.x; idx < rows * OC; idx += blockDim.x) {
+            const int r = idx / OC, cc = idx % OC, row = pass0 * 4 + r;
+            const float gt = yt[r * YS + cc] * rs[r], up = yt[r * YS + OC + cc] * rs[r];
+            vt[r * YS + cc] = row < a.m ? gt / (1.0f + dev_exp(-gt)) * up : 0.0f;
+        }
+        __syncthreads();
+        const int n_items = (a.N2 >> 4) * 32, qq = (lane >> 4) & 1;
+        long long* accp = a.acc + (size_t)(blockIdx.x % kAccCopies) * 4 * a.acc_ld;
+#pragma unroll
+        for (int it = 0; it < DWI; it++) {
+            const int i = (int)threadIdx.x + it * (int)blockDim.x;
+            const int n = (min(i, n_items - 1) >> 5) * 16 + (lane & 15);
+            float w8[8];
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                w8[2 * e] = bf16_bits_to_f32(dw[it][e] & 0xFFFFu);
+                w8[2 * e + 1] = bf16_bits_to_f32(dw[it][e] >> 16);
+            }
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                if (r >= rows) break;  // uniform
+                const float* vr = &vt[r * YS + 8 * qq];
+                float y = w8[0] * vr[0];
+#pragma unroll
+                for (int e = 1; e < 8; e++) y = fmaf(w8[e], vr[e], y);
+                y = reduce_rows<false, false>(y);
+                if (qq == 0 && i < n_items && pass0 * 4 + r < a.m) {
+                    const double d = fmin(fmax((double)y * (double)(1ll << kAccFrac), -4.0e18), 4.0e18);
+                    __hip_atomic_fetch_add(accp + (size_t)r * a.acc_ld + n, (long long)rint(d), __ATOMIC_RELAXED,
+                                           __HIP_MEMORY_SCOPE_AGENT);
+                }
+            }
+        }
+        return;
+    }
     if (EPI == EPI_STORE || EPI == EPI_QKV) {
 #pragma unroll
         for (int it = 0; it < EPI_IT; it++) {
@@ -747,6 +908,10 @@ __global__ __launch_bounds__(64 * WMAX) void k_gemv(const GemvArgs a) {
         if (EPI == EPI_RESID) {
             const float xn = live ? et[r * YS + cc] + yt[r * YS + cc] : 0.0f;
             if (live) a.x[(size_t)row * a.ldx + blockIdx.x * OC + cc] = xn;
+            // the fused MLP that follows adds into the accumulator: this group's columns start at zero
+            if (a.acc && live)
+#pragma unroll
+                for (int c = 0; c < kAccCopies; c++) a.acc[((size_t)c * 4 + row) * a.acc_ld + blockIdx.x * OC + cc] = 0;
             yt[r * YS + cc] = xn;
             vt[r * YS + cc] = a.g_next ? gs[cc] * xn : xn;
         } else {
@@ -1343,6 +1508,19 @@ static void gemv_kind(hipStream_t st, int epi, const DMat& w, const GemvArgs& a,
     switch (epi) {
         case EPI_STORE: gemv_pg<KIND, 2, EPI_STORE>(st, w, a, e0, e1); break;
         case EPI_QKV:
+            if constexpr (KIND == BF16) {
+                if (a.ax) {
+                    // input formed in the workgroup: one chunk per wave
+                    const int W = std::max(1, std::min(8, w.kb / 4));
+                    if (a.nt == 1)
+                        launch_timed(k_gemv<BF16, 1, EPI_QKV, 1, 8, false, true>, dim3(w.n_tiles, 1, 1), dim3(64 * W),
+                                     st, a, e0, e1);
+                    else
+                        launch_timed(k_gemv<BF16, 2, EPI_QKV, 1, 8, false, true>, dim3(w.n_tiles / 2, 1, 1),
+                                     dim3(64 * W), st, a, e0, e1);
+                    break;
+                }
+            }
             if (a.nt == 1)
                 gemv_pg<KIND, 1, EPI_QKV>(st, w, a, e0, e1);
             else
@@ -1372,6 +1550,12 @@ static void gemv_kind(hipStream_t st, int epi, const DMat& w, const GemvArgs& a,
                 gemv_pg<KIND, 2, EPI_SILU>(st, w, a, e0, e1);
             else
                 gemv_pg<KIND, 4, EPI_SILU>(st, w, a, e0, e1);
+            break;
+        case EPI_MLP:
+            if constexpr (KIND == BF16) {
+                const int W = std::max(1, std::min(8, w.kb / 4));
+                launch_timed(k_gemv<BF16, 2, EPI_MLP, 1>, dim3(w.n_tiles / 2, 1, 1), dim3(64 * W), st, a, e0, e1);
+            }
             break;
         case EPI_ARGMAX:
             // bf16 lm_head when decoding: 96 or 128 columns per group (fewer, fuller

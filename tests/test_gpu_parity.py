@@ -338,6 +338,59 @@ def test_output_projection_merge_matches_separate_merge(ctx, shape, monkeypatch)
         pos += len(toks)
 
 
+@pytest.mark.parametrize("shape", [(576, 9, 3, 64, 1536), (512, 4, 2, 128, 1024), (1024, 16, 4, 64, 2048)],
+                         ids=["draft-135m", "hd128", "wide1024"])
+def test_fused_mlp_matches_unfused_and_oracle(ctx, shape, monkeypatch):
+    """Decode steps of 1 to 4 rows on bf16 models fuse each layer's gate/up
+    and down but the last (EPI_MLP: the down projection's output summed
+    exactly in a fixed-point accumulator, 2^-36; the next q/k/v forms x + acc
+    and its norm, AX). A context created with FERRO_NO_MLP_FUSE=1 runs the
+    separate kernels. Logits and cache slots of the two agree to the rounding
+    of the different summation orders, and both agree with the oracle's to the
+    bars of the other forward tests; the greedy ids are equal (near-tie rule)."""
+    from ferrolm_amd.synth import random_model
+    from ferrolm_amd.weights import Config
+    hidden, heads, kv_heads, hd, inter = shape
+    cfg = Config(vocab=512, hidden=hidden, intermediate=inter, layers=4, heads=heads, kv_heads=kv_heads,
+                 head_dim=hd, rms_eps=1e-5, max_position=2048)
+    hm = random_model(cfg, seed=41, std=0.05)
+    monkeypatch.setenv("FERRO_NO_MLP_FUSE", "1")
+    ctx2 = gpu.Context()
+    monkeypatch.delenv("FERRO_NO_MLP_FUSE")
+    table, blocks = scattered_table(200)
+    rng = np.random.default_rng(42)
+    prompt = [int(x) for x in rng.integers(3, 500, 150)]
+    steps = [[int(x) for x in rng.integers(3, 500, n)] for n in (1, 2, 3, 4, 1)]
+    runs = []
+    for c in (ctx, ctx2):
+        m = gpu.Model(c, hm)
+        kv = gpu.KvCache(c, hm.cfg, blocks)
+        gpu.forward(c, m, kv, [(prompt, 0, table, gpu.LOGITS_LAST)])
+        outs, pos = [], len(prompt)
+        for toks in steps:
+            o = gpu.forward(c, m, kv, [(toks, pos, table, gpu.LOGITS_ALL)])
+            outs.append((o.logits, o.argmax))
+            pos += len(toks)
+        runs.append((outs, [kv.layer(i) for i in range(cfg.layers)]))
+        del kv, m
+    ctx2.close()
+    (o1, kv1), (o2, kv2) = runs
+    for (l1, a1), (l2, a2) in zip(o1, o2):
+        assert np.abs(l1 - l2).max() <= 1e-5 * np.abs(l2).max()
+    for (k1, v1), (k2, v2) in zip(kv1, kv2):
+        assert np.array_equal(k1 != 0, k2 != 0)
+        assert np.abs(k1 - k2).max() <= 1e-5 * np.abs(k2).max() and np.abs(v1 - v2).max() <= 1e-5 * np.abs(v2).max()
+    om = oracle.Model(hm)
+    okv = om.kv(blocks)
+    om.forward(okv, [(prompt, 0, table, 1)])
+    pos = len(prompt)
+    for toks, (lg, am) in zip(steps, o1):
+        ol = om.forward(okv, [(toks, pos, table, 2)])
+        assert np.abs(lg - ol).max() < 1e-4 * np.abs(ol).max()
+        assert_argmax_parity(am, ol)
+        pos += len(toks)
+
+
 @pytest.mark.parametrize("hd,heads,kv_heads,n", [(64, 16, 4, 1100), (128, 8, 2, 700), (64, 16, 16, 520)],
                          ids=["hd64", "hd128", "mha-hd64"])
 def test_long_gqa_prefill_runs_multi_span_attention(ctx, hd, heads, kv_heads, n):
