@@ -85,10 +85,13 @@ enum Epi {
 // The fused MLP of a bf16 layer (EPI_MLP) leaves the down projection's output
 // in a fixed-point accumulator instead of x: int64 sums of round(y * 2^kAccFrac),
 // exact and so independent of the order the workgroups add in. Each workgroup
-// adds into copy blockIdx.x % kAccCopies (the workgroups of one XCD share a
-// copy, so the atomics of different XCDs do not contend); a consumer sums the
-// copies. Layout [copy][row (4)][acc_ld]. Range: |y| < 2^26.
-constexpr int kAccCopies = 8;
+// adds into copy blockIdx.x % kAccCopies (workgroup w runs on XCD w % 8, so
+// the workgroups of two XCDs share a copy); a consumer sums the copies.
+// Fewer copies mean fewer bytes for the consumer, more for the atomics to
+// contend on. Measured on the 135M draft (cfg2, one box): 8 copies
+// 2119-2123 us of draft per step, 4: 2089-2091, 2: 2111-2113, 1: 2193-2195.
+// Layout [copy][row (4)][acc_ld]. Range: |y| < 2^26.
+constexpr int kAccCopies = 4;
 constexpr int kAccFrac = 36;
 
 struct GemvArgs {
