@@ -91,7 +91,7 @@ struct fg_ctx {
     hipEvent_t ev[3] = {nullptr, nullptr, nullptr};
     float last_us[3] = {0, 0, 0};
     bool merge_in_o = true;  // small bf16 output projections merge the attention spans themselves
-    bool mlp_fuse = true;    // bf16 layers of one pass fuse gate/up and down (EPI_MLP)
+    bool mlp_fuse = true;    // bf16 layers of one pass run fused (mlp_fuse: split output projection, EPI_MLP)
     // split-K GEMV meeting counters (GemvArgs::gcnt): zeroed once here, left at
     // zero by every launch's last workgroups
     unsigned* gcnt = nullptr;
@@ -604,7 +604,8 @@ struct Work {
     float* kpart;  // GEMM split-K partial tiles (steps of more than kGemvRows rows)
     size_t kpart_cap;
     float* gpart;  // GEMV split-K partial tiles (decode steps of one pass)
-    long long* acc;  // the fused MLP's residual accumulator (steps of one pass): [kAccCopies][4][hidden]
+    long long* acc;   // fused layers' accumulators (steps of one pass), [kAccCopies][4][hidden]:
+    long long* acc2;  // A (acc) the MLP's output, B (acc2) the output projection's
     void* pa[2];   // activation pieces, ping-pong: each kernel reads one and writes the other
     float* pxs[2];
     float2* best;
@@ -677,20 +678,26 @@ static bool merge_in_o(const fg_config& c, const Plan& P, const DMat& wo, bool m
     return part_bytes <= 160 * 1024;
 }
 
-// Whether the layers of a forward fuse gate/up and down (EPI_MLP: each gate/up
-// workgroup multiplies its channels' activations by their columns of the down
-// projection and adds the result to a fixed-point accumulator; the next
-// layer's q/k/v forms x + acc and its norm itself, AX): bf16 layers, one pass
-// of at most 4 rows on the GEMV path, at most 1024 wide, no hidden-state or
-// calibration taps (x is complete only at the next layer's q/k/v). One launch
-// less per layer but the last: the 135M draft's rounds.
+// Whether the layers of a forward run fused (all but the last): the output
+// projection split by head (k_o_heads: each workgroup merges one head's
+// attention spans) adds into a fixed-point accumulator, and gate/up, SiLU and
+// down run as one launch (EPI_MLP: each workgroup multiplies its channels'
+// activations by their columns of the down projection) whose prologue forms x +
+// that accumulator and its norm (AX) and whose output goes into a second
+// accumulator, which the next layer's q/k/v reads the same way. Four launches
+// per layer instead of five, and no workgroup reads every head's partials.
+// For bf16 layers of one pass of at most 4 rows on the GEMV path, at most 1024
+// wide, head dim 64 or 128, without hidden-state or calibration taps (x is
+// complete only inside the next layer's first launch): the 135M draft's rounds.
 static bool mlp_fuse(const fg_ctx* ctx, const fg_model* m, const Plan& P, bool mm) {
     const fg_config& c = m->cfg;
-    if (!ctx->mlp_fuse || mm || P.t < 1 || P.t > 4 || c.hidden > 1024 || c.hidden % 8 || m->layers.size() < 2)
+    if (!ctx->mlp_fuse || mm || P.t < 1 || P.t > 4 || c.hidden > 1024 || c.hidden % 8 || m->layers.size() < 2 ||
+        (c.head_dim != 64 && c.head_dim != 128))
         return false;
     for (const DLayer& l : m->layers) {
-        if (l.wqkv.kind != BF16 || l.w_gate_up.kind != BF16 || l.w_down.kind != BF16 || l.w_gate_up.il != 16 ||
-            l.w_down.rows != c.hidden || l.w_down.cols != c.intermediate)
+        if (l.wqkv.kind != BF16 || l.wo.kind != BF16 || l.w_gate_up.kind != BF16 || l.w_down.kind != BF16 ||
+            l.w_gate_up.il != 16 || l.w_down.rows != c.hidden || l.w_down.cols != c.intermediate ||
+            l.wo.rows != c.hidden)
             return false;
         // the down columns of a gate/up group: 32 items per n-tile, at most four per thread
         const int wv = std::max(1, std::min(8, l.w_gate_up.kb / 4));
@@ -726,6 +733,7 @@ static size_t layout_work(const fg_model* m, const Plan& P, Work& w, void* base)
     // GEMV split K: [group][split][16 rows][group columns] over the hidden columns
     w.gpart = w.passes == 1 ? cv.take<float>((size_t)kGemvSplitMax * 16 * H) : nullptr;
     w.acc = w.passes == 1 ? cv.take<long long>((size_t)kAccCopies * 4 * H) : nullptr;
+    w.acc2 = w.passes == 1 ? cv.take<long long>((size_t)kAccCopies * 4 * H) : nullptr;
     w.x2 = w.passes == 1 ? cv.take<float>((size_t)4 * H) : nullptr;
     return cv.off + 256;
 }
@@ -811,7 +819,15 @@ static int run_forward(fg_ctx* ctx, const fg_model* m, fg_kv* kv, const Plan& P,
     bool sel_all = P.S == t;
     for (int i = 0; sel_all && i < P.S; i++) sel_all = P.sel[i] == i;
     int ss_cols = 32;  // columns per sum-of-squares partial in w.ss (the embedding writes one per k-block)
+    // Fused layers (all but the last; mlp_fuse): the residual rows alternate
+    // between xb[0] and xb[1] (a stage that forms x + acc reads one and writes the
+    // other); accumulator B (w.acc2) takes the output projection, A (w.acc) the
+    // MLP. Each is cleared by the launch before the one that adds into it: B by
+    // the q/k/v, A by the output projection.
     const bool fuse = w.acc && !hidden_host && !cap && mlp_fuse(ctx, m, P, mm);
+    float* xb[2] = {w.x, w.x2};
+    int xc = 0;
+    const int acc_n = kAccCopies * 4 * H;
     // calibration capture: per layer the four projection inputs [t][H], [t][qd], [t][H], [t][inter]
     const int qd = nh * hd;
     const size_t cap_layer = (size_t)t * (2 * H + qd + c.intermediate);
@@ -831,27 +847,71 @@ static int run_forward(fg_ctx* ctx, const fg_model* m, fg_kv* kv, const Plan& P,
         g.eps = c.rms_eps;
         g.nt = narrow_nt(l.wqkv, false);
         g.mm = mm;
+        const bool fuse_l = fuse && li + 1 < L;
         if (fuse && li > 0) {
-            // the previous layer's MLP left its output in the accumulator
+            // the previous layer's MLP left its output in accumulator A
             g.ax = true;
             g.acc = w.acc;
             g.acc_ld = H;
             g.g_in = l.attn_norm;
-            g.x = w.x;
-            g.x_alt = w.x2;
+            g.x = xb[xc];
+            g.x_alt = xb[xc ^ 1];
             g.ldx = H;
+            xc ^= 1;
+        }
+        if (fuse_l) {
+            g.zero = w.acc2;
+            g.zero_n = acc_n;
         }
         gemv(ctx, EPI_QKV, l.wqkv, g);
         // attention (RoPE, cache write) and the merge into wo's pieces
         aa.kc = kv->k + li * kv->layer_floats();
         aa.vc = kv->v + li * kv->layer_floats();
         Pieces po = pieces(w, cur ^ 1, l.wo.kb, passes);
-        const bool am = ctx->merge_in_o && merge_in_o(c, P, l.wo, mm);
+        const bool am = fuse_l || (ctx->merge_in_o && merge_in_o(c, P, l.wo, mm));
         if (launch_attention(st, aa, t, am ? -1 : ck(l.wo), po))
             return fail(FG_E_SHAPE, "no attention kernel for head_dim " + std::to_string(hd));
         if (cap && launch_cap_merge(st, aa, t, capl + (size_t)t * H, qd))
             return fail(FG_E_SHAPE, "no attention kernel for head_dim " + std::to_string(hd));
         cur ^= 1;
+        if (fuse_l) {
+            // the output projection by head, into accumulator B (A cleared for the MLP)
+            g = gemv_args(l.wo, pieces(w, cur, l.wo.kb, passes), t, w);
+            g.apart = w.apart;
+            g.amrec = aa.mrec;
+            g.anh = nh;
+            g.ankv = nkv;
+            g.ahd = hd;
+            g.aqm = attn_qmax(hd);
+            g.acc_out = w.acc2;
+            g.acc_ld = H;
+            g.zero = w.acc;
+            g.zero_n = acc_n;
+            if (launch_o_heads(st, l.wo, g))
+                return fail(FG_E_SHAPE, "no split output projection for head_dim " + std::to_string(hd));
+            cur ^= 1;
+            // gate/up, SiLU and down in one launch: input x + B, output into A
+            g = gemv_args(l.w_gate_up, pieces(w, cur, l.w_gate_up.kb, passes), t, w);
+            g.ax = true;
+            g.acc = w.acc2;
+            g.acc_ld = H;
+            g.g_in = l.mlp_norm;
+            g.x = xb[xc];
+            g.x_alt = xb[xc ^ 1];
+            g.ldx = H;
+            xc ^= 1;
+            g.hidden = H;
+            g.eps = c.rms_eps;
+            g.il = l.w_gate_up.il;
+            g.acc_out = w.acc;
+            g.W2 = (const uint8_t*)l.w_down.w;
+            g.N2 = l.w_down.rows;
+            g.KB2 = l.w_down.kb;
+            gemv(ctx, EPI_MLP, l.w_gate_up, g);
+            cur ^= 1;
+            cur ^= 1;
+            continue;
+        }
         // o projection + residual; pieces of mlp_norm * x for gate/up
         g = gemv_args(l.wo, pieces(w, cur, l.wo.kb, passes), t, w);
         if (am) {
@@ -864,7 +924,8 @@ static int run_forward(fg_ctx* ctx, const fg_model* m, fg_kv* kv, const Plan& P,
             g.aqm = attn_qmax(hd);
         }
         g.x = w.x;
-        if (fuse && li > 0) g.x_alt = w.x2;  // the layer input x + acc, formed by this layer's q/k/v
+        if (xb[xc] != w.x) g.x_alt = xb[xc];  // the layer input x + acc, formed by this layer's q/k/v
+        xc = 0;
         g.ldx = H;
         g.ss_out = w.ss;
         g.ss_m = t;
@@ -882,33 +943,9 @@ static int run_forward(fg_ctx* ctx, const fg_model* m, fg_kv* kv, const Plan& P,
             g.gcnt = ctx->gcnt;
         }
         ss_cols = mm ? 64 : 16 * g.nt;
-        const bool fuse_l = fuse && li + 1 < L;
-        if (fuse_l) {
-            g.acc = w.acc;  // zeroed here for the fused MLP
-            g.acc_ld = H;
-        }
         gemv(ctx, EPI_RESID, l.wo, g);
         if (cap) launch_cap_norm(st, w.x, t, H, l.mlp_norm, c.rms_eps, capl + (size_t)t * (H + qd), H);
         cur ^= 1;
-        if (fuse_l) {
-            // gate/up, SiLU and down in one launch, into the accumulator
-            g = gemv_args(l.w_gate_up, pieces(w, cur, l.w_gate_up.kb, passes), t, w);
-            g.ss_in = w.ss;
-            g.ss_tiles = (H + ss_cols - 1) / ss_cols;
-            g.ss_m = t;
-            g.hidden = H;
-            g.eps = c.rms_eps;
-            g.il = l.w_gate_up.il;
-            g.acc = w.acc;
-            g.acc_ld = H;
-            g.W2 = (const uint8_t*)l.w_down.w;
-            g.N2 = l.w_down.rows;
-            g.KB2 = l.w_down.kb;
-            gemv(ctx, EPI_MLP, l.w_gate_up, g);
-            cur ^= 1;
-            cur ^= 1;
-            continue;
-        }
         // gate/up with SiLU; pieces of the activation for down
         g = gemv_args(l.w_gate_up, pieces(w, cur, l.w_gate_up.kb, passes), t, w);
         g.ss_in = w.ss;

@@ -146,18 +146,22 @@ struct GemvArgs {
     const float* apart = nullptr;
     const int32_t* amrec = nullptr;
     int anh = 0, ankv = 0, ahd = 0, aqm = 0;
-    // The residual accumulator of a fused MLP (kAccCopies copies of [4][acc_ld]).
-    // EPI_MLP adds into it; EPI_RESID (the output projection before it) zeroes the
-    // group's columns of every copy; with ax (EPI_QKV of the next layer) the
-    // input rows are x + the copies' sum, normed here (g_in, hidden, eps) into
-    // the operand, and stored to x_alt (not to x, which the launch's other
-    // workgroups are still reading). EPI_RESID reads its residual rows from
-    // x_alt when set (then writes the sum to x as always).
+    // Fixed-point accumulators (kAccCopies copies of [4][acc_ld]) of a fused layer:
+    // with ax (EPI_QKV, EPI_MLP) the input rows are x + the sum of acc's copies,
+    // normed here (g_in, hidden, eps) into the operand, and stored to x_alt (not
+    // to x, which the launch's other workgroups are still reading); EPI_MLP adds
+    // its output into acc_out. EPI_RESID reads its residual rows from x_alt when
+    // set (then writes the sum to x as always). zero: zero_n words every launch
+    // clears before anything else (grid-stride), for an accumulator that a
+    // later kernel adds into.
     long long* acc = nullptr;
+    long long* acc_out = nullptr;
     int acc_ld = 0;
     bool ax = false;
     const float* g_in = nullptr;
     float* x_alt = nullptr;
+    long long* zero = nullptr;
+    int zero_n = 0;
     // EPI_MLP: the down projection (bf16, the device layout) of N2 outputs, KB2 k-blocks
     const uint8_t* W2 = nullptr;
     int N2 = 0, KB2 = 0;
@@ -167,6 +171,13 @@ struct GemvArgs {
 // so their interval is the kernel's own execution time.
 void launch_gemv(hipStream_t st, int epi, const DMat& w, const GemvArgs& a, hipEvent_t start = nullptr,
                  hipEvent_t stop = nullptr);
+// The output projection of a fused bf16 layer split by query head (k_o_heads):
+// a.apart / a.amrec the attention's span partials and merge records, a.anh,
+// a.ankv, a.ahd, a.aqm their geometry; the product is added into a.acc_out and
+// a.zero is cleared. Returns -1 (nothing launched) for a head dim without an
+// instance (64 and 128 have one).
+int launch_o_heads(hipStream_t st, const DMat& w, const GemvArgs& a, hipEvent_t start = nullptr,
+                   hipEvent_t stop = nullptr);
 
 void launch_pieces(hipStream_t st, int consumer_kind, const float* x, int ldx, int m, int K, const float* g,
                    const int32_t* rows_src, Pieces& out);

@@ -306,10 +306,10 @@ void launch_embed(hipStream_t st, const uint32_t* tokens, int stride, const uint
 // AM: the input is the attention output, merged by the workgroup itself from
 // the span partials (instead of a separate merge kernel writing pieces):
 // bf16 weights, one pass, at most 1024 inputs.
-// AX: the input is the residual x plus the fixed-point accumulator of the
-// previous layer's fused MLP, normed by the workgroup itself (sum of squares
-// over the whole row, 1/rms in the epilogue, g_in as the norm weight): bf16
-// q/k/v, one pass, at most 1024 inputs; x + acc is stored to x_alt.
+// AX: the input is the residual x plus a fixed-point accumulator (the previous
+// fused stage's output), normed by the workgroup itself (sum of squares over
+// the whole row, 1/rms in the epilogue, g_in as the norm weight): bf16 q/k/v
+// or fused MLP, one pass, at most 1024 inputs; x + acc is stored to x_alt.
 template <int KIND, int NT, int EPI, int PG, int WMAX = 8, bool AM = false, bool AX = false>
 __global__ __launch_bounds__(64 * WMAX) void k_gemv(const GemvArgs a) {
     constexpr bool Q = KIND != BF16;
@@ -334,12 +334,18 @@ __global__ __launch_bounds__(64 * WMAX) void k_gemv(const GemvArgs a) {
     __shared__ __align__(16) float vt[16 * YS];  // finished values for the next consumer's pieces
     constexpr int AMKB = 32;  // AM, AX: the operand of up to 32 k-blocks, [kb][lane] bf16 pieces as in global memory
     __shared__ __align__(16) u16x8 xm[AM || AX ? AMKB * 64 : 1];
-    static_assert(!AX || (KIND == BF16 && PG == 1 && EPI == EPI_QKV), "AX: bf16 q/k/v of one pass");
+    static_assert(!AX || (KIND == BF16 && PG == 1 && (EPI == EPI_QKV || EPI == EPI_MLP)), "AX: bf16 q/k/v or MLP of one pass");
     static_assert(EPI != EPI_MLP || (KIND == BF16 && PG == 1 && NT == 2), "EPI_MLP: bf16 gate/up of one pass");
 
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, W = blockDim.x >> 6;
     const int tile0 = blockIdx.x * NT;
     const int pass0 = blockIdx.z * PG;
+    // an accumulator a later kernel adds into starts at zero
+    if (a.zero) {
+        const int nthr = (int)(blockDim.x * gridDim.x * gridDim.y * gridDim.z);
+        const int g = (int)threadIdx.x + (int)blockDim.x * (int)(blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z));
+        for (int i = g; i < a.zero_n; i += nthr) a.zero[i] = 0;
+    }
     // AM: the merge records of the (at most four) rows (uniform loads; the
     // records sit in a 64-word padded region) and the first span batch of the
     // thread's first merge item are requested before anything else, so that
@@ -617,12 +623,13 @@ __global__ __launch_bounds__(64 * WMAX) void k_gemv(const GemvArgs a) {
             }
         }
     } else if constexpr (AX) {
-        // The wave's weights first; then per item (row slot, 8 inputs): x + acc
+        // The wave's weights first; then per item (row slot, two inputs): x + acc
         // (every copy requested before any is added; the copies sum exactly),
         // stored to x_alt by one workgroup per item, the four bf16 pieces of
-        // g * (x + acc) straight into the operand (rows past m and inputs past
-        // the row: zero), and the row's sum of squares; the rows' 1/rms (the
-        // waves' sums in wave order) is needed only by the epilogue.
+        // g * (x + acc) straight into their operand slots (rows past m and
+        // inputs past the row: zero), and the row's sum of squares; the rows'
+        // 1/rms (the waves' sums in wave order) is needed only by the epilogue.
+        // Two inputs per item spread the loads and conversions over every wave.
         const int wv = __builtin_amdgcn_readfirstlane(wave);
         const int a0 = wv * KC / W, a1 = (wv + 1) * KC / W;
         bf16x8 wm[NT][4];
@@ -634,59 +641,45 @@ __global__ __launch_bounds__(64 * WMAX) void k_gemv(const GemvArgs a) {
                 for (int j = 0; j < 4; j++)
                     wm[t][j] = ((const bf16x8*)a.W)[((size_t)(tile0 + t) * KB + cc * 4 + j) * 64 + lane];
         }
-        const int H = a.hidden, G8 = KB * 4;
+        const int H = a.hidden, KP = KB * 16;  // input pairs of the padded row
+        uint32_t* xw = (uint32_t*)xm;
         float sq[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-        for (int idx = threadIdx.x; idx < 4 * G8; idx += blockDim.x) {
-            const int r = idx / G8, kg = idx - r * G8, k0 = kg * 8;
-            float v[8];
+        for (int idx = threadIdx.x; idx < 4 * KP; idx += blockDim.x) {
+            const int r = idx / KP, k = 2 * (idx - r * KP);
+            float v0 = 0.0f, v1 = 0.0f;
+            if (r < a.m && k < H) {  // H is even
+                const float2 xv = *(const float2*)(a.x + (size_t)r * a.ldx + k);
+                i64x2 cv[kAccCopies];
 #pragma unroll
-            for (int e = 0; e < 8; e++) v[e] = 0.0f;
-            if (r < a.m && k0 < H) {  // H is a multiple of 8
-                const float* xp = a.x + (size_t)r * a.ldx + k0;
-                const float4 xv0 = *(const float4*)xp, xv1 = *(const float4*)(xp + 4);
-                i64x2 cv[kAccCopies][4];
+                for (int c = 0; c < kAccCopies; c++) cv[c] = *(const i64x2*)(a.acc + ((size_t)c * 4 + r) * a.acc_ld + k);
+                const float2 gv = *(const float2*)(a.g_in + k);
+                long long s0 = 0, s1 = 0;
 #pragma unroll
-                for (int c = 0; c < kAccCopies; c++)
-#pragma unroll
-                    for (int q = 0; q < 4; q++)
-                        cv[c][q] = *(const i64x2*)(a.acc + ((size_t)c * 4 + r) * a.acc_ld + k0 + 2 * q);
-                const float4 g0 = *(const float4*)(a.g_in + k0), g1 = *(const float4*)(a.g_in + k0 + 4);
-                const float xs[8] = {xv0.x, xv0.y, xv0.z, xv0.w, xv1.x, xv1.y, xv1.z, xv1.w};
-                const float gs8[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
+                for (int c = 0; c < kAccCopies; c++) {
+                    s0 += cv[c][0];
+                    s1 += cv[c][1];
+                }
                 const float unit = 1.0f / (float)(1ll << kAccFrac);
-                float xn[8], q2 = 0.0f;
-#pragma unroll
-                for (int e = 0; e < 8; e++) {
-                    long long sum = 0;
-#pragma unroll
-                    for (int c = 0; c < kAccCopies; c++) sum += cv[c][e >> 1][e & 1];
-                    xn[e] = xs[e] + (float)sum * unit;
-                    q2 = fmaf(xn[e], xn[e], q2);
-                    v[e] = gs8[e] * xn[e];
-                }
-                if (idx % (int)gridDim.x == (int)blockIdx.x) {
-                    float* op = a.x_alt + (size_t)r * a.ldx + k0;
-                    *(float4*)op = make_float4(xn[0], xn[1], xn[2], xn[3]);
-                    *(float4*)(op + 4) = make_float4(xn[4], xn[5], xn[6], xn[7]);
-                }
+                const float x0 = xv.x + (float)s0 * unit, x1 = xv.y + (float)s1 * unit;
+                if (idx % (int)gridDim.x == (int)blockIdx.x)
+                    *(float2*)(a.x_alt + (size_t)r * a.ldx + k) = make_float2(x0, x1);
+                const float q2 = fmaf(x1, x1, x0 * x0);
 #pragma unroll
                 for (int rr = 0; rr < 4; rr++)
                     if (rr == r) sq[rr] += q2;
+                v0 = gv.x * x0;
+                v1 = gv.y * x1;
             }
-            // the four pieces at once (bf16_piece's successive roundings)
-            u16x8 o[4];
+            // slot (k-block, 8-input group, operand row r * 4 + piece) holds 8 bf16; these are
+            // its elements k % 8 and k % 8 + 1 (bf16_piece's successive roundings)
+            const int slot = (k >> 5) * 64 + ((k & 31) >> 3) * 16 + r * 4;
 #pragma unroll
-            for (int e = 0; e < 8; e++) {
-                float x = v[e];
-#pragma unroll
-                for (int pc = 0; pc < 4; pc++) {
-                    const uint32_t h = f32_to_bf16_bits(x);
-                    o[pc][e] = (uint16_t)h;
-                    x = x - bf16_bits_to_f32(h);
-                }
+            for (int pc = 0; pc < 4; pc++) {
+                const uint32_t h0 = f32_to_bf16_bits(v0), h1 = f32_to_bf16_bits(v1);
+                xw[(slot + pc) * 4 + ((k & 7) >> 1)] = h0 | (h1 << 16);
+                v0 = v0 - bf16_bits_to_f32(h0);
+                v1 = v1 - bf16_bits_to_f32(h1);
             }
-#pragma unroll
-            for (int pc = 0; pc < 4; pc++) xm[(kg >> 2) * 64 + (kg & 3) * 16 + r * 4 + pc] = o[pc];
         }
         // (the partials go to rtmp, which nothing else uses here: red is
         // rewritten by the waves' products while these are being summed)
@@ -824,7 +817,7 @@ __global__ __launch_bounds__(64 * WMAX) void k_gemv(const GemvArgs a) {
         }
         __syncthreads();
         const int n_items = (a.N2 >> 4) * 32, qq = (lane >> 4) & 1;
-        long long* accp = a.acc + (size_t)(blockIdx.x % kAccCopies) * 4 * a.acc_ld;
+        long long* accp = a.acc_out + (size_t)(blockIdx.x % kAccCopies) * 4 * a.acc_ld;
 #pragma unroll
         for (int it = 0; it < DWI; it++) {
             const int i = (int)threadIdx.x + it * (int)blockDim.x;
@@ -837,13 +830,13 @@ __global__ __launch_bounds__(64 * WMAX) void k_gemv(const GemvArgs a) {
             }
 #pragma unroll
             for (int r = 0; r < 4; r++) {
-                if (r >= rows) break;  // uniform
+                if (pass0 * 4 + r >= a.m) break;  // uniform: the live rows only
                 const float* vr = &vt[r * YS + 8 * qq];
                 float y = w8[0] * vr[0];
 #pragma unroll
                 for (int e = 1; e < 8; e++) y = fmaf(w8[e], vr[e], y);
                 y = reduce_rows<false, false>(y);
-                if (qq == 0 && i < n_items && pass0 * 4 + r < a.m) {
+                if (qq == 0 && i < n_items) {
                     const double d = fmin(fmax((double)y * (double)(1ll << kAccFrac), -4.0e18), 4.0e18);
                     __hip_atomic_fetch_add(accp + (size_t)r * a.acc_ld + n, (long long)rint(d), __ATOMIC_RELAXED,
                                            __HIP_MEMORY_SCOPE_AGENT);
@@ -908,10 +901,6 @@ __global__ __launch_bounds__(64 * WMAX) void k_gemv(const GemvArgs a) {
         if (EPI == EPI_RESID) {
             const float xn = live ? et[r * YS + cc] + yt[r * YS + cc] : 0.0f;
             if (live) a.x[(size_t)row * a.ldx + blockIdx.x * OC + cc] = xn;
-            // the fused MLP that follows adds into the accumulator: this group's columns start at zero
-            if (a.acc && live)
-#pragma unroll
-                for (int c = 0; c < kAccCopies; c++) a.acc[((size_t)c * 4 + row) * a.acc_ld + blockIdx.x * OC + cc] = 0;
             yt[r * YS + cc] = xn;
             vt[r * YS + cc] = a.g_next ? gs[cc] * xn : xn;
         } else {
@@ -1554,7 +1543,11 @@ static void gemv_kind(hipStream_t st, int epi, const DMat& w, const GemvArgs& a,
         case EPI_MLP:
             if constexpr (KIND == BF16) {
                 const int W = std::max(1, std::min(8, w.kb / 4));
-                launch_timed(k_gemv<BF16, 2, EPI_MLP, 1>, dim3(w.n_tiles / 2, 1, 1), dim3(64 * W), st, a, e0, e1);
+                if (a.ax)
+                    launch_timed(k_gemv<BF16, 2, EPI_MLP, 1, 8, false, true>, dim3(w.n_tiles / 2, 1, 1), dim3(64 * W),
+                                 st, a, e0, e1);
+                else
+                    launch_timed(k_gemv<BF16, 2, EPI_MLP, 1>, dim3(w.n_tiles / 2, 1, 1), dim3(64 * W), st, a, e0, e1);
             }
             break;
         case EPI_ARGMAX:
@@ -2266,6 +2259,99 @@ int launch_cap_merge(hipStream_t st, const AttnArgs& a, int m, float* out, int l
         case 32: hipLaunchKernelGGL((k_cap_merge<32, 64>), grid, dim3(64), 0, st, a, m, out, ldo); return 0;
         case 64: hipLaunchKernelGGL((k_cap_merge<64, 32>), grid, dim3(64), 0, st, a, m, out, ldo); return 0;
         case 128: hipLaunchKernelGGL((k_cap_merge<128, 32>), grid, dim3(64), 0, st, a, m, out, ldo); return 0;
+        default: return -1;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Output projection of a fused bf16 layer, split by query head: workgroup
+// (n-tile, head h) merges head h's spans for the step's rows (SpanMerge, the
+// merge kernel's arithmetic; the four lanes of a quad write the four bf16
+// pieces of 8 merged values), multiplies them by the HD columns of W_o that
+// belong to head h (HD / 32 k-blocks of its n-tile, bf16 MFMA), and adds the
+// 16 outputs of each row into the accumulator a.acc_out (copy = workgroup %
+// kAccCopies) as round(y * 2^kAccFrac). A workgroup reads one head's partials
+// (about 4.6 KB per row for the 135M draft) instead of every head's, which is
+// what an output projection that merges for itself must read per workgroup;
+// a CU streams only about 27 GB/s, so that read was most of its time. The
+// heads' contributions meet in the accumulator (integer sums: their order
+// does not matter). Every launch also clears a.zero (the next stage's
+// accumulator). 2 HD threads: an item (row slot, 8 dims, phase) per thread.
+// ---------------------------------------------------------------------------
+template <int HD>
+__global__ __launch_bounds__(2 * HD) void k_o_heads(const GemvArgs a) {
+    constexpr int KBH = HD / 32, SB = 5, IPR = HD / 2;  // k-blocks of a head, items per row
+    __shared__ __align__(16) u16x8 xm[KBH * 64];
+    const int t = blockIdx.x, h = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wg = (int)(blockIdx.x + gridDim.x * blockIdx.y);
+    if (a.zero)
+        for (int i = wg * (int)blockDim.x + tid; i < a.zero_n; i += (int)(blockDim.x * gridDim.x * gridDim.y)) a.zero[i] = 0;
+    // this n-tile's columns of head h: wave w takes k-blocks w, w + 2, ... (requested first)
+    constexpr int KW = (KBH + 1) / 2;
+    bf16x8 wb[KW];
+#pragma unroll
+    for (int j = 0; j < KW; j++) {
+        const int kb = min(wave + 2 * j, KBH - 1);
+        wb[j] = ((const bf16x8*)a.W)[((size_t)t * a.KB + h * KBH + kb) * 64 + lane];
+    }
+    const int row = tid / IPR, rem = tid % IPR, k0 = (rem >> 2) * 8, phase = rem & 3;
+    float v[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    if (row < a.m) {
+        // the row's merge record (a vector load: the same address in every lane of the row)
+        const int4 mr = ((const int4*)a.amrec)[row];
+        SpanMerge<SB> sm;
+        sm.init(a.apart, mr, a.anh, a.ankv, a.ahd, a.aqm, h * HD + k0);
+        for (int s0 = phase; s0 < sm.ns; s0 += 4 * SB) {
+            sm.load(s0);
+            sm.fold(s0);
+        }
+        sm.finish(v);
+    }
+    u16x8 o;
+#pragma unroll
+    for (int e = 0; e < 8; e++) o[e] = (uint16_t)bf16_piece(v[e], phase);
+    xm[(k0 >> 5) * 64 + ((k0 & 31) >> 3) * 16 + row * 4 + phase] = o;
+    __syncthreads();
+    // D of the 16 x 16 product: lane l holds the four pieces of row l / 16, column l % 16
+    f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int j = 0; j < KW; j++) {
+        const int kb = wave + 2 * j;
+        if (kb < KBH) {
+            const u16x8 x = xm[kb * 64 + lane];
+            bf16x8 ab;
+            __builtin_memcpy(&ab, &x, sizeof(ab));
+            acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ab, wb[j], acc, 0, 0, 0);
+        }
+    }
+    // the two waves' k-blocks meet in LDS (wave 1 hands its product to wave 0)
+    __shared__ f32x4 red[64];
+    if (KBH > 1 && wave == 1) red[lane] = acc;
+    __syncthreads();
+    if (wave == 0) {
+        if (KBH > 1) acc += red[lane];
+        const int r = lane >> 4, n = t * 16 + (lane & 15);
+        if (r < a.m && n < a.N) {
+            const float y = ((acc[0] + acc[1]) + acc[2]) + acc[3];
+            const double d = fmin(fmax((double)y * (double)(1ll << kAccFrac), -4.0e18), 4.0e18);
+            __hip_atomic_fetch_add(a.acc_out + ((size_t)(wg % kAccCopies) * 4 + r) * a.acc_ld + n, (long long)rint(d),
+                                   __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+    }
+}
+
+int launch_o_heads(hipStream_t st, const DMat& w, const GemvArgs& a, hipEvent_t e0, hipEvent_t e1) {
+    if (a.m <= 0) return 0;
+    const dim3 grid(w.n_tiles, a.anh);
+    auto run = [&](auto kern, int threads) {
+        if (e0 || e1)
+            hipExtLaunchKernelGGL(kern, grid, dim3(threads), 0, st, e0, e1, 0, a);
+        else
+            hipLaunchKernelGGL(kern, grid, dim3(threads), 0, st, a);
+    };
+    switch (a.ahd) {
+        case 64: run(k_o_heads<64>, 128); return 0;
+        case 128: run(k_o_heads<128>, 256); return 0;
         default: return -1;
     }
 }
