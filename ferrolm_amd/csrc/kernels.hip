@@ -340,12 +340,7 @@ __global__ __launch_bounds__(64 * WMAX) void k_gemv(const GemvArgs a) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, W = blockDim.x >> 6;
     const int tile0 = blockIdx.x * NT;
     const int pass0 = blockIdx.z * PG;
-    // an accumulator a later kernel adds into starts at zero
-    if (a.zero) {
-        const int nthr = (int)(blockDim.x * gridDim.x * gridDim.y * gridDim.z);
-        const int g = (int)threadIdx.x + (int)blockDim.x * (int)(blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z));
-        for (int i = g; i < a.zero_n; i += nthr) a.zero[i] = 0;
-    }
+
     // AM: the merge records of the (at most four) rows (uniform loads; the
     // records sit in a 64-word padded region) and the first span batch of the
     // thread's first merge item are requested before anything else, so that
@@ -644,41 +639,42 @@ __global__ __launch_bounds__(64 * WMAX) void k_gemv(const GemvArgs a) {
         const int H = a.hidden, KP = KB * 16;  // input pairs of the padded row
         uint32_t* xw = (uint32_t*)xm;
         float sq[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-        for (int idx = threadIdx.x; idx < 4 * KP; idx += blockDim.x) {
-            const int r = idx / KP, k = 2 * (idx - r * KP);
-            float v0 = 0.0f, v1 = 0.0f;
-            if (r < a.m && k < H) {  // H is even
-                const float2 xv = *(const float2*)(a.x + (size_t)r * a.ldx + k);
-                i64x2 cv[kAccCopies];
 #pragma unroll
-                for (int c = 0; c < kAccCopies; c++) cv[c] = *(const i64x2*)(a.acc + ((size_t)c * 4 + r) * a.acc_ld + k);
-                const float2 gv = *(const float2*)(a.g_in + k);
-                long long s0 = 0, s1 = 0;
+        for (int r = 0; r < 4; r++) {
+            for (int kp = threadIdx.x; kp < KP; kp += blockDim.x) {
+                const int k = 2 * kp;
+                // slot (k-block, 8-input group, operand row r * 4 + piece) holds 8 bf16; these
+                // are its elements k % 8 and k % 8 + 1 (bf16_piece's successive roundings)
+                const int slot = (k >> 5) * 64 + ((k & 31) >> 3) * 16 + r * 4, wd = (k & 7) >> 1;
+                if (r < a.m && k < H) {  // (H is even)
+                    const float2 xv = *(const float2*)(a.x + (size_t)r * a.ldx + k);
+                    i64x2 cv[kAccCopies];
 #pragma unroll
-                for (int c = 0; c < kAccCopies; c++) {
-                    s0 += cv[c][0];
-                    s1 += cv[c][1];
+                    for (int c = 0; c < kAccCopies; c++)
+                        cv[c] = *(const i64x2*)(a.acc + ((size_t)c * 4 + r) * a.acc_ld + k);
+                    const float2 gv = *(const float2*)(a.g_in + k);
+                    long long s0 = 0, s1 = 0;
+#pragma unroll
+                    for (int c = 0; c < kAccCopies; c++) {
+                        s0 += cv[c][0];
+                        s1 += cv[c][1];
+                    }
+                    const float unit = 1.0f / (float)(1ll << kAccFrac);
+                    const float x0 = xv.x + (float)s0 * unit, x1 = xv.y + (float)s1 * unit;
+                    if (blockIdx.x == 0) *(float2*)(a.x_alt + (size_t)r * a.ldx + k) = make_float2(x0, x1);
+                    sq[r] += fmaf(x1, x1, x0 * x0);
+                    float v0 = gv.x * x0, v1 = gv.y * x1;
+#pragma unroll
+                    for (int pc = 0; pc < 4; pc++) {
+                        const uint32_t h0 = f32_to_bf16_bits(v0), h1 = f32_to_bf16_bits(v1);
+                        xw[(slot + pc) * 4 + wd] = h0 | (h1 << 16);
+                        v0 = v0 - bf16_bits_to_f32(h0);
+                        v1 = v1 - bf16_bits_to_f32(h1);
+                    }
+                } else {
+#pragma unroll
+                    for (int pc = 0; pc < 4; pc++) xw[(slot + pc) * 4 + wd] = 0u;
                 }
-                const float unit = 1.0f / (float)(1ll << kAccFrac);
-                const float x0 = xv.x + (float)s0 * unit, x1 = xv.y + (float)s1 * unit;
-                if (idx % (int)gridDim.x == (int)blockIdx.x)
-                    *(float2*)(a.x_alt + (size_t)r * a.ldx + k) = make_float2(x0, x1);
-                const float q2 = fmaf(x1, x1, x0 * x0);
-#pragma unroll
-                for (int rr = 0; rr < 4; rr++)
-                    if (rr == r) sq[rr] += q2;
-                v0 = gv.x * x0;
-                v1 = gv.y * x1;
-            }
-            // slot (k-block, 8-input group, operand row r * 4 + piece) holds 8 bf16; these are
-            // its elements k % 8 and k % 8 + 1 (bf16_piece's successive roundings)
-            const int slot = (k >> 5) * 64 + ((k & 31) >> 3) * 16 + r * 4;
-#pragma unroll
-            for (int pc = 0; pc < 4; pc++) {
-                const uint32_t h0 = f32_to_bf16_bits(v0), h1 = f32_to_bf16_bits(v1);
-                xw[(slot + pc) * 4 + ((k & 7) >> 1)] = h0 | (h1 << 16);
-                v0 = v0 - bf16_bits_to_f32(h0);
-                v1 = v1 - bf16_bits_to_f32(h1);
             }
         }
         // (the partials go to rtmp, which nothing else uses here: red is
@@ -744,6 +740,14 @@ __global__ __launch_bounds__(64 * WMAX) void k_gemv(const GemvArgs a) {
     }
     if (EPI == EPI_RESID && threadIdx.x < OC) gs[threadIdx.x] = gv;
 
+    // an accumulator a later kernel adds into starts at zero (stored only now:
+    // loads and stores retire in order, so earlier stores would hold up every
+    // wait on the loads above)
+    if (a.zero) {
+        const int nthr = (int)(blockDim.x * gridDim.x * gridDim.y * gridDim.z);
+        const int g = (int)threadIdx.x + (int)blockDim.x * (int)(blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z));
+        for (int i = g; i < a.zero_n; i += nthr) a.zero[i] = 0;
+    }
     // reduce across waves
 #pragma unroll
     for (int t = 0; t < NT; t++)
@@ -2284,8 +2288,6 @@ __global__ __launch_bounds__(2 * HD) void k_o_heads(const GemvArgs a) {
     __shared__ __align__(16) u16x8 xm[KBH * 64];
     const int t = blockIdx.x, h = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wg = (int)(blockIdx.x + gridDim.x * blockIdx.y);
-    if (a.zero)
-        for (int i = wg * (int)blockDim.x + tid; i < a.zero_n; i += (int)(blockDim.x * gridDim.x * gridDim.y)) a.zero[i] = 0;
     // this n-tile's columns of head h: wave w takes k-blocks w, w + 2, ... (requested first)
     constexpr int KW = (KBH + 1) / 2;
     bf16x8 wb[KW];
@@ -2338,6 +2340,10 @@ __global__ __launch_bounds__(2 * HD) void k_o_heads(const GemvArgs a) {
                                    __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
     }
+    // the next stage's accumulator starts at zero (stored last: loads and stores
+    // retire in order, so earlier stores would hold up every wait on a load)
+    if (a.zero)
+        for (int i = wg * (int)blockDim.x + tid; i < a.zero_n; i += (int)(blockDim.x * gridDim.x * gridDim.y)) a.zero[i] = 0;
 }
 
 int launch_o_heads(hipStream_t st, const DMat& w, const GemvArgs& a, hipEvent_t e0, hipEvent_t e1) {
