@@ -332,8 +332,13 @@ __global__ __launch_bounds__(64 * WMAX) void k_gemv(const GemvArgs a) {
     __shared__ __align__(16) float et[16 * YS];  // epilogue inputs: x tile (EPI_RESID) or bias
     __shared__ __align__(16) float gs[32];       // g_next of this group's 32 columns (EPI_RESID)
     __shared__ __align__(16) float vt[16 * YS];  // finished values for the next consumer's pieces
-    constexpr int AMKB = 32;  // AM, AX: the operand of up to 32 k-blocks, [kb][lane] bf16 pieces as in global memory
-    __shared__ __align__(16) u16x8 xm[AM || AX ? AMKB * 64 : 1];
+    constexpr int AMKB = 32;  // AM: the operand of up to 32 k-blocks, [kb][lane] bf16 pieces as in global memory
+    __shared__ __align__(16) u16x8 xm[AM ? AMKB * 64 : 1];
+    // AX: the operand as bf16 pieces [piece][row][XPK]: a row pitch of 8 (mod 128)
+    // bf16 puts the 16 (piece, row) rows of an MFMA read 4 banks apart, and
+    // lanes writing consecutive inputs of one row hit consecutive banks
+    constexpr int XPK = AMKB * 32 + 8;
+    __shared__ __align__(16) uint16_t xp[AX ? 16 * XPK : 1];
     static_assert(!AX || (KIND == BF16 && PG == 1 && (EPI == EPI_QKV || EPI == EPI_MLP)), "AX: bf16 q/k/v or MLP of one pass");
     static_assert(EPI != EPI_MLP || (KIND == BF16 && PG == 1 && NT == 2), "EPI_MLP: bf16 gate/up of one pass");
 
@@ -637,16 +642,15 @@ __global__ __launch_bounds__(64 * WMAX) void k_gemv(const GemvArgs a) {
                     wm[t][j] = ((const bf16x8*)a.W)[((size_t)(tile0 + t) * KB + cc * 4 + j) * 64 + lane];
         }
         const int H = a.hidden, KP = KB * 16;  // input pairs of the padded row
-        uint32_t* xw = (uint32_t*)xm;
+        uint32_t* xw = (uint32_t*)xp;
         float sq[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
         for (int r = 0; r < 4; r++) {
+            if (r >= a.m) break;  // uniform
             for (int kp = threadIdx.x; kp < KP; kp += blockDim.x) {
                 const int k = 2 * kp;
-                // slot (k-block, 8-input group, operand row r * 4 + piece) holds 8 bf16; these
-                // are its elements k % 8 and k % 8 + 1 (bf16_piece's successive roundings)
-                const int slot = (k >> 5) * 64 + ((k & 31) >> 3) * 16 + r * 4, wd = (k & 7) >> 1;
-                if (r < a.m && k < H) {  // (H is even)
+                float v0 = 0.0f, v1 = 0.0f;
+                if (k < H) {  // (H is even)
                     const float2 xv = *(const float2*)(a.x + (size_t)r * a.ldx + k);
                     i64x2 cv[kAccCopies];
 #pragma unroll
@@ -663,19 +667,23 @@ __global__ __launch_bounds__(64 * WMAX) void k_gemv(const GemvArgs a) {
                     const float x0 = xv.x + (float)s0 * unit, x1 = xv.y + (float)s1 * unit;
                     if (blockIdx.x == 0) *(float2*)(a.x_alt + (size_t)r * a.ldx + k) = make_float2(x0, x1);
                     sq[r] += fmaf(x1, x1, x0 * x0);
-                    float v0 = gv.x * x0, v1 = gv.y * x1;
+                    v0 = gv.x * x0;
+                    v1 = gv.y * x1;
+                }
+                // the four pieces (bf16_piece's successive roundings) of inputs k, k + 1
 #pragma unroll
-                    for (int pc = 0; pc < 4; pc++) {
-                        const uint32_t h0 = f32_to_bf16_bits(v0), h1 = f32_to_bf16_bits(v1);
-                        xw[(slot + pc) * 4 + wd] = h0 | (h1 << 16);
-                        v0 = v0 - bf16_bits_to_f32(h0);
-                        v1 = v1 - bf16_bits_to_f32(h1);
-                    }
-                } else {
-#pragma unroll
-                    for (int pc = 0; pc < 4; pc++) xw[(slot + pc) * 4 + wd] = 0u;
+                for (int pc = 0; pc < 4; pc++) {
+                    const uint32_t h0 = f32_to_bf16_bits(v0), h1 = f32_to_bf16_bits(v1);
+                    xw[((pc * 4 + r) * XPK + k) >> 1] = h0 | (h1 << 16);
+                    v0 = v0 - bf16_bits_to_f32(h0);
+                    v1 = v1 - bf16_bits_to_f32(h1);
                 }
             }
+        }
+        // rows past m: zero pieces (four 16-byte words per thread-step, consecutive)
+        for (int i = threadIdx.x; i < 4 * (4 - a.m) * (KB * 4); i += blockDim.x) {
+            const int pr = i / (KB * 4), kg = i - pr * (KB * 4), pc = pr & 3, r = a.m + (pr >> 2);
+            *(u16x8*)&xp[(pc * 4 + r) * XPK + kg * 8] = (u16x8){0, 0, 0, 0, 0, 0, 0, 0};
         }
         // (the partials go to rtmp, which nothing else uses here: red is
         // rewritten by the waves' products while these are being summed)
@@ -691,9 +699,11 @@ __global__ __launch_bounds__(64 * WMAX) void k_gemv(const GemvArgs a) {
             rs[threadIdx.x] = 1.0f / sqrtf(v / (float)H + a.eps);
         }
         if (a0 < a1) {
+            // lane l: piece l % 4 of row (l % 16) / 4, inputs 8 (l / 16) .. + 7 of the k-block
+            const uint16_t* xl = xp + ((lane & 3) * 4 + ((lane & 15) >> 2)) * XPK + 8 * (lane >> 4);
 #pragma unroll
             for (int j = 0; j < 4; j++) {
-                const u16x8 o = xm[(a0 * 4 + j) * 64 + lane];
+                const u16x8 o = *(const u16x8*)(xl + (a0 * 4 + j) * 32);
                 bf16x8 ab;
                 __builtin_memcpy(&ab, &o, sizeof(ab));
 #pragma unroll
