@@ -92,6 +92,11 @@ struct fg_ctx {
     float last_us[3] = {0, 0, 0};
     bool merge_in_o = true;  // small bf16 output projections merge the attention spans themselves
     bool mlp_fuse = true;    // bf16 layers of one pass run fused (mlp_fuse: split output projection, EPI_MLP)
+    // in-kernel timeline (libraries built with stamps): the next launch's slot
+    // (every fg_forward and speculative step starts over at 0, so a captured
+    // graph bakes the same slots each time) and each slot's kernel label
+    int stamp_seq = 0;
+    std::vector<std::string> stamp_labels;
     // split-K GEMV meeting counters (GemvArgs::gcnt): zeroed once here, left at
     // zero by every launch's last workgroups
     unsigned* gcnt = nullptr;
@@ -155,10 +160,35 @@ static hipEvent_t prof_event(fg_ctx* c) {
     return c->pev[c->pev_used++];
 }
 
+// The timeline slot of the next launch, labelled (-1 in a library built without stamps).
+static int next_stamp(fg_ctx* c, const std::string& label) {
+#ifdef FERRO_STAMPS
+    const int s = c->stamp_seq++;
+    if (s >= kStampSlots) return -1;
+    if ((int)c->stamp_labels.size() <= s) c->stamp_labels.resize(s + 1);
+    c->stamp_labels[s] = label;
+    return s;
+#else
+    (void)c;
+    (void)label;
+    return -1;
+#endif
+}
+
+static std::string gemv_label(int epi, const DMat& w, const GemvArgs& a) {
+    static const char* epis[] = {"store", "qkv", "resid", "silu", "lm_head", "mlp"};
+    static const char* kinds[] = {"bf16", "int8", "int4"};
+    std::string s = std::string(a.mm ? "gemm " : "gemv ") + kinds[w.kind] + " " + epis[epi];
+    if (a.ax) s += " ax";
+    if (a.am) s += " am";
+    return s + " " + std::to_string(w.rows) + "x" + std::to_string(w.cols);
+}
+
 // launch_gemv, timed by its own dispatch while profiling (fg_profile). The
 // speculative step launches directly (no graph) while profiling is on.
 static void gemv(fg_ctx* c, int epi, const DMat& w, const GemvArgs& a0) {
     GemvArgs a = a0;
+    a.stamp = next_stamp(c, gemv_label(epi, w, a));
     if (a.mm) a.gcnt = c->gcnt;  // a split GEMM of small tiles meets on these counters and finishes in place
     if (!c->prof || c->capturing) {
         launch_gemv(c->stream, epi, w, a);
@@ -869,6 +899,8 @@ static int run_forward(fg_ctx* ctx, const fg_model* m, fg_kv* kv, const Plan& P,
         aa.vc = kv->v + li * kv->layer_floats();
         Pieces po = pieces(w, cur ^ 1, l.wo.kb, passes);
         const bool am = fuse_l || (ctx->merge_in_o && merge_in_o(c, P, l.wo, mm));
+        aa.stamp = next_stamp(ctx, "attention");
+        if (!am && aa.stamp >= 0) next_stamp(ctx, "merge");  // the merge launch takes the next slot
         if (launch_attention(st, aa, t, am ? -1 : ck(l.wo), po))
             return fail(FG_E_SHAPE, "no attention kernel for head_dim " + std::to_string(hd));
         if (cap && launch_cap_merge(st, aa, t, capl + (size_t)t * H, qd))
@@ -887,6 +919,7 @@ static int run_forward(fg_ctx* ctx, const fg_model* m, fg_kv* kv, const Plan& P,
             g.acc_ld = H;
             g.zero = w.acc;
             g.zero_n = acc_n;
+            g.stamp = next_stamp(ctx, "o by head bf16 " + std::to_string(l.wo.rows) + "x" + std::to_string(l.wo.cols));
             if (launch_o_heads(st, l.wo, g))
                 return fail(FG_E_SHAPE, "no split output projection for head_dim " + std::to_string(hd));
             cur ^= 1;
@@ -1269,6 +1302,7 @@ int fg_forward(fg_ctx* ctx, const fg_model* m, fg_kv* kv, const fg_chunk* chunks
     int rc = check_model_kv(m, kv);
     if (rc) return rc;
     HIPCHK(hipSetDevice(ctx->device));
+    ctx->stamp_seq = 0;
     std::vector<ChunkIn> in(n_chunks);
     for (int i = 0; i < n_chunks; i++) {
         if (chunks[i].n > 0 && !chunks[i].tokens) return fail(FG_E_ARG, "chunk without tokens");
@@ -1392,6 +1426,7 @@ static int spec_step(fg_ctx* ctx, const fg_model* target, fg_kv* tkv, const fg_m
         return fail(FG_E_ARG, "bad argument");
     const bool sampling = params != nullptr;
     if (sampling && n_chunks > 0) return fail(FG_E_ARG, "chunks ride only with greedy steps");
+    ctx->stamp_seq = 0;
     int c_last = 0;  // FG_LOGITS_LAST rows of the chunks
     for (int c = 0; c < n_chunks; c++) {
         if (chunks[c].n > 0 && !chunks[c].tokens) return fail(FG_E_ARG, "chunk without tokens");
@@ -1695,6 +1730,31 @@ int fg_last_step_times(const fg_ctx* ctx, float* us3) {
     if (!ctx || !us3) return fail(FG_E_ARG, "null argument");
     memcpy(us3, ctx->last_us, sizeof(ctx->last_us));
     return 0;
+}
+
+int fg_stamps_reset(fg_ctx* ctx) {
+    if (!ctx) return fail(FG_E_ARG, "null ctx");
+    HIPCHK(hipSetDevice(ctx->device));
+    HIPCHK(hipStreamSynchronize(ctx->stream));
+    if (stamps_clear()) return fail(FG_E_ARG, "this library was built without stamps (python -m ferrolm_amd.build --stamps)");
+    return 0;
+}
+
+int fg_stamps_read(fg_ctx* ctx, int32_t slots, uint64_t* ticks, char* labels, int32_t label_cap) {
+    if (!ctx || slots < 0 || (slots > 0 && !ticks) || (label_cap > 0 && !labels)) return fail(FG_E_ARG, "bad argument");
+    HIPCHK(hipSetDevice(ctx->device));
+    HIPCHK(hipStreamSynchronize(ctx->stream));
+    const int used = (int)ctx->stamp_labels.size();
+    if (stamps_read(ticks, std::min(slots, kStampSlots)))
+        return fail(FG_E_ARG, "this library was built without stamps (python -m ferrolm_amd.build --stamps)");
+    std::string all;
+    for (const auto& l : ctx->stamp_labels) all += l + "\n";
+    if (label_cap > 0) {
+        const size_t n = std::min(all.size(), (size_t)label_cap - 1);
+        memcpy(labels, all.data(), n);
+        labels[n] = 0;
+    }
+    return used;
 }
 
 int fg_profile(fg_ctx* ctx, int32_t on) {

@@ -39,6 +39,29 @@ __device__ __forceinline__ float4 ld_nt_f4(const float* p) {
 
 __device__ __forceinline__ float bf16_bits_to_f32(uint32_t h) { return __uint_as_float(h << 16); }
 
+// In-kernel timeline (see stamps_read): declared at a kernel's entry, end()
+// at each of its exits. Without FERRO_STAMPS it is empty and compiles away.
+#ifdef FERRO_STAMPS
+extern __device__ unsigned long long g_stamps[kStampSlots][kStampWgs][2];
+struct Stamp {
+    unsigned long long t0;
+    int slot;
+    __device__ explicit Stamp(int s) : t0(__builtin_amdgcn_s_memrealtime()), slot(s) {}
+    __device__ void end() const {
+        const int wg = (int)(blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z));
+        if (threadIdx.x == 0 && slot >= 0 && slot < kStampSlots && wg < kStampWgs) {
+            g_stamps[slot][wg][0] = t0;
+            g_stamps[slot][wg][1] = __builtin_amdgcn_s_memrealtime();
+        }
+    }
+};
+#else
+struct Stamp {
+    __device__ explicit Stamp(int) {}
+    __device__ void end() const {}
+};
+#endif
+
 // round to nearest even (v_cvt_pk_bf16_f32)
 __device__ __forceinline__ uint32_t f32_to_bf16_bits(float x) { return __builtin_bit_cast(uint16_t, (__bf16)x); }
 

@@ -162,6 +162,7 @@ struct GemvArgs {
     float* x_alt = nullptr;
     long long* zero = nullptr;
     int zero_n = 0;
+    int stamp = -1;  // timeline slot of the launch (libraries built with stamps; -1: none)
     // EPI_MLP: the down projection (bf16, the device layout) of N2 outputs, KB2 k-blocks
     const uint8_t* W2 = nullptr;
     int N2 = 0, KB2 = 0;
@@ -211,6 +212,7 @@ struct AttnArgs {
     int flash;
     const int32_t* btab;
     int maxq = 0;  // queries of the largest row group (0: unknown, the full QM)
+    int stamp = -1;  // timeline slot of the launch (libraries built with stamps; -1: none)
 };
 // Attention over the paged cache (RoPE, K/V write of the new rows), then the
 // split merge straight into the output projection's pieces (consumer_kind < 0:
@@ -295,5 +297,13 @@ void launch_mm_exact(hipStream_t st, int kind, const float* x, int m, int K, con
 // (n a multiple of 4, ystride of 4)
 void launch_sq_err(hipStream_t st, const float* y, int64_t ystride, int count, const float* yref, int64_t n,
                    double* out);
+
+// In-kernel timeline (a library built with -DFERRO_STAMPS): thread 0 of each
+// workgroup of a launch with a slot stores its s_memrealtime entry and exit
+// ticks (100 MHz) into [slot][workgroup][2]. stamps_read copies the first
+// `slots` slots; both return -1 in a library built without stamps.
+constexpr int kStampSlots = 1024, kStampWgs = 1024;
+int stamps_read(uint64_t* out, int slots);
+int stamps_clear();
 
 }  // namespace fg

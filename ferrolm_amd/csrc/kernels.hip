@@ -342,6 +342,7 @@ __global__ __launch_bounds__(64 * WMAX) void k_gemv(const GemvArgs a) {
     static_assert(!AX || (KIND == BF16 && PG == 1 && (EPI == EPI_QKV || EPI == EPI_MLP)), "AX: bf16 q/k/v or MLP of one pass");
     static_assert(EPI != EPI_MLP || (KIND == BF16 && PG == 1 && NT == 2), "EPI_MLP: bf16 gate/up of one pass");
 
+    const Stamp stamp(a.stamp);
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, W = blockDim.x >> 6;
     const int tile0 = blockIdx.x * NT;
     const int pass0 = blockIdx.z * PG;
@@ -800,7 +801,10 @@ __global__ __launch_bounds__(64 * WMAX) void k_gemv(const GemvArgs a) {
             if (last) __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
         __syncthreads();
-        if (!last) return;
+        if (!last) {
+            stamp.end();
+            return;
+        }
         constexpr int KSMAX = 8;
         for (int idx = threadIdx.x; idx < rows * COLS; idx += blockDim.x) {
             float pv[KSMAX];
@@ -857,6 +861,7 @@ __global__ __launch_bounds__(64 * WMAX) void k_gemv(const GemvArgs a) {
                 }
             }
         }
+        stamp.end();
         return;
     }
     if (EPI == EPI_STORE || EPI == EPI_QKV) {
@@ -873,6 +878,7 @@ __global__ __launch_bounds__(64 * WMAX) void k_gemv(const GemvArgs a) {
                 }
             }
         }
+        stamp.end();
         return;
     }
     if (EPI == EPI_ARGMAX) {
@@ -900,6 +906,7 @@ __global__ __launch_bounds__(64 * WMAX) void k_gemv(const GemvArgs a) {
                     make_float2(bv, __int_as_float(tile0 * 16 + j * 32 + bi));
             }
         }
+        stamp.end();
         return;
     }
     // EPI_RESID / EPI_SILU finish the group's OC output columns: one k-block of
@@ -974,6 +981,7 @@ __global__ __launch_bounds__(64 * WMAX) void k_gemv(const GemvArgs a) {
                               a.pa, a.pxs);
         }
     }
+    stamp.end();
 }
 
 template <class K>
@@ -1642,6 +1650,7 @@ __global__ __launch_bounds__(256, MINW) void k_attn(AttnArgs a) {
     static_assert(QL <= QM && QL % 8 == 0, "an item's queries fit the partials' stride");
     // grid (kv head, work item): every real item is dispatched before the
     // launch's unused capacity slots, which exit at once
+    const Stamp stamp(a.stamp);
     const int h = blockIdx.x, wi = blockIdx.y;
     // the work item's record: one 64-byte read, everything else is arithmetic
     const int4* rec = (const int4*)(a.wrec + (size_t)wi * 16);
@@ -1956,6 +1965,7 @@ __global__ __launch_bounds__(256, MINW) void k_attn(AttnArgs a) {
             if (i < Q * HD) partq[(i / HD) * (HD + 4) + 4 + i % HD] = ov[j];
         }
     }
+    stamp.end();
 }
 
 // Long-chunk attention (prefill at hd 64 and 128): one workgroup per (kv head, item),
@@ -2170,6 +2180,7 @@ __global__ __launch_bounds__(256, 2) void k_attn_flash(AttnArgs a) {
 template <int HD, int QM, int CK>
 __global__ __launch_bounds__(64) void k_merge_pieces(AttnArgs a, int m, void* __restrict__ out, float* __restrict__ xs,
                                                      int passes) {
+    const Stamp stamp(a.stamp);
     const int kb = blockIdx.x, pass = blockIdx.y, lane = threadIdx.x;
     const int c = lane & 15, row = pass * 4 + (c >> 2), piece = c & 3;
     const int k0 = kb * 32 + (lane >> 4) * 8;
@@ -2177,6 +2188,7 @@ __global__ __launch_bounds__(64) void k_merge_pieces(AttnArgs a, int m, void* __
     if (row < m && k0 < a.nh * HD)
         merge_spans<8>(a.part, *(const int4*)(a.mrec + (size_t)row * 4), a.nh, a.nkv, HD, QM, k0, piece, v);
     write_pieces<CK>(v, kb, pass, passes, row, piece, lane, out, xs);
+    stamp.end();
 }
 
 template <int HD, int P, int QM, int QL, int MINW>
@@ -2208,14 +2220,16 @@ static void attention_hd(hipStream_t st, const AttnArgs& a, int m, int ck, Piece
         attn_ns<HD, P, QM, QM, 2>(st, a);
 merge:
     if (ck < 0) return;  // the consumer merges the spans itself
+    AttnArgs am = a;
+    am.stamp = a.stamp >= 0 ? a.stamp + 1 : -1;  // the merge's timeline slot follows the attention's
     if (ck == BF16)
-        hipLaunchKernelGGL((k_merge_pieces<HD, QM, BF16>), dim3(out.kb, out.passes), dim3(64), 0, st, a, m, out.a,
+        hipLaunchKernelGGL((k_merge_pieces<HD, QM, BF16>), dim3(out.kb, out.passes), dim3(64), 0, st, am, m, out.a,
                            out.xs, out.passes);
     else if (ck == MM)
-        hipLaunchKernelGGL((k_merge_pieces<HD, QM, MM>), dim3(out.kb, out.passes), dim3(64), 0, st, a, m, out.a,
+        hipLaunchKernelGGL((k_merge_pieces<HD, QM, MM>), dim3(out.kb, out.passes), dim3(64), 0, st, am, m, out.a,
                            out.xs, out.passes);
     else
-        hipLaunchKernelGGL((k_merge_pieces<HD, QM, INT8>), dim3(out.kb, out.passes), dim3(64), 0, st, a, m, out.a,
+        hipLaunchKernelGGL((k_merge_pieces<HD, QM, INT8>), dim3(out.kb, out.passes), dim3(64), 0, st, am, m, out.a,
                            out.xs, out.passes);
 }
 
@@ -2297,6 +2311,7 @@ __global__ __launch_bounds__(2 * HD) void k_o_heads(const GemvArgs a) {
     constexpr int KBH = HD / 32, SB = 5, IPR = HD / 2;  // k-blocks of a head, items per row
     __shared__ __align__(16) u16x8 xm[KBH * 64];
     const int t = blockIdx.x, h = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const Stamp stamp(a.stamp);
     const int wg = (int)(blockIdx.x + gridDim.x * blockIdx.y);
     // this n-tile's columns of head h: wave w takes k-blocks w, w + 2, ... (requested first)
     constexpr int KW = (KBH + 1) / 2;
@@ -2354,6 +2369,7 @@ __global__ __launch_bounds__(2 * HD) void k_o_heads(const GemvArgs a) {
     // retire in order, so earlier stores would hold up every wait on a load)
     if (a.zero)
         for (int i = wg * (int)blockDim.x + tid; i < a.zero_n; i += (int)(blockDim.x * gridDim.x * gridDim.y)) a.zero[i] = 0;
+    stamp.end();
 }
 
 int launch_o_heads(hipStream_t st, const DMat& w, const GemvArgs& a, hipEvent_t e0, hipEvent_t e1) {
@@ -2371,6 +2387,22 @@ int launch_o_heads(hipStream_t st, const DMat& w, const GemvArgs& a, hipEvent_t 
         default: return -1;
     }
 }
+
+#ifdef FERRO_STAMPS
+__device__ unsigned long long g_stamps[kStampSlots][kStampWgs][2];
+int stamps_read(uint64_t* out, int slots) {
+    if (slots < 0 || slots > kStampSlots) return -1;
+    return hipMemcpyFromSymbol(out, HIP_SYMBOL(g_stamps), (size_t)slots * kStampWgs * 2 * 8) == hipSuccess ? 0 : -1;
+}
+int stamps_clear() {
+    void* p = nullptr;
+    if (hipGetSymbolAddress(&p, HIP_SYMBOL(g_stamps)) != hipSuccess) return -1;
+    return hipMemset(p, 0, sizeof(g_stamps)) == hipSuccess ? 0 : -1;
+}
+#else
+int stamps_read(uint64_t*, int) { return -1; }
+int stamps_clear() { return -1; }
+#endif
 
 int launch_attention(hipStream_t st, const AttnArgs& a, int m, int consumer_kind, Pieces& out) {
     if (m <= 0 || a.n_wi <= 0) return 0;

@@ -7,6 +7,7 @@ calls raise.
 from __future__ import annotations
 
 import ctypes as C
+import os
 from dataclasses import dataclass
 from pathlib import Path
 
@@ -15,7 +16,9 @@ import numpy as np
 from .weights import BF16, INT8, Config, HostModel, Matrix
 
 PKG = Path(__file__).resolve().parent
-LIB_PATH = PKG / "libferro_gpu.so"
+# FERRO_STAMPS=1 loads the library built with the in-kernel timeline (python -m
+# ferrolm_amd.build --stamps): the same kernels, each recording its entry and exit
+LIB_PATH = PKG / ("libferro_gpu_stamps.so" if os.environ.get("FERRO_STAMPS") == "1" else "libferro_gpu.so")
 
 f32p = C.POINTER(C.c_float)
 u16p = C.POINTER(C.c_uint16)
@@ -121,6 +124,8 @@ EXPORTS = {
                                      C.POINTER(FgSampling), u64p, u32p, i32p]),
     "fg_last_step_times": (C.c_int, [C.c_void_p, f32p]),
     "fg_profile": (C.c_int, [C.c_void_p, C.c_int32]),
+    "fg_stamps_reset": (C.c_int, [C.c_void_p]),
+    "fg_stamps_read": (C.c_int, [C.c_void_p, C.c_int32, C.c_void_p, C.c_char_p, C.c_int32]),
     "fg_profile_read": (C.c_int, [C.c_void_p, C.c_int32, i32p, C.POINTER(C.c_int64), C.POINTER(C.c_double),
                                   C.POINTER(C.c_double), C.POINTER(C.c_double), C.c_int32]),
     "fg_mat_upload": (C.c_int, [C.c_void_p, C.POINTER(FgMatrix), C.POINTER(C.c_void_p)]),
@@ -489,6 +494,22 @@ def last_step_times(ctx: Context) -> np.ndarray:
 
 
 KIND_LABEL = {0: "bf16", 1: "int8", 2: "int4"}
+
+
+def stamps_reset(ctx: Context) -> None:
+    """Clears the in-kernel timeline (fg_stamps_reset; a library built with stamps)."""
+    check(lib().fg_stamps_reset(ctx.h))
+
+
+def stamps_read(ctx: Context, slots: int = 1024):
+    """(ticks [slots][1024 workgroups][entry, exit] uint64 at 100 MHz, 0 = no record;
+    labels of the labelled slots) (fg_stamps_read)."""
+    ticks = np.zeros((slots, 1024, 2), np.uint64)
+    buf = C.create_string_buffer(1 << 16)
+    n = lib().fg_stamps_read(ctx.h, slots, ticks.ctypes.data_as(C.c_void_p), buf, len(buf))
+    if n < 0:
+        check(n)
+    return ticks, buf.value.decode().split("\n")[:n]
 
 
 def profile(ctx: Context, on: bool) -> None:

@@ -272,6 +272,21 @@ int fg_last_step_times(const fg_ctx* ctx, float* us3);
  * (summed algorithmic flops, 2 x rows x n x k per launch).
  * Returns the record count (or a negative error). reset != 0 clears. */
 int fg_profile(fg_ctx* ctx, int32_t on);
+/* In-kernel timeline of the GEMV, attention, merge and split output-projection
+ * launches (no reference counterpart; a measurement aid). Only a library built
+ * with stamps records (python -m ferrolm_amd.build --stamps, which writes
+ * libferro_gpu_stamps.so): each such launch takes the next slot in launch order,
+ * starting at 0 in every fg_forward and speculative step (a step replayed from
+ * a graph keeps the slots of its capture), and thread 0 of each of its first
+ * 1024 workgroups stores its s_memrealtime ticks (100 MHz) at entry and at exit.
+ * fg_stamps_reset synchronises and clears every slot. fg_stamps_read
+ * synchronises, copies `slots` (at most 1024) slots of 1024 workgroups x
+ * {entry, exit} ticks (0: no record) into ticks, and the slots' kernel labels,
+ * one per line, into labels (label_cap bytes, NUL-terminated); it returns the
+ * number of labelled slots. Both return FG_E_ARG in a library built without
+ * stamps. */
+int fg_stamps_reset(fg_ctx* ctx);
+int fg_stamps_read(fg_ctx* ctx, int32_t slots, uint64_t* ticks, char* labels, int32_t label_cap);
 int fg_profile_read(fg_ctx* ctx, int32_t cap, int32_t* cls, int64_t* launches,
                     double* us, double* bytes, double* flops, int32_t reset);
 
