@@ -357,7 +357,9 @@ class Engine:
         k = cfg.spec_k if self.draft is not None else 0
         budget = cfg.max_batch_tokens
         plans = []
-        # running sequences, oldest first; the newest are preempted first
+        # Sequences already in flight are served in admission order. When the
+        # block pool cannot cover one of them, the most recently admitted
+        # sequence gives its blocks back and is requeued.
         i = 0
         while i < len(self.running) and budget > 0:
             s = self.running[i]
@@ -372,7 +374,8 @@ class Engine:
                 i += 1
                 continue
             self._preempt(self.running.pop())
-        # new requests, first come first served
+        # Then the queue, strictly in arrival order: admission stops at the first
+        # request that does not fit.
         static_open = not self.running
         while self.waiting:
             s = self.waiting[0]
@@ -382,7 +385,9 @@ class Engine:
                 break
             if cfg.admission == "static" and not static_open:
                 break
-            # leading full blocks already cached (never the block of the last prompt token)
+            # Reuse published blocks for the prompt's whole leading blocks. The
+            # block that holds the final prompt token is always recomputed: its
+            # forward produces the logits of the first new token.
             if not s.blocks:
                 parent = ROOT
                 body = s.tokens[:len(s.tokens) - 1]

@@ -100,8 +100,11 @@ def test_bf16_round_to_nearest_even():
 #    here from the golden ratio; the output multiplier is the published
 #    xorshift64* constant 2685821657736338717 (Vigna, "An experimental
 #    exploration of Marsaglia's xorshift generators, scrambled", 2016);
-#  - uniform = top 53 bits / 2^53 and normal = Box-Muller of two uniforms,
-#    bit for bit from the oracle's own stream, and the normals pass a KS test.
+#  - uniform = top 53 bits / 2^53, bit for bit from the oracle's own stream;
+#  - normal: only its distribution is pinned (a KS test and the moments). Which
+#    of its two uniforms sets the radius and which the angle follows the
+#    reference's text (src/rng.rs:41-45); a swapped order would pass every check
+#    here. The bit-for-bit check below restates the formula and pins nothing more.
 # ---------------------------------------------------------------------------
 MASK64 = (1 << 64) - 1
 PRIMES_2_64_MINUS_1 = [3, 5, 17, 257, 641, 65537, 6700417]
