@@ -65,6 +65,22 @@ struct Stamp {
 // round to nearest even (v_cvt_pk_bf16_f32)
 __device__ __forceinline__ uint32_t f32_to_bf16_bits(float x) { return __builtin_bit_cast(uint16_t, (__bf16)x); }
 
+__device__ __forceinline__ bf16x8 as_bf16x8(u16x8 v) { return __builtin_bit_cast(bf16x8, v); }
+__device__ __forceinline__ bf16x8 as_bf16x8(u32x4 v) { return __builtin_bit_cast(bf16x8, v); }
+
+// Four f32 values as two bf16 pieces each, hi = bf16(x) and lo = bf16(x - hi),
+// stored as four consecutive bf16 at hi and at lo (8-byte aligned).
+__device__ __forceinline__ void split4(const float (&v)[4], uint16_t* hi, uint16_t* lo) {
+    uint32_t h[4], l[4];
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        h[e] = f32_to_bf16_bits(v[e]);
+        l[e] = f32_to_bf16_bits(v[e] - bf16_bits_to_f32(h[e]));
+    }
+    *(uint2*)hi = make_uint2(h[0] | (h[1] << 16), h[2] | (h[3] << 16));
+    *(uint2*)lo = make_uint2(l[0] | (l[1] << 16), l[2] | (l[3] << 16));
+}
+
 // exp(x) by range reduction and the Cephes expf polynomial, the same
 // sequence of operations as the reference's kernels::exp (src/kernels.rs:609-637).
 __device__ __forceinline__ float dev_exp(float x) {

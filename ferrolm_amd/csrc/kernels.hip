@@ -1636,11 +1636,28 @@ void launch_gemv(hipStream_t st, int epi, const DMat& w, const GemvArgs& a, hipE
 template <int HD, int P, int QM, int NS, int QL = QM, int MINW = 2>
 __global__ __launch_bounds__(256, MINW) void k_attn(AttnArgs a) {
     constexpr int HALF = HD / 2;
-    // rows padded by 4 floats (16-byte aligned): lanes reading one column of
+    // Items of several sub-spans at head_dim 128 with 16 or more queries (GQA
+    // verify batches) score and weigh on bf16 MFMA with split operands: every f32
+    // value x of q, k, the probabilities and v is held as hi = bf16(x) and lo =
+    // bf16(x - hi), and a product as lo*hi + hi*lo + hi*hi
+    // (v_mfma_f32_16x16x32_bf16, three per 32 inputs, f32 accumulation): 2^-16 of
+    // each term against the f32 MFMA's 2^-24, at five times its rate. (cfg4's 8B
+    // target: 92.6 -> 82.2 us per layer. At head_dim 64 with 8 queries the
+    // splitting and the column reads of v cost more than the MFMA saves: 112.3
+    // -> 126.7 us per layer for cfg3's target at 32 sequences.)
+    constexpr bool BF = NS > 1 && HD >= 128 && HD % 32 == 0 && P % 32 == 0 && QL >= 16;
+    // f32 rows padded by 4 floats (16-byte aligned): lanes reading one column of
     // consecutive rows (the MFMA operands) hit distinct banks
-    __shared__ __align__(16) float ks[P][HD + 4];
-    __shared__ __align__(16) float vs[P][HD + 4];
-    __shared__ __align__(16) float qs[QL][HD + 4];
+    __shared__ __align__(16) float ks[BF ? 1 : P][HD + 4];
+    __shared__ __align__(16) float vs[BF ? 1 : P][HD + 4];
+    __shared__ __align__(16) float qs[BF ? 1 : QL][HD + 4];
+    // (BF) the pieces: q and k rows read 8 inputs per lane (16 bytes; rows 16
+    // bytes apart in the bank map), v columns 2 bytes per lane (rows 8 bytes apart)
+    __shared__ __align__(16) uint16_t qh[BF ? QL : 1][HD + 8], ql[BF ? QL : 1][HD + 8];
+    __shared__ __align__(16) uint16_t kh[BF ? P : 1][HD + 8], kl[BF ? P : 1][HD + 8];
+    __shared__ __align__(16) uint16_t vh[BF ? P : 1][HD + 4], vl[BF ? P : 1][HD + 4];
+    // scores; (BF) after the softmax each slot holds its probability's pieces,
+    // hi in the low half (written by the thread that read the score)
     __shared__ __align__(16) float pr[QL][P + 4];
     __shared__ int lim[QL];
     __shared__ float mrun[NS > 1 ? QL : 1], lrun[NS > 1 ? QL : 1], fac[NS > 1 ? QL : 1];
@@ -1742,10 +1759,21 @@ __global__ __launch_bounds__(256, MINW) void k_attn(AttnArgs a) {
             const float a2[4] = {qx2[it].x, qx2[it].y, qx2[it].z, qx2[it].w};
             const float cc[4] = {qcs[it].x, qcs[it].y, qcs[it].z, qcs[it].w};
             const float ss[4] = {qsn[it].x, qsn[it].y, qsn[it].z, qsn[it].w};
+            float r1[4], r2[4];
 #pragma unroll
             for (int e = 0; e < 4; e++) {
-                qs[q][d + e] = __fadd_rn(__fmul_rn(a1[e], cc[e]), __fmul_rn(-a2[e], ss[e]));
-                qs[q][d + HALF + e] = __fadd_rn(__fmul_rn(a2[e], cc[e]), __fmul_rn(a1[e], ss[e]));
+                r1[e] = __fadd_rn(__fmul_rn(a1[e], cc[e]), __fmul_rn(-a2[e], ss[e]));
+                r2[e] = __fadd_rn(__fmul_rn(a2[e], cc[e]), __fmul_rn(a1[e], ss[e]));
+            }
+            if constexpr (BF) {
+                split4(r1, &qh[q][d], &ql[q][d]);
+                split4(r2, &qh[q][d + HALF], &ql[q][d + HALF]);
+            } else {
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    qs[q][d + e] = r1[e];
+                    qs[q][d + HALF + e] = r2[e];
+                }
             }
         }
     }
@@ -1776,6 +1804,13 @@ __global__ __launch_bounds__(256, MINW) void k_attn(AttnArgs a) {
         if (sp0 >= p1) break;
         const int sp1 = min(sp0 + P, p1);
         if (s > 0) __syncthreads();  // the previous sub-span's readers of ks, vs and pr are done
+        // (BF) this group's new rows in the sub-span: written to the cache from
+        // the staging registers (the pieces in LDS are not the f32 values)
+        const int nr0 = max(max(sp0, cpos0), cpos0 + row0 - crow0);
+        const int nr1 = min(sp1, cpos0 + row0 + nrows - crow0);
+        auto cache_at = [&](int p, int d) {
+            return ((blk((p - p0) >> 4) * a.nkv + h) * 16 + (p & 15)) * HD + d;
+        };
         // keys (rotated when new) and values to LDS
 #pragma unroll
         for (int it = 0; it < KIT; it++) {
@@ -1787,12 +1822,27 @@ __global__ __launch_bounds__(256, MINW) void k_attn(AttnArgs a) {
                 const float cc[4] = {kcs[it].x, kcs[it].y, kcs[it].z, kcs[it].w};
                 const float ss[4] = {ksn[it].x, ksn[it].y, ksn[it].z, ksn[it].w};
                 const bool live = p < sp1, rot = live && p >= cpos0;
+                float r1[4], r2[4];
 #pragma unroll
                 for (int e = 0; e < 4; e++) {
-                    const float r1 = rot ? __fadd_rn(__fmul_rn(a1[e], cc[e]), __fmul_rn(-a2[e], ss[e])) : a1[e];
-                    const float r2 = rot ? __fadd_rn(__fmul_rn(a2[e], cc[e]), __fmul_rn(a1[e], ss[e])) : a2[e];
-                    ks[o][d + e] = live ? r1 : 0.0f;
-                    ks[o][d + HALF + e] = live ? r2 : 0.0f;
+                    const float x1 = rot ? __fadd_rn(__fmul_rn(a1[e], cc[e]), __fmul_rn(-a2[e], ss[e])) : a1[e];
+                    const float x2 = rot ? __fadd_rn(__fmul_rn(a2[e], cc[e]), __fmul_rn(a1[e], ss[e])) : a2[e];
+                    r1[e] = live ? x1 : 0.0f;
+                    r2[e] = live ? x2 : 0.0f;
+                }
+                if constexpr (BF) {
+                    split4(r1, &kh[o][d], &kl[o][d]);
+                    split4(r2, &kh[o][d + HALF], &kl[o][d + HALF]);
+                    if (p >= nr0 && p < nr1) {
+                        *(float4*)(a.kc + cache_at(p, d)) = make_float4(r1[0], r1[1], r1[2], r1[3]);
+                        *(float4*)(a.kc + cache_at(p, d + HALF)) = make_float4(r2[0], r2[1], r2[2], r2[3]);
+                    }
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 4; e++) {
+                        ks[o][d + e] = r1[e];
+                        ks[o][d + HALF + e] = r2[e];
+                    }
                 }
             }
         }
@@ -1801,23 +1851,29 @@ __global__ __launch_bounds__(256, MINW) void k_attn(AttnArgs a) {
             for (int it = 0; it < VIT; it++) {
                 const int i = tid + it * 256;
                 if (i < VI) {
-                    const bool live = sp0 + i / (HD / 4) < sp1;
-                    *(float4*)&vs[i / (HD / 4)][(i % (HD / 4)) * 4] =
-                        make_float4(live ? vv[it].x : 0.0f, live ? vv[it].y : 0.0f, live ? vv[it].z : 0.0f,
-                                    live ? vv[it].w : 0.0f);
+                    const int o = i / (HD / 4), d = (i % (HD / 4)) * 4, p = sp0 + o;
+                    const bool live = p < sp1;
+                    const float v4[4] = {live ? vv[it].x : 0.0f, live ? vv[it].y : 0.0f, live ? vv[it].z : 0.0f,
+                                         live ? vv[it].w : 0.0f};
+                    if constexpr (BF) {
+                        split4(v4, &vh[o][d], &vl[o][d]);
+                        if (p >= nr0 && p < nr1) *(float4*)(a.vc + cache_at(p, d)) = make_float4(v4[0], v4[1], v4[2], v4[3]);
+                    } else {
+                        *(float4*)&vs[o][d] = make_float4(v4[0], v4[1], v4[2], v4[3]);
+                    }
                 }
             }
         };
         // this group's new rows in the sub-span go to the cache (from ks and vs;
         // other items read new positions from the q/k/v rows, never the cache)
         auto new_rows_to_cache = [&]() {
-            const int n0 = max(max(sp0, cpos0), cpos0 + row0 - crow0);
-            const int n1 = min(sp1, cpos0 + row0 + nrows - crow0);
-            for (int i = tid; i < (n1 - n0) * HD; i += 256) {
-                const int p = n0 + i / HD, d = i % HD, o = p - sp0;
-                const size_t at = ((blk((p - p0) >> 4) * a.nkv + h) * 16 + (p & 15)) * HD + d;
-                a.kc[at] = ks[o][d];
-                a.vc[at] = vs[o][d];
+            if constexpr (!BF) {
+                for (int i = tid; i < (nr1 - nr0) * HD; i += 256) {
+                    const int p = nr0 + i / HD, d = i % HD, o = p - sp0;
+                    const size_t at = cache_at(p, d);
+                    a.kc[at] = ks[o][d];
+                    a.vc[at] = vs[o][d];
+                }
             }
         };
         // An item of one sub-span scores its keys while its values are still
@@ -1835,11 +1891,25 @@ __global__ __launch_bounds__(256, MINW) void k_attn(AttnArgs a) {
             constexpr int NTP = P / 16;
             for (int ti = wave; ti < mtu * NTP; ti += 4) {
                 const int mt = ti / NTP, nt = ti % NTP, kk = lane >> 4;
-                const float* qa = &qs[qrow(mt * 16 + (lane & 15))][kk];
-                const float* kb = &ks[nt * 16 + (lane & 15)][kk];
                 f32x4 c = {0.0f, 0.0f, 0.0f, 0.0f};
+                if constexpr (BF) {
+                    // A: q row mt*16 + lane%16, inputs d0 + 8 (lane/16) .. + 7; B: the same inputs of key nt*16 + lane%16
+                    const int qr = qrow(mt * 16 + (lane & 15)), kr = nt * 16 + (lane & 15);
 #pragma unroll
-                for (int d0 = 0; d0 < HD; d0 += 4) c = __builtin_amdgcn_mfma_f32_16x16x4f32(qa[d0], kb[d0], c, 0, 0, 0);
+                    for (int d0 = 0; d0 < HD; d0 += 32) {
+                        const int dd = d0 + 8 * kk;
+                        const bf16x8 ah = as_bf16x8(*(const u16x8*)&qh[qr][dd]), al = as_bf16x8(*(const u16x8*)&ql[qr][dd]);
+                        const bf16x8 bh = as_bf16x8(*(const u16x8*)&kh[kr][dd]), bl = as_bf16x8(*(const u16x8*)&kl[kr][dd]);
+                        c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, bh, c, 0, 0, 0);
+                        c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bl, c, 0, 0, 0);
+                        c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bh, c, 0, 0, 0);
+                    }
+                } else {
+                    const float* qa = &qs[qrow(mt * 16 + (lane & 15))][kk];
+                    const float* kb = &ks[nt * 16 + (lane & 15)][kk];
+#pragma unroll
+                    for (int d0 = 0; d0 < HD; d0 += 4) c = __builtin_amdgcn_mfma_f32_16x16x4f32(qa[d0], kb[d0], c, 0, 0, 0);
+                }
 #pragma unroll
                 for (int r = 0; r < 4; r++)
                     if (mt * 16 + 4 * kk + r < QL) pr[mt * 16 + 4 * kk + r][nt * 16 + (lane & 15)] = c[r] * a.scale;
@@ -1860,7 +1930,7 @@ __global__ __launch_bounds__(256, MINW) void k_attn(AttnArgs a) {
             float sc = -INFINITY;
             if (q < Q && p < sp1 && p <= lim[q] && mf) {
                 sc = pr[q][o];
-            } else if (q < Q && p < sp1 && p <= lim[q]) {
+            } else if (!BF && q < Q && p < sp1 && p <= lim[q]) {
                 const float4* kr = (const float4*)&ks[o][0];
                 const float4* qr = (const float4*)&qs[q][0];
                 float acc = 0.0f;
@@ -1882,7 +1952,12 @@ __global__ __launch_bounds__(256, MINW) void k_attn(AttnArgs a) {
             const float e = (sc == -INFINITY) ? 0.0f : dev_exp(sc - mx);
             const float sum = group_reduce<P, false>(e);
             if (q < Q) {
-                pr[q][o] = e;
+                if constexpr (BF) {
+                    const uint32_t eh = f32_to_bf16_bits(e), el = f32_to_bf16_bits(e - bf16_bits_to_f32(eh));
+                    ((uint32_t*)&pr[q][0])[o] = eh | (el << 16);
+                } else {
+                    pr[q][o] = e;
+                }
                 if (o == 0) {
                     if (NS == 1) {
                         partq[q * (HD + 4)] = mx;
@@ -1910,11 +1985,40 @@ __global__ __launch_bounds__(256, MINW) void k_attn(AttnArgs a) {
 #pragma unroll
                         for (int r = 0; r < 4; r++) oc[j][r] *= fac[qrow(mt * 16 + 4 * kk + r)];
                     }
-                    const float* pa = &pr[qrow(mt * 16 + (lane & 15))][kk];
-                    const float* vb = &vs[kk][nd * 16 + (lane & 15)];
+                    if constexpr (BF) {
+                        // A: the probabilities of row mt*16 + lane%16 at positions k0 + 8 (lane/16) .. + 7
+                        // (pairs (hi, lo) per slot, split here); B: value column nd*16 + lane%16 at the same positions
+                        const uint32_t* prow = (const uint32_t*)&pr[qrow(mt * 16 + (lane & 15))][0];
+                        const int vc = nd * 16 + (lane & 15);
 #pragma unroll
-                    for (int k0 = 0; k0 < P; k0 += 4)
-                        oc[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(pa[k0], vb[k0 * (HD + 4)], oc[j], 0, 0, 0);
+                        for (int k0 = 0; k0 < P; k0 += 32) {
+                            const int kp = k0 + 8 * kk;
+                            const u32x4 w0 = *(const u32x4*)&prow[kp], w1 = *(const u32x4*)&prow[kp + 4];
+                            u32x4 ah4, al4, bh4, bl4;
+#pragma unroll
+                            for (int e = 0; e < 2; e++) {
+                                ah4[e] = (w0[2 * e] & 0xFFFFu) | (w0[2 * e + 1] << 16);
+                                al4[e] = (w0[2 * e] >> 16) | (w0[2 * e + 1] & 0xFFFF0000u);
+                                ah4[e + 2] = (w1[2 * e] & 0xFFFFu) | (w1[2 * e + 1] << 16);
+                                al4[e + 2] = (w1[2 * e] >> 16) | (w1[2 * e + 1] & 0xFFFF0000u);
+                            }
+#pragma unroll
+                            for (int e = 0; e < 4; e++) {
+                                bh4[e] = (uint32_t)vh[kp + 2 * e][vc] | ((uint32_t)vh[kp + 2 * e + 1][vc] << 16);
+                                bl4[e] = (uint32_t)vl[kp + 2 * e][vc] | ((uint32_t)vl[kp + 2 * e + 1][vc] << 16);
+                            }
+                            const bf16x8 ah = as_bf16x8(ah4), al = as_bf16x8(al4), bh = as_bf16x8(bh4), bl = as_bf16x8(bl4);
+                            oc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, bh, oc[j], 0, 0, 0);
+                            oc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bl, oc[j], 0, 0, 0);
+                            oc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bh, oc[j], 0, 0, 0);
+                        }
+                    } else {
+                        const float* pa = &pr[qrow(mt * 16 + (lane & 15))][kk];
+                        const float* vb = &vs[kk][nd * 16 + (lane & 15)];
+#pragma unroll
+                        for (int k0 = 0; k0 < P; k0 += 4)
+                            oc[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(pa[k0], vb[k0 * (HD + 4)], oc[j], 0, 0, 0);
+                    }
                 }
             }
         } else {
