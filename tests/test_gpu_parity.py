@@ -224,6 +224,53 @@ def test_batched_speculative_steps_gqa_head_dim_128(ctx):
     _batched_matches_oracle(ctx, hm, prompts, k=4, steps=6, kv_blocks=160, seed=6)
 
 
+def test_split_bf16_attention_head_dim_128_matches_oracle(ctx):
+    """The split-operand bf16 MFMA attention (items of four 32-position
+    sub-spans, 20 queries each: five verify rows of a GQA-4 model at head_dim
+    128): four sequences of 4,100 to 4,300 positions make more than 1024
+    one-span items, which is when the plan takes sub-spans. One forward of five
+    rows per sequence, all logits and every layer's hidden state, against the
+    oracle from a copy of the device's cache (src/model.rs:395-432,
+    src/kernels.rs:671-756). Each product term is within 2^-16 of its f32 value;
+    the bars are the ones the f32 paths hold (measured: logits 2.6e-5 and
+    hidden states 2.3e-5 relative, against 1.2e-5 for both with f32 MFMA)."""
+    from ferrolm_amd.synth import random_model
+    from ferrolm_amd.weights import Config
+    cfg = Config(vocab=512, hidden=1024, intermediate=1024, layers=2, heads=8, kv_heads=2, head_dim=128,
+                 rms_eps=1e-5, rope_theta=500000.0, max_position=8192)
+    hm = random_model(cfg, seed=21, std=0.05)
+    rng = np.random.default_rng(22)
+    lens = [4100, 4170, 4230, 4300]
+    per_seq = max(lens) // 16 + 2
+    nb = per_seq * len(lens)
+    perm = [int(x) for x in rng.permutation(nb)]
+    tables = [perm[i * per_seq:(i + 1) * per_seq] for i in range(len(lens))]
+    prompts = [[int(x) for x in rng.integers(3, 500, n)] for n in lens]
+    gm = gpu.Model(ctx, hm)
+    kv = gpu.KvCache(ctx, cfg, nb)
+    for p, tb in zip(prompts, tables):
+        for a in range(0, len(p), 2048):
+            gpu.forward(ctx, gm, kv, [(p[a:a + 2048], a, tb, gpu.LOGITS_NONE)], logits=False)
+    om = oracle.Model(hm)
+    okv = om.kv(nb)
+    for i in range(cfg.layers):
+        okv.set_layer(i, *kv.layer(i))
+    chunks = [([int(x) for x in rng.integers(3, 500, 5)], n, tb, gpu.LOGITS_ALL) for n, tb in zip(lens, tables)]
+    out = gpu.forward(ctx, gm, kv, chunks, hidden=True)
+    ol, oh = om.forward(okv, chunks, hidden=True)
+    lrel = np.abs(out.logits - ol).max(axis=1) / np.abs(ol).max(axis=1)
+    hrel = np.linalg.norm(out.hidden - oh, axis=-1) / np.linalg.norm(oh, axis=-1)
+    print(f"split bf16 attention, hd 128: logits rel max {lrel.max():.2e}, hidden rel max {hrel.max():.2e}")
+    assert out.logits.shape == (20, cfg.vocab)
+    assert lrel.max() <= 1e-4 and hrel.max() <= 1e-4, (lrel.max(), hrel.max())
+    assert_argmax_parity(out.argmax, ol, tol=2e-3, max_ties=1)
+    for i in range(cfg.layers):  # the new rows' cache slots
+        gk, gv = kv.layer(i)
+        ok, ov = okv.layer(i)
+        assert np.abs(gk - ok).max() <= 1e-4 * np.abs(ok).max()
+        assert np.abs(gv - ov).max() <= 1e-4 * np.abs(ov).max()
+
+
 @pytest.mark.parametrize("n_seqs", [1, 2])
 def test_speculative_steps_head_dim_64_one_and_two_passes(ctx, n_seqs):
     """Head dim 64 (64-position spans, three query heads per kv head): one sequence
