@@ -28,6 +28,17 @@
 
 namespace fg {
 
+// The int8 pieces layout: a lane's slots (8 bytes: pieces of 8 inputs) of the
+// four k-blocks of a chunk sit together (32 bytes), so a consumer reads them in
+// two 16-byte loads; the block scales 2^e likewise, [chunk][row][4 k-blocks].
+// Indices in 8-byte slots and in floats.
+__device__ __forceinline__ size_t i8_slot(int kb, int pass, int passes, int lane) {
+    return ((((size_t)(kb >> 2) * passes + pass) * 64 + lane) << 2) + (kb & 3);
+}
+__device__ __forceinline__ size_t i8_scale(int kb, int passes, int row) {
+    return (((size_t)(kb >> 2) * passes * 4 + row) << 2) + (kb & 3);
+}
+
 template <int CK>
 __device__ __forceinline__ void write_pieces(const float (&v)[8], int kb, int pass, int passes, int row, int piece,
                                              int lane, void* out, float* xs) {
@@ -57,8 +68,8 @@ __device__ __forceinline__ void write_pieces(const float (&v)[8], int kb, int pa
         i8x8 o;
 #pragma unroll
         for (int s = 0; s < 8; s++) o[s] = (int8_t)int8_piece(v[s], e, piece);
-        ((i8x8*)out)[slot] = o;
-        if (lane < 16 && (lane & 3) == 0) xs[(size_t)kb * passes * 4 + row] = ldexpf(1.0f, e);
+        ((i8x8*)out)[i8_slot(kb, pass, passes, lane)] = o;
+        if (lane < 16 && (lane & 3) == 0) xs[i8_scale(kb, passes, row)] = ldexpf(1.0f, e);
     }
 }
 
@@ -83,9 +94,9 @@ __device__ __forceinline__ void write_pieces_pair(float x0, float x1, float mx, 
         ((uint32_t*)out)[slot * 4 + pair] = bf16_piece(x0, piece) | (bf16_piece(x1, piece) << 16);
     } else {
         const int e = int8_block_exp(mx);
-        ((uint16_t*)out)[slot * 4 + pair] =
+        ((uint16_t*)out)[i8_slot(kb, pass, passes, lane) * 4 + pair] =
             (uint16_t)((uint8_t)int8_piece(x0, e, piece) | ((uint32_t)(uint8_t)int8_piece(x1, e, piece) << 8));
-        if (pair == 0 && lane < 16 && (lane & 3) == 0) xs[(size_t)kb * passes * 4 + row] = ldexpf(1.0f, e);
+        if (pair == 0 && lane < 16 && (lane & 3) == 0) xs[i8_scale(kb, passes, row)] = ldexpf(1.0f, e);
     }
 }
 
@@ -490,11 +501,12 @@ __global__ __launch_bounds__(64 * WMAX) void k_gemv(const GemvArgs a) {
                     // lanes of input rows past m read row 4 pp's slot instead (the same
                     // addresses as its lanes, so no extra bytes move; those output rows
                     // are dropped): at one row, a quarter of the operand's bytes
-                    const size_t idx = ((size_t)(kb + j) * a.p_total + pp) * 64 + (lane_alive(pp) ? lane : (lane & ~12));
+                    const int al = lane_alive(pp) ? lane : (lane & ~12);
                     if (Q) {
-                        aq[u][j][p] = ((const long*)a.XA)[idx];
-                        sx[u][j][p] = a.XS[(size_t)(kb + j) * a.p_total * 4 + pp * 4 + (lane >> 4)];
+                        aq[u][j][p] = ((const long*)a.XA)[i8_slot(kb + j, pp, a.p_total, al)];
+                        sx[u][j][p] = a.XS[i8_scale(kb + j, a.p_total, pp * 4 + (lane >> 4))];
                     } else {
+                        const size_t idx = ((size_t)(kb + j) * a.p_total + pp) * 64 + al;
                         ab[u][j][p] = ((const bf16x8*)a.XA)[idx];
                     }
                 }
