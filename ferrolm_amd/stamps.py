@@ -22,11 +22,7 @@ import os
 import sys
 from collections import defaultdict
 
-os.environ["FERRO_STAMPS"] = "1"  # before the binding loads its library
-
-import numpy as np  # noqa: E402
-
-from . import gpu, spec, synth  # noqa: E402
+import numpy as np
 
 TICK_US = 0.01  # s_memrealtime counts at 100 MHz
 
@@ -46,6 +42,11 @@ def timeline(ticks: np.ndarray, labels: list) -> list:
 
 
 def main() -> int:
+    # the binding picks its library when it is first imported: the stamps build
+    os.environ["FERRO_STAMPS"] = "1"
+    from . import gpu, spec, synth
+    if not gpu.LIB_PATH.name.endswith("_stamps.so"):
+        raise SystemExit("ferrolm_amd.gpu was imported before the stamps library was selected")
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--config", type=int, default=2)
     ap.add_argument("--warmup", type=int, default=8)
