@@ -1622,6 +1622,17 @@ void launch_gemv(hipStream_t st, int epi, const DMat& w, const GemvArgs& a, hipE
         gemv_kind<BF16>(st, epi, w, a, start, stop);
 }
 
+// The V tile in LDS (f32, rows = positions): at HD >= 64 rows are unpadded and
+// the four 16-float quarters of row r are permuted by r % 4 (an XOR of column
+// bits 4-5). The PV products read, per MFMA, 16 consecutive columns of 4
+// consecutive rows (B[k][j] in lane j + 16k): with the permutation the 64 lanes
+// hit 64 distinct banks; with rows padded by 4 floats they met 4 to a bank.
+constexpr int vstride(int hd) { return hd >= 64 ? hd : hd + 4; }
+template <int HD>
+__device__ __forceinline__ int vcol(int r, int d) {
+    return HD >= 64 ? d ^ ((r & 3) << 4) : d;
+}
+
 // ---------------------------------------------------------------------------
 // Paged attention, split over the context (flash-decoding). A work item is
 // (row group, span of P positions) x kv head: the rows of a group are
@@ -1661,7 +1672,7 @@ __global__ __launch_bounds__(256, MINW) void k_attn(AttnArgs a) {
     // f32 rows padded by 4 floats (16-byte aligned): lanes reading one column of
     // consecutive rows (the MFMA operands) hit distinct banks
     __shared__ __align__(16) float ks[BF ? 1 : P][HD + 4];
-    __shared__ __align__(16) float vs[BF ? 1 : P][HD + 4];
+    __shared__ __align__(16) float vs[BF ? 1 : P][vstride(HD)];
     __shared__ __align__(16) float qs[BF ? 1 : QL][HD + 4];
     // (BF) the pieces: q and k rows read 8 inputs per lane (16 bytes; rows 16
     // bytes apart in the bank map), v columns 2 bytes per lane (rows 8 bytes apart)
@@ -1871,7 +1882,7 @@ __global__ __launch_bounds__(256, MINW) void k_attn(AttnArgs a) {
                         split4(v4, &vh[o][d], &vl[o][d]);
                         if (p >= nr0 && p < nr1) *(float4*)(a.vc + cache_at(p, d)) = make_float4(v4[0], v4[1], v4[2], v4[3]);
                     } else {
-                        *(float4*)&vs[o][d] = make_float4(v4[0], v4[1], v4[2], v4[3]);
+                        *(float4*)&vs[o][vcol<HD>(o, d)] = make_float4(v4[0], v4[1], v4[2], v4[3]);
                     }
                 }
             }
@@ -1884,7 +1895,7 @@ __global__ __launch_bounds__(256, MINW) void k_attn(AttnArgs a) {
                     const int p = nr0 + i / HD, d = i % HD, o = p - sp0;
                     const size_t at = cache_at(p, d);
                     a.kc[at] = ks[o][d];
-                    a.vc[at] = vs[o][d];
+                    a.vc[at] = vs[o][vcol<HD>(o, d)];
                 }
             }
         };
@@ -2026,10 +2037,10 @@ __global__ __launch_bounds__(256, MINW) void k_attn(AttnArgs a) {
                         }
                     } else {
                         const float* pa = &pr[qrow(mt * 16 + (lane & 15))][kk];
-                        const float* vb = &vs[kk][nd * 16 + (lane & 15)];
+                        const float* vb = &vs[kk][vcol<HD>(kk, nd * 16 + (lane & 15))];  // rows kk + k0: k0 % 4 == 0
 #pragma unroll
                         for (int k0 = 0; k0 < P; k0 += 4)
-                            oc[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(pa[k0], vb[k0 * (HD + 4)], oc[j], 0, 0, 0);
+                            oc[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(pa[k0], vb[k0 * vstride(HD)], oc[j], 0, 0, 0);
                     }
                 }
             }
@@ -2045,10 +2056,10 @@ __global__ __launch_bounds__(256, MINW) void k_attn(AttnArgs a) {
 #pragma unroll
                     for (int o4 = 0; o4 < P / 4; o4++) {
                         const float4 w = prr[o4];
-                        acc = fmaf(w.x, vs[4 * o4][d], acc);
-                        acc = fmaf(w.y, vs[4 * o4 + 1][d], acc);
-                        acc = fmaf(w.z, vs[4 * o4 + 2][d], acc);
-                        acc = fmaf(w.w, vs[4 * o4 + 3][d], acc);
+                        acc = fmaf(w.x, vs[4 * o4][vcol<HD>(0, d)], acc);
+                        acc = fmaf(w.y, vs[4 * o4 + 1][vcol<HD>(1, d)], acc);
+                        acc = fmaf(w.z, vs[4 * o4 + 2][vcol<HD>(2, d)], acc);
+                        acc = fmaf(w.w, vs[4 * o4 + 3][vcol<HD>(3, d)], acc);
                     }
                     ov[j] = acc;
                 }
@@ -2100,7 +2111,7 @@ __global__ __launch_bounds__(256, 2) void k_attn_flash(AttnArgs a) {
     constexpr int HALF = HD / 2, QM = 32, NTD = HD / 16;
     static_assert(P % 16 == 0 && 64 % P == 0, "blocks of whole 16-position MFMA tiles");
     __shared__ __align__(16) float ks[P][HD + 4];
-    __shared__ __align__(16) float vs[P][HD + 4];
+    __shared__ __align__(16) float vs[P][vstride(HD)];
     __shared__ __align__(16) float qs[64][HD + 4];
     __shared__ __align__(16) float pw[4][16][P + 4];
     __shared__ int lim[64];
@@ -2205,7 +2216,7 @@ __global__ __launch_bounds__(256, 2) void k_attn_flash(AttnArgs a) {
         for (int it = 0; it < VIT; it++) {
             const int i = tid + it * 256, o = i / (HD / 4), d = (i % (HD / 4)) * 4;
             const bool live = b0 + o < L;
-            *(float4*)&vs[o][d] = make_float4(live ? vv[it].x : 0.0f, live ? vv[it].y : 0.0f,
+            *(float4*)&vs[o][vcol<HD>(o, d)] = make_float4(live ? vv[it].x : 0.0f, live ? vv[it].y : 0.0f,
                                               live ? vv[it].z : 0.0f, live ? vv[it].w : 0.0f);
         }
         __syncthreads();
@@ -2217,7 +2228,7 @@ __global__ __launch_bounds__(256, 2) void k_attn_flash(AttnArgs a) {
                 const int p = n0 + i / HD, d = i % HD, o = p - b0;
                 const size_t at = (((size_t)(uint32_t)bt[p >> 4] * a.nkv + h) * 16 + (p & 15)) * HD + d;
                 a.kc[at] = ks[o][d];
-                a.vc[at] = vs[o][d];
+                a.vc[at] = vs[o][vcol<HD>(o, d)];
             }
         }
         // the wave's 16 x 64 scores (v_mfma_f32_16x16x4f32: A[i][k] in lane i + 16k,
@@ -2267,10 +2278,10 @@ __global__ __launch_bounds__(256, 2) void k_attn_flash(AttnArgs a) {
 #pragma unroll
         for (int j = 0; j < NTD; j++) {
             const float* pa = &pw[wave][c16][kk];
-            const float* vb = &vs[kk][j * 16 + c16];
+            const float* vb = &vs[kk][vcol<HD>(kk, j * 16 + c16)];  // rows kk + k0: k0 % 4 == 0
 #pragma unroll
             for (int k0 = 0; k0 < P; k0 += 4)
-                oc[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(pa[k0], vb[k0 * (HD + 4)], oc[j], 0, 0, 0);
+                oc[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(pa[k0], vb[k0 * vstride(HD)], oc[j], 0, 0, 0);
         }
     }
     // the partials of the item's two row halves
