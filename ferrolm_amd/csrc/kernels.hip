@@ -16,6 +16,7 @@
 //     EPI_ARGMAX    final rms_norm + lm_head + argmax         src/model.rs:338-361; src/sampler.rs:41-51
 //   k_attn          rope + KvCache::write + attend            src/model.rs:314-322,395-459; src/kv.rs:48-56;
 //                                                             src/kernels.rs:703-756
+//   k_attn_dec      the same, decode-sized items              src/model.rs:395-459; src/kernels.rs:703-756
 //   k_merge_pieces  the softmax normalisation of attend       src/kernels.rs:722-732
 //   k_accept        Engine::execute greedy accept             src/engine.rs:563-616
 #include "devutil.h"
@@ -2318,6 +2319,207 @@ __global__ __launch_bounds__(64) void k_merge_pieces(AttnArgs a, int m, void* __
     stamp.end();
 }
 
+// Decode attention for items of one span and at most QL <= 8 queries (the
+// rows of a decode or verify step x the GQA group), with the keys and values
+// used from the registers they are loaded into. KL = HD/8 lanes hold a key
+// (4 + 4 inputs of its rotation pairs each): they dot it with every query
+// (rotated queries read from LDS) and sum across their group. HD/4 lanes hold a
+// value row (4 dims each): each weighs its rows by the probabilities and the
+// partial sums meet across the wave's rows (lane swaps) and the four waves (LDS,
+// summed in wave order). Only the queries, the scores and the per-wave sums go
+// through LDS (12 KB at hd 64), so the launch is bound by registers, not LDS.
+// Same records, partials and cache writes as k_attn.
+template <int HD, int P, int QM, int QL, int MINW>
+__global__ __launch_bounds__(256, MINW) void k_attn_dec(AttnArgs a) {
+    constexpr int HALF = HD / 2;
+    constexpr int KL = HALF / 4, KIT = P * KL / 256;  // lanes per key, key passes
+    constexpr int VL = HD / 4, VIT = P * VL / 256;    // lanes per value row, value passes
+    static_assert(HD == 64 || HD == 128, "head_dim 64 or 128");
+    static_assert(KIT >= 1 && P * KL % 256 == 0 && VIT >= 1 && P * VL % 256 == 0, "whole passes of 256 lanes");
+    static_assert(QL <= 8 && QL <= QM, "decode-sized items");
+    __shared__ __align__(16) float qs[QL][HD];
+    __shared__ __align__(16) float pr[QL][P + 4];
+    __shared__ __align__(16) float ow[4][QL][HD];
+    __shared__ int lim[QL];
+    const Stamp stamp(a.stamp);
+    const int h = blockIdx.x, wi = blockIdx.y;
+    const int4* rec = (const int4*)(a.wrec + (size_t)wi * 16);
+    const int4 r0 = rec[0], r1 = rec[1], rb = rec[2], rb2 = rec[3];
+    const int row0 = r0.x, nrows = r0.y, crow0 = r0.z, cpos0 = r0.w;
+    const int p0 = r1.x, p1 = r1.y;
+    if (nrows == 0) return;  // an unused slot of the launch's capacity
+    const int G = a.nh / a.nkv, Q = nrows * G;
+    const int qd = a.nh * HD, kvd = a.nkv * HD;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    auto blk = [&](int j) -> size_t {
+        const int4 b = j < 4 ? rb : rb2;
+        const int jj = j & 3;
+        return (uint32_t)(jj == 0 ? b.x : jj == 1 ? b.y : jj == 2 ? b.z : b.w);
+    };
+    auto cache_at = [&](int p, int d) -> size_t { return ((blk((p - p0) >> 4) * a.nkv + h) * 16 + (p & 15)) * HD + d; };
+    auto src_of = [&](int p, int col) -> const float* {  // position p's key (col 0) or value (col kvd)
+        return p < cpos0 ? (col ? a.vc : a.kc) + cache_at(p, 0)
+                         : a.qkv + (size_t)(crow0 + p - cpos0) * a.ld + qd + col + h * HD;
+    };
+    const int pos_of_row0 = cpos0 + row0 - crow0;
+    // this group's new rows in the span (written to the cache by this item)
+    const int nr0 = max(max(p0, cpos0), pos_of_row0), nr1 = min(p1, pos_of_row0 + nrows);
+    for (int q = tid; q < Q; q += 256) lim[q] = pos_of_row0 + q / G;
+    // loads, none of them under a branch: q, the keys (with the cos/sin of new
+    // positions), the values; positions past the span read its last position
+    constexpr int QI = QL * (HALF / 4), QIT = (QI + 255) / 256;
+    const int qn = Q * (HALF / 4);
+    float4 qx1[QIT], qx2[QIT], qcs[QIT], qsn[QIT];
+#pragma unroll
+    for (int it = 0; it < QIT; it++) {
+        const int i = min(tid + it * 256, qn - 1);
+        const int q = i / (HALF / 4), d = (i % (HALF / 4)) * 4, r = q / G, j = q % G;
+        const float* src = a.qkv + (size_t)(row0 + r) * a.ld + (size_t)(h * G + j) * HD;
+        qx1[it] = *(const float4*)(src + d);
+        qx2[it] = *(const float4*)(src + d + HALF);
+        qcs[it] = *(const float4*)(a.cos_t + (size_t)(pos_of_row0 + r) * HALF + d);
+        qsn[it] = *(const float4*)(a.sin_t + (size_t)(pos_of_row0 + r) * HALF + d);
+    }
+    const int kd = (tid % KL) * 4, vd = (tid % VL) * 4;
+    float4 ku[KIT], kw[KIT], kcs[KIT], ksn[KIT], vv[VIT];
+#pragma unroll
+    for (int it = 0; it < KIT; it++) {
+        const int p = min(p0 + tid / KL + it * (256 / KL), p1 - 1);
+        const float* kp = src_of(p, 0);
+        ku[it] = ld_nt_f4(kp + kd);
+        kw[it] = ld_nt_f4(kp + kd + HALF);
+        const int pc = max(p, cpos0);  // cached keys are not rotated: one table row for all
+        kcs[it] = *(const float4*)(a.cos_t + (size_t)pc * HALF + kd);
+        ksn[it] = *(const float4*)(a.sin_t + (size_t)pc * HALF + kd);
+    }
+#pragma unroll
+    for (int it = 0; it < VIT; it++) {
+        const int p = min(p0 + tid / VL + it * (256 / VL), p1 - 1);
+        vv[it] = ld_nt_f4(src_of(p, kvd) + vd);
+    }
+    // q, rotated
+#pragma unroll
+    for (int it = 0; it < QIT; it++) {
+        const int i = tid + it * 256;
+        if (i < qn) {
+            const int q = i / (HALF / 4), d = (i % (HALF / 4)) * 4;
+            const float a1[4] = {qx1[it].x, qx1[it].y, qx1[it].z, qx1[it].w};
+            const float a2[4] = {qx2[it].x, qx2[it].y, qx2[it].z, qx2[it].w};
+            const float cc[4] = {qcs[it].x, qcs[it].y, qcs[it].z, qcs[it].w};
+            const float ss[4] = {qsn[it].x, qsn[it].y, qsn[it].z, qsn[it].w};
+            float4 o1, o2;
+            o1.x = __fadd_rn(__fmul_rn(a1[0], cc[0]), __fmul_rn(-a2[0], ss[0]));
+            o1.y = __fadd_rn(__fmul_rn(a1[1], cc[1]), __fmul_rn(-a2[1], ss[1]));
+            o1.z = __fadd_rn(__fmul_rn(a1[2], cc[2]), __fmul_rn(-a2[2], ss[2]));
+            o1.w = __fadd_rn(__fmul_rn(a1[3], cc[3]), __fmul_rn(-a2[3], ss[3]));
+            o2.x = __fadd_rn(__fmul_rn(a2[0], cc[0]), __fmul_rn(a1[0], ss[0]));
+            o2.y = __fadd_rn(__fmul_rn(a2[1], cc[1]), __fmul_rn(a1[1], ss[1]));
+            o2.z = __fadd_rn(__fmul_rn(a2[2], cc[2]), __fmul_rn(a1[2], ss[2]));
+            o2.w = __fadd_rn(__fmul_rn(a2[3], cc[3]), __fmul_rn(a1[3], ss[3]));
+            *(float4*)&qs[q][d] = o1;
+            *(float4*)&qs[q][d + HALF] = o2;
+        }
+    }
+    __syncthreads();
+    // scores: each key group dots its key with every query, sums across its KL
+    // lanes, and the group's first lane stores the scaled score (or -inf past
+    // the span or the query's own position)
+#pragma unroll
+    for (int it = 0; it < KIT; it++) {
+        const int o = tid / KL + it * (256 / KL), p = p0 + o;
+        const bool live = p < p1, rot = live && p >= cpos0;
+        const float a1[4] = {ku[it].x, ku[it].y, ku[it].z, ku[it].w};
+        const float a2[4] = {kw[it].x, kw[it].y, kw[it].z, kw[it].w};
+        const float cc[4] = {kcs[it].x, kcs[it].y, kcs[it].z, kcs[it].w};
+        const float ss[4] = {ksn[it].x, ksn[it].y, ksn[it].z, ksn[it].w};
+        float k1[4], k2[4];
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            k1[e] = rot ? __fadd_rn(__fmul_rn(a1[e], cc[e]), __fmul_rn(-a2[e], ss[e])) : a1[e];
+            k2[e] = rot ? __fadd_rn(__fmul_rn(a2[e], cc[e]), __fmul_rn(a1[e], ss[e])) : a2[e];
+        }
+        if (p >= nr0 && p < nr1) {
+            *(float4*)(a.kc + cache_at(p, kd)) = make_float4(k1[0], k1[1], k1[2], k1[3]);
+            *(float4*)(a.kc + cache_at(p, kd + HALF)) = make_float4(k2[0], k2[1], k2[2], k2[3]);
+        }
+#pragma unroll
+        for (int q = 0; q < QL; q++) {
+            const float4 x1 = *(const float4*)&qs[q][kd], x2 = *(const float4*)&qs[q][kd + HALF];
+            float s = 0.0f;
+            s = fmaf(x1.x, k1[0], s);
+            s = fmaf(x1.y, k1[1], s);
+            s = fmaf(x1.z, k1[2], s);
+            s = fmaf(x1.w, k1[3], s);
+            s = fmaf(x2.x, k2[0], s);
+            s = fmaf(x2.y, k2[1], s);
+            s = fmaf(x2.z, k2[2], s);
+            s = fmaf(x2.w, k2[3], s);
+            s = group_reduce<KL, false>(s);
+            if (tid % KL == 0 && q < Q) pr[q][o] = (live && p <= lim[q]) ? s * a.scale : -INFINITY;
+        }
+    }
+    __syncthreads();
+    // softmax statistics per query (one query per P lanes), exponentials in place
+    float* partq = a.part + ((size_t)wi * a.nkv + h) * QM * (HD + 4);
+#pragma unroll
+    for (int pass = 0; pass < (QL * P + 255) / 256; pass++) {
+        const int base = wave * 64 + pass * 256;
+        if (base >= Q * P) break;
+        const int i = base + lane, q = i / P, o = i % P;
+        const float sc = q < Q ? pr[q][o] : -INFINITY;
+        const float mx = group_reduce<P, true>(sc);
+        const float e = (sc == -INFINITY) ? 0.0f : dev_exp(sc - mx);
+        const float sum = group_reduce<P, false>(e);
+        if (q < Q) {
+            pr[q][o] = e;
+            if (o == 0) {
+                partq[q * (HD + 4)] = mx;
+                partq[q * (HD + 4) + 1] = sum;
+            }
+        }
+    }
+    __syncthreads();
+    // weighted values: this lane's value rows, then the wave's other rows of the
+    // same dims, then the four waves
+    float acc[QL][4];
+#pragma unroll
+    for (int q = 0; q < QL; q++) acc[q][0] = acc[q][1] = acc[q][2] = acc[q][3] = 0.0f;
+#pragma unroll
+    for (int it = 0; it < VIT; it++) {
+        const int o = tid / VL + it * (256 / VL), p = p0 + o;
+        if (p >= nr0 && p < nr1) *(float4*)(a.vc + cache_at(p, vd)) = vv[it];
+#pragma unroll
+        for (int q = 0; q < QL; q++) {
+            const float w = pr[q][o];  // 0 past the span and the query's position
+            acc[q][0] = fmaf(w, vv[it].x, acc[q][0]);
+            acc[q][1] = fmaf(w, vv[it].y, acc[q][1]);
+            acc[q][2] = fmaf(w, vv[it].z, acc[q][2]);
+            acc[q][3] = fmaf(w, vv[it].w, acc[q][3]);
+        }
+    }
+#pragma unroll
+    for (int q = 0; q < QL; q++) {
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            float v = acc[q][e];
+            if constexpr (VL == 16) {
+                v = reduce_rows<false, true>(v);  // lanes l, l^16, l^32, l^48
+            } else {
+                const auto hh = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+                v = __uint_as_float(hh[0]) + __uint_as_float(hh[1]);  // lanes l, l^32
+            }
+            acc[q][e] = v;
+        }
+        if (lane < VL) *(float4*)&ow[wave][q][vd] = make_float4(acc[q][0], acc[q][1], acc[q][2], acc[q][3]);
+    }
+    __syncthreads();
+    for (int i = tid; i < Q * HD; i += 256) {
+        const int q = i / HD, d = i % HD;
+        partq[q * (HD + 4) + 4 + d] = ((ow[0][q][d] + ow[1][q][d]) + ow[2][q][d]) + ow[3][q][d];
+    }
+    stamp.end();
+}
+
 template <int HD, int P, int QM, int QL, int MINW>
 static void attn_ns(hipStream_t st, const AttnArgs& a) {
     if (a.ns >= 4 && 4 * P <= 128)
@@ -2338,7 +2540,19 @@ static void attention_hd(hipStream_t st, const AttnArgs& a, int m, int ck, Piece
             goto merge;
         }
     }
-    // items of at most 8 or 24 queries hold fewer (three workgroups per CU)
+    // items of at most 8 or 24 queries hold fewer (three workgroups per CU);
+    // large launches of decode-sized items of one span at hd 64 and 128 keep
+    // their keys and values in registers (small ones: the general kernel's
+    // shorter chain of barriers finishes a lone item sooner)
+    if constexpr ((HD == 64 || HD == 128) && QM >= 8) {
+        if (a.ns == 1 && a.maxq > 0 && a.maxq <= 8 && (int64_t)a.nkv * a.n_wi >= kAttnDecWorkgroups) {
+            if (a.maxq <= 4)
+                hipLaunchKernelGGL((k_attn_dec<HD, P, QM, 4, 4>), dim3(a.nkv, a.n_wi), dim3(256), 0, st, a);
+            else
+                hipLaunchKernelGGL((k_attn_dec<HD, P, QM, 8, 4>), dim3(a.nkv, a.n_wi), dim3(256), 0, st, a);
+            goto merge;
+        }
+    }
     if (QM > 8 && a.maxq > 0 && a.maxq <= 8)
         attn_ns<HD, P, QM, 8, 3>(st, a);
     else if (QM > 24 && a.maxq > 0 && a.maxq <= 24)

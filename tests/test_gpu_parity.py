@@ -271,6 +271,56 @@ def test_split_bf16_attention_head_dim_128_matches_oracle(ctx):
         assert np.abs(gv - ov).max() <= 1e-4 * np.abs(ov).max()
 
 
+@pytest.mark.parametrize("hd,heads,kv_heads,rows", [(64, 8, 4, 1), (64, 16, 4, 2), (128, 8, 2, 1), (128, 16, 2, 1)])
+def test_register_decode_attention_matches_oracle(ctx, hd, heads, kv_heads, rows):
+    """The decode attention that keeps keys and values in registers
+    (k_attn_dec): launches of one-span items with at most 8 queries and at
+    least 1024 workgroups. Eight sequences of 2,090 to 2,160 positions over
+    shuffled tables give 33 to 34 spans of 64 positions each (hd 64; 1,056 to
+    1,088 workgroups over 4 kv heads, under the 4,096 from which hd 64 takes two
+    sub-spans) or 66 to 68 of 32 (hd 128, 2 kv heads); rows x the GQA group
+    makes 2, 8, 4 and 8 queries per item (the 4- and 8-query instances). One
+    forward of those rows, all logits and every layer's hidden state, against
+    the oracle from a copy of the device's cache (src/model.rs:395-432), and
+    the new rows' cache slots."""
+    from ferrolm_amd.synth import random_model
+    from ferrolm_amd.weights import Config
+    cfg = Config(vocab=512, hidden=heads * hd, intermediate=512, layers=2, heads=heads, kv_heads=kv_heads,
+                 head_dim=hd, rms_eps=1e-5, rope_theta=10000.0, max_position=4096)
+    hm = random_model(cfg, seed=31 + hd + heads, std=0.05)
+    rng = np.random.default_rng(32)
+    lens = [int(x) for x in rng.integers(2090, 2161, 8)]
+    per_seq = (max(lens) + rows) // 16 + 2
+    nb = per_seq * len(lens)
+    perm = [int(x) for x in rng.permutation(nb)]
+    tables = [perm[i * per_seq:(i + 1) * per_seq] for i in range(len(lens))]
+    prompts = [[int(x) for x in rng.integers(3, 500, n)] for n in lens]
+    gm = gpu.Model(ctx, hm)
+    kv = gpu.KvCache(ctx, cfg, nb)
+    for p, tb in zip(prompts, tables):
+        for a in range(0, len(p), 2048):
+            gpu.forward(ctx, gm, kv, [(p[a:a + 2048], a, tb, gpu.LOGITS_NONE)], logits=False)
+    om = oracle.Model(hm)
+    okv = om.kv(nb)
+    for i in range(cfg.layers):
+        okv.set_layer(i, *kv.layer(i))
+    chunks = [([int(x) for x in rng.integers(3, 500, rows)], n, tb, gpu.LOGITS_ALL) for n, tb in zip(lens, tables)]
+    out = gpu.forward(ctx, gm, kv, chunks, hidden=True)
+    ol, oh = om.forward(okv, chunks, hidden=True)
+    lrel = np.abs(out.logits - ol).max(axis=1) / np.abs(ol).max(axis=1)
+    hrel = np.linalg.norm(out.hidden - oh, axis=-1) / np.linalg.norm(oh, axis=-1)
+    print(f"register decode attention, hd {hd}, {heads}/{kv_heads} heads, {rows} rows: "
+          f"logits rel max {lrel.max():.2e}, hidden rel max {hrel.max():.2e}")
+    assert out.logits.shape == (8 * rows, cfg.vocab)
+    assert lrel.max() <= 1e-4 and hrel.max() <= 1e-4, (lrel.max(), hrel.max())
+    assert_argmax_parity(out.argmax, ol, tol=2e-3, max_ties=1)
+    for i in range(cfg.layers):  # the new rows' cache slots
+        gk, gv = kv.layer(i)
+        ok, ov = okv.layer(i)
+        assert np.abs(gk - ok).max() <= 1e-4 * np.abs(ok).max()
+        assert np.abs(gv - ov).max() <= 1e-4 * np.abs(ov).max()
+
+
 @pytest.mark.parametrize("n_seqs", [1, 2])
 def test_speculative_steps_head_dim_64_one_and_two_passes(ctx, n_seqs):
     """Head dim 64 (64-position spans, three query heads per kv head): one sequence
