@@ -495,10 +495,12 @@ static int build_plan(const fg_config& c, const fg_kv& kv, int max_pos, const Ch
     // 6105-6111 against 5867 us; 32-position spans instead: 6182 us. At 8
     // sequences (about 4,400 items) verify 2595-2599 against 2546-2549 us; the
     // 135M draft at 32 sequences (1,584 items) is slower with them (draft
-    // 5594-5601 against 5456-5458 us), so the bar sits between. cfg4's 1B draft
-    // (about 4,600 items of 4 queries): device time 1% more, but half the item
-    // records to pack and upload per round, step 15.8 -> 15.4 ms.
-    if (c.head_dim == 64 && w1 * c.kv_heads >= kTwoSubSpanItems) P.ns = 128 / span1;
+    // 5594-5601 against 5456-5458 us), so the bar sits between. Groups of at
+    // most 4 queries stay on one-span items, which large launches run with the
+    // keys and values in registers (k_attn_dec): cfg4's 1B draft (about 4,600
+    // items of 4 queries) 6358 -> 6152 us per step and 1079 -> 1094 tok/s, where
+    // cfg3's target (5 queries) went 5547-5607 -> 6101 us the same way.
+    if (c.head_dim == 64 && w1 * c.kv_heads >= kTwoSubSpanItems && maxq > 4) P.ns = 128 / span1;
     P.maxq = maxq;
     const int span = span1 * P.ns;
     // Long chunks at hd 64 and 128 take the flash items (rf rows each, split into
