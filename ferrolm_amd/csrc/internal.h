@@ -239,11 +239,11 @@ int attn_qmax(int hd);
 // several sub-spans when the launch is large (k_attn's NS): the loads of the
 // next sub-span then overlap MFMA work worth hiding them behind.
 constexpr int kAttnMfmaQueries = 16;
-// Workgroups (kv heads x work items) from which a launch of decode-sized items
-// (one span, at most 8 queries) takes k_attn_dec, the kernel that keeps keys
-// and values in registers (measured: the 135M draft at 32 sequences, 1,728
-// workgroups, draft 4886 -> 4795 us per step; the cfg2 draft's 51 workgroups
-// +12 us per step, its verify's 544 unchanged).
+// Workgroups (kv heads x work-item slots, empty slots included) from which a
+// launch of decode-sized items (one span, at most 8 queries) takes k_attn_dec,
+// the kernel that keeps keys and values in registers (measured: the 135M draft
+// at 32 sequences, 3 x 576 slots, draft 4886 -> 4795 us per step; the cfg2
+// draft's 3 x 32 +12 us per step; the cfg2 verify's 32 x 32 unchanged).
 constexpr int kAttnDecWorkgroups = 1024;
 // Positions per block of the flash attention items, and per part of an item.
 constexpr int kFlashBlock(int hd) { return hd >= 128 ? 32 : 64; }
