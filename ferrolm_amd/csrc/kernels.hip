@@ -2327,7 +2327,8 @@ __global__ __launch_bounds__(64) void k_merge_pieces(AttnArgs a, int m, void* __
 // value row (4 dims each): each weighs its rows by the probabilities and the
 // partial sums meet across the wave's rows (lane swaps) and the four waves (LDS,
 // summed in wave order). Only the queries, the scores and the per-wave sums go
-// through LDS (12 KB at hd 64), so the launch is bound by registers, not LDS.
+// through LDS (6 or 12 KB at hd 64 for 4 or 8 queries), so registers, not LDS,
+// bound the launch.
 // Same records, partials and cache writes as k_attn.
 template <int HD, int P, int QM, int QL, int MINW>
 __global__ __launch_bounds__(256, MINW) void k_attn_dec(AttnArgs a) {
