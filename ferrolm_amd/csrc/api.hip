@@ -636,7 +636,7 @@ struct Work {
     float* kpart;  // GEMM split-K partial tiles (steps of more than kGemvRows rows)
     size_t kpart_cap;
     float* gpart;  // GEMV split-K partial tiles (decode steps of one pass)
-    long long* acc;   // fused layers' accumulators (steps of one pass), [kAccCopies][4][hidden]:
+    long long* acc;   // fused layers' accumulators (steps of one pass), [copies][4][hidden]:
     long long* acc2;  // A (acc) the MLP's output, B (acc2) the output projection's
     void* pa[2];   // activation pieces, ping-pong: each kernel reads one and writes the other
     float* pxs[2];
@@ -765,7 +765,7 @@ static size_t layout_work(const fg_model* m, const Plan& P, Work& w, void* base)
     // GEMV split K: [group][split][16 rows][group columns] over the hidden columns
     w.gpart = w.passes == 1 ? cv.take<float>((size_t)kGemvSplitMax * 16 * H) : nullptr;
     w.acc = w.passes == 1 ? cv.take<long long>((size_t)kAccCopies * 4 * H) : nullptr;
-    w.acc2 = w.passes == 1 ? cv.take<long long>((size_t)kAccCopies * 4 * H) : nullptr;
+    w.acc2 = w.passes == 1 ? cv.take<long long>((size_t)kAccCopiesB * 4 * H) : nullptr;
     w.x2 = w.passes == 1 ? cv.take<float>((size_t)4 * H) : nullptr;
     return cv.off + 256;
 }
@@ -893,7 +893,7 @@ static int run_forward(fg_ctx* ctx, const fg_model* m, fg_kv* kv, const Plan& P,
         }
         if (fuse_l) {
             g.zero = w.acc2;
-            g.zero_n = acc_n;
+            g.zero_n = kAccCopiesB * 4 * H;
         }
         gemv(ctx, EPI_QKV, l.wqkv, g);
         // attention (RoPE, cache write) and the merge into wo's pieces

@@ -90,8 +90,15 @@ enum Epi {
 // Fewer copies mean fewer bytes for the consumer, more for the atomics to
 // contend on. Measured on the 135M draft (cfg2, one box): 8 copies
 // 2119-2123 us of draft per step, 4: 2089-2091, 2: 2111-2113, 1: 2193-2195.
+// The output projection by head (k_o_heads) adds into the other accumulator,
+// which the MLP reads: there each output gets one add per head (9 for the
+// 135M draft) against one per MLP workgroup (96), so one copy suffices and the
+// MLP's 96 workgroups read a quarter of the bytes (kAccCopiesB; with the MLP's
+// accumulator at 4: draft 1861 -> 1843 us per step, 2 copies 1854; the MLP's at
+// 2 copies 1865, at 8 1841).
 // Layout [copy][row (4)][acc_ld]. Range: |y| < 2^26.
 constexpr int kAccCopies = 4;
+constexpr int kAccCopiesB = 1;
 constexpr int kAccFrac = 36;
 
 struct GemvArgs {
@@ -146,7 +153,8 @@ struct GemvArgs {
     const float* apart = nullptr;
     const int32_t* amrec = nullptr;
     int anh = 0, ankv = 0, ahd = 0, aqm = 0;
-    // Fixed-point accumulators (kAccCopies copies of [4][acc_ld]) of a fused layer:
+    // Fixed-point accumulators ([copy][4][acc_ld]: kAccCopies copies of the MLP's,
+    // kAccCopiesB of the output projection's) of a fused layer:
     // with ax (EPI_QKV, EPI_MLP) the input rows are x + the sum of acc's copies,
     // normed here (g_in, hidden, eps) into the operand, and stored to x_alt (not
     // to x, which the launch's other workgroups are still reading); EPI_MLP adds

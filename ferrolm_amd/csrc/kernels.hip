@@ -666,14 +666,15 @@ __global__ __launch_bounds__(64 * WMAX) void k_gemv(const GemvArgs a) {
                 float v0 = 0.0f, v1 = 0.0f;
                 if (k < H) {  // (H is even)
                     const float2 xv = *(const float2*)(a.x + (size_t)r * a.ldx + k);
-                    i64x2 cv[kAccCopies];
+                    constexpr int NCP = EPI == EPI_MLP ? kAccCopiesB : kAccCopies;  // the MLP reads k_o_heads' sums
+                    i64x2 cv[NCP];
 #pragma unroll
-                    for (int c = 0; c < kAccCopies; c++)
+                    for (int c = 0; c < NCP; c++)
                         cv[c] = *(const i64x2*)(a.acc + ((size_t)c * 4 + r) * a.acc_ld + k);
                     const float2 gv = *(const float2*)(a.g_in + k);
                     long long s0 = 0, s1 = 0;
 #pragma unroll
-                    for (int c = 0; c < kAccCopies; c++) {
+                    for (int c = 0; c < NCP; c++) {
                         s0 += cv[c][0];
                         s1 += cv[c][1];
                     }
@@ -2640,7 +2641,7 @@ int launch_cap_merge(hipStream_t st, const AttnArgs& a, int m, float* out, int l
 // pieces of 8 merged values), multiplies them by the HD columns of W_o that
 // belong to head h (HD / 32 k-blocks of its n-tile, bf16 MFMA), and adds the
 // 16 outputs of each row into the accumulator a.acc_out (copy = workgroup %
-// kAccCopies) as round(y * 2^kAccFrac). A workgroup reads one head's partials
+// kAccCopiesB) as round(y * 2^kAccFrac). A workgroup reads one head's partials
 // (about 4.6 KB per row for the 135M draft) instead of every head's, which is
 // what an output projection that merges for itself must read per workgroup;
 // a CU streams only about 27 GB/s, so that read was most of its time. The
@@ -2703,7 +2704,7 @@ __global__ __launch_bounds__(2 * HD) void k_o_heads(const GemvArgs a) {
         if (r < a.m && n < a.N) {
             const float y = ((acc[0] + acc[1]) + acc[2]) + acc[3];
             const double d = fmin(fmax((double)y * (double)(1ll << kAccFrac), -4.0e18), 4.0e18);
-            __hip_atomic_fetch_add(a.acc_out + ((size_t)(wg % kAccCopies) * 4 + r) * a.acc_ld + n, (long long)rint(d),
+            __hip_atomic_fetch_add(a.acc_out + ((size_t)(wg % kAccCopiesB) * 4 + r) * a.acc_ld + n, (long long)rint(d),
                                    __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
     }
