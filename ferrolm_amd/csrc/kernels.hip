@@ -2304,13 +2304,14 @@ __global__ __launch_bounds__(256, 2) void k_attn_flash(AttnArgs a) {
 }
 
 // Merge of the spans of each (row, head) into the attention output, written
-// as the output projection's pieces. One wave per (k-block, pass); the four
-// lanes of a (row, 8 dims) pair (one per piece) share the spans.
-template <int HD, int QM, int CK>
-__global__ __launch_bounds__(64) void k_merge_pieces(AttnArgs a, int m, void* __restrict__ out, float* __restrict__ xs,
-                                                     int passes) {
+// as the output projection's pieces. One wave per (k-block, pass), KBW waves
+// (consecutive k-blocks) per workgroup; the four lanes of a (row, 8 dims) pair
+// (one per piece) share the spans.
+template <int HD, int QM, int CK, int KBW = 1>
+__global__ __launch_bounds__(64 * KBW) void k_merge_pieces(AttnArgs a, int m, void* __restrict__ out,
+                                                           float* __restrict__ xs, int passes) {
     const Stamp stamp(a.stamp);
-    const int kb = blockIdx.x, pass = blockIdx.y, lane = threadIdx.x;
+    const int kb = blockIdx.x * KBW + (int)(threadIdx.x >> 6), pass = blockIdx.y, lane = threadIdx.x & 63;
     const int c = lane & 15, row = pass * 4 + (c >> 2), piece = c & 3;
     const int k0 = kb * 32 + (lane >> 4) * 8;
     float v[8] = {0, 0, 0, 0, 0, 0, 0, 0};
@@ -2568,6 +2569,12 @@ merge:
     if (ck == BF16)
         hipLaunchKernelGGL((k_merge_pieces<HD, QM, BF16>), dim3(out.kb, out.passes), dim3(64), 0, st, am, m, out.a,
                            out.xs, out.passes);
+    // GEMM consumers of 1024 or more (k-block, pass) waves: four consecutive k-blocks
+    // per workgroup (cfg4 at 16 sequences, 2,560 waves: verify 8185-8197 -> 8096-8099
+    // us per step; eight per workgroup 8094 against 8043-8046 us on another box)
+    else if (ck == MM && out.kb % 4 == 0 && out.kb * out.passes >= 1024)
+        hipLaunchKernelGGL((k_merge_pieces<HD, QM, MM, 4>), dim3(out.kb / 4, out.passes), dim3(256), 0, st, am, m,
+                           out.a, out.xs, out.passes);
     else if (ck == MM)
         hipLaunchKernelGGL((k_merge_pieces<HD, QM, MM>), dim3(out.kb, out.passes), dim3(64), 0, st, am, m, out.a,
                            out.xs, out.passes);
