@@ -49,9 +49,9 @@ HBM_PEAK_GBS = 8000.0
 # L2-to-memory bytes per launch of the target int4 decode GEMVs (class mean), counted by
 # request size with rocprofv3 --pmc (TCC_EA0_RDREQ_{32,64,128}B, TCC_EA0_WRREQ_64B; a
 # plain copy of known size reads back exactly); profiles/gemv_int4_cfg2_pmc.md has the
-# commands and the per-GEMV figures, taken at commit 831f852 (kernels as of be9ad0e). A
-# measurement of the current kernels, re-taken whenever they change.
-MEASURED_TRAFFIC = {"int4": 11_385_072}
+# commands and the per-GEMV figures, taken at commit 5450b44. A measurement of the
+# current kernels, re-taken whenever they change.
+MEASURED_TRAFFIC = {"int4": 11_382_519}
 
 
 def log(msg: str) -> None:
